@@ -1,0 +1,332 @@
+// BN254 base field Fq and scalar field Fr for gfx950.
+//
+// Representation (device and host-math builds alike)
+// ---------------------------------------------------
+// An element is 9 limbs of 29 bits (uint32 each, limb < 2^29), little endian,
+// holding a value in the lazy range [0, 2m) for modulus m.  The Montgomery
+// radix inside kernels is R' = 2^261 (= 2^(29*9)), not the reference's 2^256:
+// with 29-bit limbs every limb product is one v_mad_u64_u32 into a 64-bit
+// column accumulator and no carry has to be propagated until the column is
+// finished (18 products of < 2^60 plus a 2^35 carry stay below 2^64).  On
+// gfx950 the 32x32->64 mad issues at full rate, so the instruction count of
+// the multiply is what matters; this layout needs 162 mads and ~45 other ops
+// against ~560 instructions for a compiler-lowered 8x32-bit CIOS.
+//
+// At the memory boundary elements are the reference's 32-byte little-endian
+// form (4 x u64 = 8 x u32 words), Montgomery form with R = 2^256
+// (reference: src/field/montgomery.cuh:33-60, src/field/fp.cuh:322-349).
+// from_mont256/to_mont256 convert between the two radices with one multiply
+// by a constant (2^266 mod m in, 2^256 mod m out).  For maps that are linear
+// over the field (NTT, scaling by a constant prepared in the internal radix)
+// the radix cancels and a plain limb repack suffices (repack_in/repack_out).
+#pragma once
+#include <stdint.h>
+
+#if defined(__HIPCC__)
+#include <hip/hip_runtime.h>
+#define ZK_HD __host__ __device__ __forceinline__
+#else
+#define ZK_HD static inline
+#endif
+
+namespace zk {
+
+constexpr int NL = 9;
+constexpr uint32_t LMASK = (1u << 29) - 1u;
+
+// BN254 base field q = 0x30644e72e131a029b85045b68181585d97816a916871ca8d3c208c16d87cfd47
+// (reference src/field/montgomery.cuh:33-38).
+struct FqP {
+  static constexpr uint32_t MOD[9] = {0x187cfd47u, 0x010460b6u, 0x1c72a34fu, 0x02d522d0u, 0x1585d978u,
+                                      0x02db40c0u, 0x00a6e141u, 0x0e5c2634u, 0x0030644eu};
+  static constexpr uint32_t MOD2[9] = {0x10f9fa8eu, 0x0208c16du, 0x18e5469eu, 0x05aa45a1u, 0x0b0bb2f0u,
+                                       0x05b68181u, 0x014dc282u, 0x1cb84c68u, 0x0060c89cu};
+  static constexpr uint32_t INV = 0x04866389u;  // -q^-1 mod 2^29
+  static constexpr uint32_t ONE[9] = {0x157ccc21u, 0x141c2758u, 0x185230d3u, 0x014c0419u, 0x0aa36fb9u,
+                                      0x1d4240ceu, 0x11d54c07u, 0x052ac7a8u, 0x000dc836u};  // 2^261 mod q
+  static constexpr uint32_t R2[9] = {0x059bac10u, 0x0d1503a3u, 0x018016b8u, 0x10ab0ca8u, 0x02632639u,
+                                     0x02c0169fu, 0x169bfd53u, 0x11869d4cu, 0x002a11a6u};  // 2^522 mod q
+  static constexpr uint32_t K_IN[9] = {0x13349ca1u, 0x1a5d84a8u, 0x0a3e5cacu, 0x100249e0u, 0x12b951e8u,
+                                       0x0e92d304u, 0x14cb95b3u, 0x041b9d3du, 0x00058003u};  // 2^266 mod q
+  static constexpr uint32_t K_OUT[9] = {0x058f0d9du, 0x1aea1c6eu, 0x11c2cf74u, 0x11d651ebu, 0x1462c0a7u,
+                                        0x11b7bc3cu, 0x1cbd99bau, 0x183340fbu, 0x000e0a77u};  // 2^256 mod q
+};
+
+// BN254 scalar field r = 0x30644e72e131a029b85045b68181585d2833e84879b9709143e1f593f0000001
+// (reference src/field/fp.cuh:329-335).
+struct FrP {
+  static constexpr uint32_t MOD[9] = {0x10000001u, 0x1f0fac9fu, 0x0e5c2450u, 0x07d090f3u, 0x1585d283u,
+                                      0x02db40c0u, 0x00a6e141u, 0x0e5c2634u, 0x0030644eu};
+  static constexpr uint32_t MOD2[9] = {0x00000002u, 0x1e1f593fu, 0x1cb848a1u, 0x0fa121e6u, 0x0b0ba506u,
+                                       0x05b68181u, 0x014dc282u, 0x1cb84c68u, 0x0060c89cu};
+  static constexpr uint32_t INV = 0x0fffffffu;  // -r^-1 mod 2^29
+  static constexpr uint32_t ONE[9] = {0x0fffff57u, 0x1ea70ab4u, 0x052c068bu, 0x17504f49u, 0x0aa8075bu,
+                                      0x1d4240ceu, 0x11d54c07u, 0x052ac7a8u, 0x000dc836u};  // 2^261 mod r
+  static constexpr uint32_t R2[9] = {0x05b69bd4u, 0x06170a5au, 0x020cddceu, 0x1db6310bu, 0x0e54d0ffu,
+                                     0x1cf855e3u, 0x1c15e103u, 0x07d09161u, 0x000a054au};  // 2^522 mod r
+  static constexpr uint32_t K_IN[9] = {0x0fffead7u, 0x1d5444f4u, 0x04438aa5u, 0x03b4d096u, 0x134c84dau,
+                                       0x0e92d304u, 0x14cb95b3u, 0x041b9d3du, 0x00058003u};  // 2^266 mod r
+  static constexpr uint32_t K_OUT[9] = {0x0ffffffbu, 0x04b1a0e2u, 0x18334a6bu, 0x18ed2b3eu, 0x1462e36fu,
+                                        0x11b7bc3cu, 0x1cbd99bau, 0x183340fbu, 0x000e0a77u};  // 2^256 mod r
+};
+
+template <class P>
+struct fe {
+  uint32_t l[NL];
+};
+
+using fq = fe<FqP>;
+using fr = fe<FrP>;
+
+template <class P>
+ZK_HD fe<P> fe_zero() {
+  fe<P> r;
+#pragma unroll
+  for (int i = 0; i < NL; i++) r.l[i] = 0;
+  return r;
+}
+
+template <class P>
+ZK_HD fe<P> fe_const(const uint32_t (&c)[NL]) {
+  fe<P> r;
+#pragma unroll
+  for (int i = 0; i < NL; i++) r.l[i] = c[i];
+  return r;
+}
+
+template <class P>
+ZK_HD fe<P> fe_one() {
+  return fe_const<P>(P::ONE);
+}
+
+// Montgomery product a*b*2^-261 mod m, column (product-scanning) order with the
+// reduction interleaved per column.  Inputs: limbs < 2^30, values < 8m.
+// Output: limbs < 2^29, value < 2m.
+template <class P>
+ZK_HD fe<P> fmul(const fe<P>& a, const fe<P>& b) {
+  uint32_t q[NL];
+  fe<P> r;
+  uint64_t acc = 0;
+#pragma unroll
+  for (int k = 0; k < 2 * NL - 1; k++) {
+#pragma unroll
+    for (int i = 0; i < NL; i++) {
+      const int j = k - i;
+      if (j >= 0 && j < NL) acc += (uint64_t)a.l[i] * b.l[j];
+    }
+#pragma unroll
+    for (int i = 0; i < NL; i++) {
+      const int j = k - i;
+      if (i < k && j >= 1 && j < NL) acc += (uint64_t)q[i] * P::MOD[j];
+    }
+    if (k < NL) {
+      q[k] = ((uint32_t)acc * P::INV) & LMASK;
+      acc += (uint64_t)q[k] * P::MOD[0];
+    } else {
+      r.l[k - NL] = (uint32_t)acc & LMASK;
+    }
+    acc >>= 29;
+  }
+  r.l[NL - 1] = (uint32_t)acc;
+  return r;
+}
+
+// Squaring: cross products are summed once and doubled per column.
+template <class P>
+ZK_HD fe<P> fsqr(const fe<P>& a) {
+  uint32_t q[NL];
+  fe<P> r;
+  uint64_t acc = 0;
+#pragma unroll
+  for (int k = 0; k < 2 * NL - 1; k++) {
+    uint64_t cross = 0;
+#pragma unroll
+    for (int i = 0; i < NL; i++) {
+      const int j = k - i;
+      if (j > i && j < NL) cross += (uint64_t)a.l[i] * a.l[j];
+    }
+    acc += cross << 1;
+    if ((k & 1) == 0 && k / 2 < NL) acc += (uint64_t)a.l[k / 2] * a.l[k / 2];
+#pragma unroll
+    for (int i = 0; i < NL; i++) {
+      const int j = k - i;
+      if (i < k && j >= 1 && j < NL) acc += (uint64_t)q[i] * P::MOD[j];
+    }
+    if (k < NL) {
+      q[k] = ((uint32_t)acc * P::INV) & LMASK;
+      acc += (uint64_t)q[k] * P::MOD[0];
+    } else {
+      r.l[k - NL] = (uint32_t)acc & LMASK;
+    }
+    acc >>= 29;
+  }
+  r.l[NL - 1] = (uint32_t)acc;
+  return r;
+}
+
+// (a + b) mod m into [0, 2m).  Inputs normalized, values < 2m.
+template <class P>
+ZK_HD fe<P> fadd(const fe<P>& a, const fe<P>& b) {
+  fe<P> s, t;
+  uint32_t c = 0;
+#pragma unroll
+  for (int i = 0; i < NL; i++) {
+    uint32_t v = a.l[i] + b.l[i] + c;
+    c = v >> 29;
+    s.l[i] = v & LMASK;
+  }
+  int32_t br = 0;
+#pragma unroll
+  for (int i = 0; i < NL; i++) {
+    int32_t v = (int32_t)s.l[i] - (int32_t)P::MOD2[i] + br;
+    br = v >> 29;
+    t.l[i] = (uint32_t)v & LMASK;
+  }
+  // br == -1: s < 2m, keep s.
+#pragma unroll
+  for (int i = 0; i < NL; i++) s.l[i] = br ? s.l[i] : t.l[i];
+  return s;
+}
+
+// (a - b) mod m into [0, 2m).  Inputs normalized, values < 2m.
+template <class P>
+ZK_HD fe<P> fsub(const fe<P>& a, const fe<P>& b) {
+  fe<P> d;
+  int32_t br = 0;
+#pragma unroll
+  for (int i = 0; i < NL; i++) {
+    int32_t v = (int32_t)a.l[i] - (int32_t)b.l[i] + br;
+    br = v >> 29;
+    d.l[i] = (uint32_t)v & LMASK;
+  }
+  const uint32_t mask = (uint32_t)br;  // all ones when a < b
+  uint32_t c = 0;
+#pragma unroll
+  for (int i = 0; i < NL; i++) {
+    uint32_t v = d.l[i] + (P::MOD2[i] & mask) + c;
+    c = v >> 29;
+    d.l[i] = v & LMASK;
+  }
+  return d;
+}
+
+template <class P>
+ZK_HD fe<P> fneg(const fe<P>& a) {
+  return fsub(fe_zero<P>(), a);
+}
+
+template <class P>
+ZK_HD fe<P> fdbl(const fe<P>& a) {
+  return fadd(a, a);
+}
+
+// Limb-wise sum without normalization: limbs < 2^30, value < 4m.  Valid only
+// as a direct input of fmul/fsqr.
+template <class P>
+ZK_HD fe<P> fadd_lazy(const fe<P>& a, const fe<P>& b) {
+  fe<P> s;
+#pragma unroll
+  for (int i = 0; i < NL; i++) s.l[i] = a.l[i] + b.l[i];
+  return s;
+}
+
+// Reduce [0, 2m) to the canonical [0, m).
+template <class P>
+ZK_HD fe<P> fcanon(const fe<P>& a) {
+  fe<P> t;
+  int32_t br = 0;
+#pragma unroll
+  for (int i = 0; i < NL; i++) {
+    int32_t v = (int32_t)a.l[i] - (int32_t)P::MOD[i] + br;
+    br = v >> 29;
+    t.l[i] = (uint32_t)v & LMASK;
+  }
+  fe<P> r;
+#pragma unroll
+  for (int i = 0; i < NL; i++) r.l[i] = br ? a.l[i] : t.l[i];
+  return r;
+}
+
+template <class P>
+ZK_HD bool fis_zero(const fe<P>& a) {
+  fe<P> c = fcanon(a);
+  uint32_t o = 0;
+#pragma unroll
+  for (int i = 0; i < NL; i++) o |= c.l[i];
+  return o == 0;
+}
+
+template <class P>
+ZK_HD bool feq(const fe<P>& a, const fe<P>& b) {
+  return fis_zero(fsub(a, b));
+}
+
+// Bit repack of a 256-bit little-endian word array into 29-bit limbs (no change
+// of value).
+template <class P>
+ZK_HD fe<P> repack_in(const uint32_t w[8]) {
+  fe<P> r;
+#pragma unroll
+  for (int i = 0; i < NL; i++) {
+    const int bit = 29 * i;
+    const int wd = bit >> 5;
+    const int sh = bit & 31;
+    uint64_t v = w[wd];
+    if (wd + 1 < 8) v |= (uint64_t)w[wd + 1] << 32;
+    r.l[i] = (uint32_t)(v >> sh) & LMASK;
+  }
+  return r;
+}
+
+// Canonicalize and repack into 8 little-endian 32-bit words.
+template <class P>
+ZK_HD void repack_out(const fe<P>& a, uint32_t w[8]) {
+  fe<P> c = fcanon(a);
+#pragma unroll
+  for (int j = 0; j < 8; j++) {
+    const int bit = 32 * j;
+    const int i = bit / 29;
+    const int sh = bit % 29;
+    uint64_t v = c.l[i];
+    if (i + 1 < NL) v |= (uint64_t)c.l[i + 1] << 29;
+    if (i + 2 < NL && sh > 26) v |= (uint64_t)c.l[i + 2] << 58;
+    w[j] = (uint32_t)(v >> sh);
+  }
+}
+
+// Reference Montgomery form (R = 2^256) <-> internal form (R' = 2^261).
+template <class P>
+ZK_HD fe<P> from_mont256(const uint32_t w[8]) {
+  return fmul(repack_in<P>(w), fe_const<P>(P::K_IN));
+}
+
+template <class P>
+ZK_HD void to_mont256(const fe<P>& a, uint32_t w[8]) {
+  repack_out(fmul(a, fe_const<P>(P::K_OUT)), w);
+}
+
+// Plain integer (standard form) <-> internal form.
+template <class P>
+ZK_HD fe<P> from_std(const uint32_t w[8]) {
+  return fmul(repack_in<P>(w), fe_const<P>(P::R2));
+}
+
+template <class P>
+ZK_HD void to_std(const fe<P>& a, uint32_t w[8]) {
+  fe<P> one_plain = fe_zero<P>();
+  one_plain.l[0] = 1;
+  repack_out(fmul(a, one_plain), w);
+}
+
+// Square-and-multiply with a 256-bit plain exponent (little-endian words).
+template <class P>
+ZK_HD fe<P> fpow(const fe<P>& a, const uint32_t e[8]) {
+  fe<P> r = fe_one<P>();
+  for (int bit = 255; bit >= 0; bit--) {
+    r = fsqr(r);
+    if ((e[bit >> 5] >> (bit & 31)) & 1u) r = fmul(r, a);
+  }
+  return r;
+}
+
+}  // namespace zk

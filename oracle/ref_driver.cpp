@@ -1,0 +1,138 @@
+// TEST INFRASTRUCTURE ONLY -- thin C wrapper over the reference's own host
+// code, compiled in place from /root/reference/src with the reference's own
+// no-CUDA shim (tests/host/shim/cuda_runtime.h), into oracle/_ref/.  Nothing
+// here is copied from the reference: it includes the reference headers and
+// calls them.  Used by tests as a second, independent checker:
+//   * the reference verifier (pairing check, src/curve/pairing.cuh:278-282,
+//     with vk_x assembled as in src/prover/groth16.cu:967-1003) on artefact
+//     files read by the reference's loaders (src/verifier/verifier.cu),
+//   * the reference field and curve arithmetic (fp.cuh, fp2.cuh, g1.cuh,
+//     g2.cuh -- G2 through its affine-inversion formulas).
+#include <cstdint>
+#include <cstring>
+#include <vector>
+
+#include "curve/pairing.cuh"
+#include "prover/circuit.cuh"
+#include "verifier/verifier.cuh"
+
+using namespace bn254;
+
+static G1Affine in_g1(const uint64_t* o) {
+  Fp x(o[0], o[1], o[2], o[3]), y(o[4], o[5], o[6], o[7]);
+  if (x.is_zero() && y.is_zero()) return G1Affine();
+  return G1Affine(x, y);
+}
+static void out_g1(const G1Affine& p, uint64_t* o) {
+  if (p.infinity) {
+    memset(o, 0, 64);
+    return;
+  }
+  memcpy(o, p.x.val, 32);
+  memcpy(o + 4, p.y.val, 32);
+}
+static G2Affine in_g2(const uint64_t* o) {
+  Fp2 x(Fp(o[0], o[1], o[2], o[3]), Fp(o[4], o[5], o[6], o[7]));
+  Fp2 y(Fp(o[8], o[9], o[10], o[11]), Fp(o[12], o[13], o[14], o[15]));
+  if (x.is_zero() && y.is_zero()) return G2Affine();
+  return G2Affine(x, y);
+}
+static void out_g2(const G2Affine& p, uint64_t* o) {
+  if (p.infinity) {
+    memset(o, 0, 128);
+    return;
+  }
+  memcpy(o, p.x.c0.val, 32);
+  memcpy(o + 4, p.x.c1.val, 32);
+  memcpy(o + 8, p.y.c0.val, 32);
+  memcpy(o + 12, p.y.c1.val, 32);
+}
+
+extern "C" {
+
+int ref_abi_version() { return 1; }
+
+void ref_fr_mul(const uint64_t* a, const uint64_t* b, uint64_t* o) { Fr::mont_mul_fr(o, a, b); }
+void ref_fq_mul(const uint64_t* a, const uint64_t* b, uint64_t* o) { host_montgomery_mul(o, a, b); }
+void ref_fr_inv(const uint64_t* a, uint64_t* o) {
+  Fr r = Fr(a[0], a[1], a[2], a[3]).inv();
+  memcpy(o, r.val, 32);
+}
+void ref_fq_from_std(const uint64_t* s, uint64_t* o) {
+  Fp r = Fp::from_standard(s[0], s[1], s[2], s[3]);
+  memcpy(o, r.val, 32);
+}
+
+void ref_g1_generator(uint64_t* o) { out_g1(G1Affine::generator(), o); }
+void ref_g2_generator(uint64_t* o) { out_g2(G2Affine::generator(), o); }
+
+void ref_g1_mul(const uint64_t* pt, const uint64_t* k, uint64_t* o) {
+  Fr s(k[0], k[1], k[2], k[3]);
+  out_g1(G1Jacobian::from_affine(in_g1(pt)).scalar_mul(s).to_affine(), o);
+}
+void ref_g2_mul(const uint64_t* pt, const uint64_t* k, uint64_t* o) {
+  Fr s(k[0], k[1], k[2], k[3]);
+  out_g2(G2Jacobian::from_affine(in_g2(pt)).scalar_mul(s).to_affine(), o);
+}
+void ref_g1_add(const uint64_t* a, const uint64_t* b, uint64_t* o) {
+  out_g1((G1Jacobian::from_affine(in_g1(a)) + G1Jacobian::from_affine(in_g1(b))).to_affine(), o);
+}
+void ref_g2_add(const uint64_t* a, const uint64_t* b, uint64_t* o) {
+  out_g2((G2Jacobian::from_affine(in_g2(a)) + G2Jacobian::from_affine(in_g2(b))).to_affine(), o);
+}
+
+// Sum of s_i * P_i by per-point double-and-add: the path the reference's
+// msm_g1 takes for n <= 256 (src/msm/msm.cu:330-339, tests/test_msm.cu:20-28).
+void ref_msm_g1_small(const uint64_t* pts, const uint64_t* sc, size_t n, uint64_t* o) {
+  G1Jacobian acc = G1Jacobian::identity();
+  for (size_t i = 0; i < n; i++) {
+    Fr s(sc[4 * i], sc[4 * i + 1], sc[4 * i + 2], sc[4 * i + 3]);
+    acc = acc + G1Jacobian::from_affine(in_g1(pts + 8 * i)).scalar_mul(s);
+  }
+  out_g1(acc.to_affine(), o);
+}
+void ref_msm_g2_small(const uint64_t* pts, const uint64_t* sc, size_t n, uint64_t* o) {
+  G2Jacobian acc = G2Jacobian::identity();
+  for (size_t i = 0; i < n; i++) {
+    Fr s(sc[4 * i], sc[4 * i + 1], sc[4 * i + 2], sc[4 * i + 3]);
+    acc = acc + G2Jacobian::from_affine(in_g2(pts + 16 * i)).scalar_mul(s);
+  }
+  out_g2(acc.to_affine(), o);
+}
+
+// Groth16 verification of artefact files with the reference's loaders and
+// pairing.  Returns 1 valid, 0 invalid, -1 on a load error.
+int ref_verify_files(const char* vk_path, const char* proof_path, const char* pub_path) {
+  zkml::VerificationKey vk = zkml::load_vk(vk_path);
+  if (vk.ic.empty()) return -1;
+  zkml::Groth16Proof proof = zkml::load_proof(proof_path);
+  if (!proof.valid) return -1;
+  std::vector<Fr> pub = zkml::load_public_inputs(pub_path);
+  if ((int)pub.size() != vk.num_public) return 0;
+  G1Jacobian vk_x = G1Jacobian::from_affine(vk.ic[0]);
+  for (int i = 0; i < (int)pub.size(); i++)
+    if (i + 1 < (int)vk.ic.size()) vk_x = vk_x + G1Jacobian::from_affine(vk.ic[i + 1]).scalar_mul(pub[i]);
+  G1Affine negA(proof.A.x, -proof.A.y);
+  G1Affine P[4] = {negA, vk.alpha_g1, vk_x.to_affine(), proof.C};
+  G2Affine Q[4] = {proof.B, vk.beta_g2, vk.gamma_g2, vk.delta_g2};
+  return verify_pairing_product(P, Q, 4) ? 1 : 0;
+}
+
+// R1CS satisfaction with the reference's own checker (src/prover/circuit.cuh:93-124).
+int ref_verify_witness(int nc, int nv, const int32_t* rows, const int32_t* cols, const uint64_t* vals,
+                       const size_t* counts, const uint64_t* w) {
+  zkml::R1CS c;
+  c.num_constraints = nc;
+  c.num_variables = nv;
+  size_t off = 0;
+  for (int which = 0; which < 3; which++) {
+    std::vector<zkml::SparseEntry>& v = which == 0 ? c.A : (which == 1 ? c.B : c.C);
+    for (size_t i = 0; i < counts[which]; i++, off++)
+      v.push_back({rows[off], cols[off], Fr(vals[4 * off], vals[4 * off + 1], vals[4 * off + 2], vals[4 * off + 3])});
+  }
+  std::vector<Fr> wv(nv);
+  for (int i = 0; i < nv; i++) wv[i] = Fr(w[4 * i], w[4 * i + 1], w[4 * i + 2], w[4 * i + 3]);
+  return c.verify_witness(wv) ? 1 : 0;
+}
+
+}  // extern "C"
