@@ -1,0 +1,117 @@
+// Internal declarations shared by the HIP translation units of libzkml_gpu.
+#pragma once
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+#include <stdio.h>
+
+#include <map>
+#include <memory>
+#include <mutex>
+#include <string>
+#include <vector>
+
+#include "../../include/zkml_gpu.h"
+#include "field.hpp"
+
+namespace zk {
+
+// Status carrier: functions return int status codes; ZK_TRY propagates.
+#define ZK_TRY(expr)               \
+  do {                             \
+    int _st = (expr);              \
+    if (_st != ZK_OK) return _st;  \
+  } while (0)
+
+// HIP error -> status with message on the context.
+#define ZK_HIP(ctx, expr)                                                            \
+  do {                                                                               \
+    hipError_t _e = (expr);                                                          \
+    if (_e != hipSuccess) return (ctx)->fail(ZK_ERR_HIP, #expr, hipGetErrorString(_e)); \
+  } while (0)
+
+struct DevBuf {
+  void* p = nullptr;
+  size_t bytes = 0;
+};
+
+struct NttPlan;
+struct MsmWorkspace;
+
+struct KernelStat {
+  uint64_t launches = 0;
+  double total_ms = 0;
+};
+
+struct PendingTiming {
+  std::string name;
+  hipEvent_t a, b;
+};
+
+}  // namespace zk
+
+struct zk_context {
+  int device = 0;
+  hipStream_t stream = nullptr;
+  std::string last_error;
+  // NTT plans keyed by log_n; coset tables keyed by (log_n, g, inverse).
+  std::map<int, zk::NttPlan*> ntt_plans;
+  std::map<uint64_t, void*> coset_tables;
+  zk::MsmWorkspace* msm_ws = nullptr;
+  zk::MsmWorkspace* msm_ws_g2 = nullptr;
+  zk::DevBuf scratch_a, scratch_b, scratch_c;
+  // fixed-base tables for the generators (device), built on first use
+  void* g1_table = nullptr;
+  void* g2_table = nullptr;
+  // profiling
+  bool profiling = false;
+  std::map<std::string, zk::KernelStat> stats;
+  std::vector<zk::PendingTiming> pending;
+  std::string stat_names;
+
+  int fail(int code, const char* what, const char* detail = "") {
+    last_error = std::string(what) + (detail && *detail ? std::string(": ") + detail : std::string());
+    return code;
+  }
+  hipStream_t s(void* st) { return st ? (hipStream_t)st : stream; }
+  int ensure(zk::DevBuf& b, size_t bytes);
+  // Kernel timing brackets; no-ops unless profiling is enabled.
+  void tic(const char* name, hipStream_t st);
+  void toc(hipStream_t st);
+  void collect();
+};
+
+namespace zk {
+
+// Launch helper with error capture.
+#define ZK_LAUNCH(ctx, st, name, kernel, grid, block, shmem, ...)                            \
+  do {                                                                                     \
+    (ctx)->tic(name, st);                                                                  \
+    hipLaunchKernelGGL(kernel, grid, block, shmem, st, __VA_ARGS__);                       \
+    hipError_t _e = hipGetLastError();                                                     \
+    if (_e != hipSuccess) return (ctx)->fail(ZK_ERR_HIP, name, hipGetErrorString(_e));    \
+    (ctx)->toc(st);                                                                        \
+  } while (0)
+
+inline uint32_t cdiv(size_t a, size_t b) { return (uint32_t)((a + b - 1) / b); }
+
+// ---- NTT (ntt.hip)
+int ntt_run(zk_context* ctx, void* d_out, const void* d_in, int log_n, int inverse, int batch, uint64_t coset_g,
+            hipStream_t st);
+// Pointwise H step: h = (a*b - c) * zinv over n elements (ntt.hip)
+int quotient_pointwise(zk_context* ctx, void* d_h, const void* d_a, const void* d_b, const void* d_c, size_t n,
+                       const uint64_t zinv_mont[4], hipStream_t st);
+
+// ---- MSM (msm.hip); results are canonical affine in the zk_g*_affine layout
+int msm_g1_run(zk_context* ctx, const void* d_points, const void* d_scalars, size_t n, uint64_t out_affine[8],
+               hipStream_t st);
+int msm_g2_run(zk_context* ctx, const void* d_points, const void* d_scalars, size_t n, uint64_t out_affine[16],
+               hipStream_t st);
+void msm_workspace_free(MsmWorkspace* ws);
+
+// ---- fixed base (pointgen.hip)
+int g1_generator_mul(zk_context* ctx, const void* d_scalars, size_t n, void* d_out, hipStream_t st);
+int g2_generator_mul(zk_context* ctx, const void* d_scalars, size_t n, void* d_out, hipStream_t st);
+
+void ntt_plans_free(zk_context* ctx);
+
+}  // namespace zk

@@ -1,0 +1,207 @@
+"""Python (ctypes) front end of libzkml_gpu.so, the MI355X Groth16 prover core.
+
+Used by the tests, bench.py and __graft_entry__.py.  It calls the C ABI of
+include/zkml_gpu.h directly; there is no CPU fallback: if the library is not
+built, or a call fails, a ZkError is raised.
+"""
+import ctypes
+import os
+
+import numpy as np
+
+HERE = os.path.dirname(os.path.abspath(__file__))
+LIB_PATH = os.path.join(HERE, "libzkml_gpu.so")
+
+vp = ctypes.c_void_p
+_lib = None
+
+
+class ZkError(RuntimeError):
+    pass
+
+
+def lib():
+    global _lib
+    if _lib is None:
+        if not os.path.exists(LIB_PATH):
+            raise ZkError(f"{LIB_PATH} is not built (run __graft_entry__.build())")
+        L = ctypes.CDLL(LIB_PATH)
+        L.zk_create.argtypes = [ctypes.c_int, ctypes.POINTER(vp)]
+        L.zk_destroy.argtypes = [vp]
+        L.zk_status_string.restype = ctypes.c_char_p
+        L.zk_status_string.argtypes = [ctypes.c_int]
+        L.zk_last_error.restype = ctypes.c_char_p
+        L.zk_last_error.argtypes = [vp]
+        L.zk_synchronize.argtypes = [vp]
+        L.zk_get_stream.restype = vp
+        L.zk_get_stream.argtypes = [vp]
+        L.zk_dev_alloc.argtypes = [vp, ctypes.c_size_t, ctypes.POINTER(vp)]
+        L.zk_dev_free.argtypes = [vp, vp]
+        for f in ("zk_memcpy_h2d", "zk_memcpy_d2h", "zk_memcpy_d2d"):
+            getattr(L, f).argtypes = [vp, vp, vp, ctypes.c_size_t]
+        L.zk_set_profiling.argtypes = [vp, ctypes.c_int]
+        L.zk_kernel_stats.argtypes = [vp, ctypes.c_char_p, ctypes.POINTER(ctypes.c_uint64),
+                                      ctypes.POINTER(ctypes.c_double)]
+        L.zk_reset_kernel_stats.argtypes = [vp]
+        L.zk_kernel_stats_names.restype = ctypes.c_char_p
+        L.zk_kernel_stats_names.argtypes = [vp]
+        L.zk_ntt.argtypes = [vp, vp, vp, ctypes.c_int, ctypes.c_int, ctypes.c_int, vp]
+        L.zk_coset_ntt.argtypes = [vp, vp, vp, ctypes.c_int, ctypes.c_uint64, ctypes.c_int, ctypes.c_int, vp]
+        L.zk_msm_g1.argtypes = [vp, vp, vp, ctypes.c_size_t, vp, vp]
+        L.zk_msm_g2.argtypes = [vp, vp, vp, ctypes.c_size_t, vp, vp]
+        L.zk_msm_g1_host.argtypes = [vp, vp, vp, ctypes.c_int, vp]
+        L.zk_msm_g2_host.argtypes = [vp, vp, vp, ctypes.c_int, vp]
+        L.zk_g1_generator_mul.argtypes = [vp, vp, ctypes.c_size_t, vp, vp]
+        L.zk_g2_generator_mul.argtypes = [vp, vp, ctypes.c_size_t, vp, vp]
+        L.zk_r1cs_create.argtypes = [vp, ctypes.c_int, ctypes.c_int, ctypes.c_int, vp, ctypes.c_size_t, vp,
+                                     ctypes.c_size_t, vp, ctypes.c_size_t, ctypes.POINTER(vp)]
+        L.zk_r1cs_destroy.argtypes = [vp]
+        L.zk_r1cs_domain.argtypes = [vp, ctypes.POINTER(ctypes.c_int)]
+        L.zk_quotient_h.argtypes = [vp, vp, vp, ctypes.c_size_t, vp, vp]
+        L.zk_pk_load.argtypes = [vp, ctypes.c_char_p, ctypes.POINTER(vp)]
+        L.zk_pk_destroy.argtypes = [vp]
+        L.zk_pk_info.argtypes = [vp] + [ctypes.POINTER(ctypes.c_int)] * 3
+        L.zk_setup.argtypes = [vp, vp, ctypes.c_uint64, ctypes.c_char_p, ctypes.c_char_p]
+        L.zk_prove.argtypes = [vp, vp, vp, vp, ctypes.c_size_t, ctypes.c_int, ctypes.c_uint64, ctypes.c_int, vp, vp]
+        _lib = L
+    return _lib
+
+
+def _np_ptr(a):
+    assert a.flags["C_CONTIGUOUS"]
+    return a.ctypes.data_as(vp)
+
+
+R_WORDS = np.array([0x43E1F593F0000001, 0x2833E84879B97091, 0xB85045B68181585D, 0x30644E72E131A029],
+                   dtype=np.uint64)
+
+
+def random_fr(n, rng):
+    """n uniform elements of [0, r) as (n, 4) uint64 words (rejection sampling).
+    Any value below r is a valid Montgomery-form element."""
+    out = np.empty((n, 4), dtype=np.uint64)
+    filled = 0
+    while filled < n:
+        k = (n - filled) * 5 // 4 + 16
+        w = rng.integers(0, 2**64, size=(k, 4), dtype=np.uint64)
+        w[:, 3] &= np.uint64((1 << 62) - 1)
+        # lexicographic compare from the top limb
+        lt = np.zeros(k, dtype=bool)
+        eq = np.ones(k, dtype=bool)
+        for i in (3, 2, 1, 0):
+            lt |= eq & (w[:, i] < R_WORDS[i])
+            eq &= w[:, i] == R_WORDS[i]
+        w = w[lt]
+        take = min(len(w), n - filled)
+        out[filled:filled + take] = w[:take]
+        filled += take
+    return out
+
+
+class DeviceBuffer:
+    def __init__(self, ctx, nbytes):
+        self.ctx = ctx
+        self.nbytes = nbytes
+        p = vp()
+        ctx._check(lib().zk_dev_alloc(ctx.h, nbytes, ctypes.byref(p)))
+        self.ptr = p.value
+
+    def free(self):
+        if self.ptr:
+            lib().zk_dev_free(self.ctx.h, vp(self.ptr))
+            self.ptr = None
+
+    def __del__(self):
+        try:
+            self.free()
+        except Exception:
+            pass
+
+
+class Context:
+    def __init__(self, device=0):
+        self.h = vp()
+        st = lib().zk_create(device, ctypes.byref(self.h))
+        if st != 0:
+            raise ZkError(f"zk_create failed: {lib().zk_status_string(st).decode()}")
+
+    def _check(self, st, what=""):
+        if st != 0:
+            msg = lib().zk_last_error(self.h).decode(errors="replace")
+            raise ZkError(f"{what} failed ({lib().zk_status_string(st).decode()}): {msg}")
+
+    def close(self):
+        if self.h:
+            lib().zk_destroy(self.h)
+            self.h = None
+
+    def __del__(self):
+        try:
+            self.close()
+        except Exception:
+            pass
+
+    # ---- memory
+    def alloc(self, nbytes):
+        return DeviceBuffer(self, int(nbytes))
+
+    def upload(self, arr):
+        arr = np.ascontiguousarray(arr)
+        buf = self.alloc(max(arr.nbytes, 1))
+        self._check(lib().zk_memcpy_h2d(self.h, vp(buf.ptr), _np_ptr(arr), arr.nbytes), "h2d")
+        return buf
+
+    def h2d(self, buf, arr):
+        arr = np.ascontiguousarray(arr)
+        assert arr.nbytes <= buf.nbytes
+        self._check(lib().zk_memcpy_h2d(self.h, vp(buf.ptr), _np_ptr(arr), arr.nbytes), "h2d")
+
+    def d2h(self, buf, shape, dtype=np.uint64):
+        out = np.empty(shape, dtype=dtype)
+        self._check(lib().zk_memcpy_d2h(self.h, _np_ptr(out), vp(buf.ptr), out.nbytes), "d2h")
+        return out
+
+    def sync(self):
+        self._check(lib().zk_synchronize(self.h), "synchronize")
+
+    # ---- profiling
+    def set_profiling(self, on):
+        self._check(lib().zk_set_profiling(self.h, 1 if on else 0))
+
+    def kernel_stats(self, name):
+        n = ctypes.c_uint64()
+        ms = ctypes.c_double()
+        self._check(lib().zk_kernel_stats(self.h, name.encode(), ctypes.byref(n), ctypes.byref(ms)))
+        return n.value, ms.value
+
+    def reset_kernel_stats(self):
+        self._check(lib().zk_reset_kernel_stats(self.h))
+
+    def kernel_names(self):
+        s = lib().zk_kernel_stats_names(self.h).decode()
+        return [x for x in s.split(",") if x]
+
+    # ---- NTT
+    def ntt(self, d_out, d_in, log_n, inverse=False, batch=1):
+        self._check(lib().zk_ntt(self.h, vp(d_out.ptr), vp(d_in.ptr), log_n, int(inverse), batch, None), "zk_ntt")
+
+    def coset_ntt(self, d_out, d_in, log_n, g, inverse=False, batch=1):
+        self._check(lib().zk_coset_ntt(self.h, vp(d_out.ptr), vp(d_in.ptr), log_n, g, int(inverse), batch, None),
+                    "zk_coset_ntt")
+
+    # ---- MSM
+    def msm_g1(self, d_points, d_scalars, n):
+        out = np.zeros(8, dtype=np.uint64)
+        self._check(lib().zk_msm_g1(self.h, vp(d_points.ptr), vp(d_scalars.ptr), n, _np_ptr(out), None), "zk_msm_g1")
+        return out
+
+    def msm_g2(self, d_points, d_scalars, n):
+        out = np.zeros(16, dtype=np.uint64)
+        self._check(lib().zk_msm_g2(self.h, vp(d_points.ptr), vp(d_scalars.ptr), n, _np_ptr(out), None), "zk_msm_g2")
+        return out
+
+    def g1_generator_mul(self, d_scalars, n, d_out):
+        self._check(lib().zk_g1_generator_mul(self.h, vp(d_scalars.ptr), n, vp(d_out.ptr), None), "g1_generator_mul")
+
+    def g2_generator_mul(self, d_scalars, n, d_out):
+        self._check(lib().zk_g2_generator_mul(self.h, vp(d_scalars.ptr), n, vp(d_out.ptr), None), "g2_generator_mul")

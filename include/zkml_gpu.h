@@ -1,0 +1,155 @@
+/* zkml_gpu.h -- C ABI of the MI355X (gfx950) Groth16 prover core.
+ *
+ * Drop-in boundary for the data-parallel hot path of gdtsitlauri/cuda-zkml's
+ * prover.  Every entry point names the reference interface it replaces
+ * (paths relative to the reference root).  Plain pointers and sizes only.
+ *
+ * Data layouts are the reference's in-memory layouts:
+ *   zk_fr, zk_fq      32 bytes: 4 x uint64 little endian, Montgomery form with
+ *                     R = 2^256 (src/field/fp.cuh:28-31, 322-324).
+ *   zk_g1_affine      64 bytes: x, y (zk_fq).  x = y = 0 encodes the point at
+ *                     infinity (no finite curve point has x = y = 0).
+ *   zk_g2_affine      128 bytes: x.c0, x.c1, y.c0, y.c1.
+ *   reference structs G1Affine (72 bytes: x, y, bool infinity at byte 64) and
+ *                     G2Affine (136 bytes, bool at byte 128) are accepted by the
+ *                     *_host entry points (src/curve/g1.cuh:29-33, g2.cuh:25-29).
+ *   zk_sparse_entry   40 bytes {int32 row; int32 col; zk_fr value}
+ *                     (src/prover/circuit.cuh:32-36).
+ *
+ * Errors: every function returns ZK_OK (0) or a positive zk_status; the
+ * reference instead exits the process on a device error (src/common.cuh:11-19).
+ * zk_last_error() gives a message for the last failure on a context.
+ *
+ * Streams: `stream` arguments are hipStream_t values; NULL selects the
+ * context's own stream.  Calls that return a host value synchronize.
+ * A context is not re-entrant: one host thread per context at a time.
+ */
+#ifndef ZKML_GPU_H
+#define ZKML_GPU_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+typedef struct zk_context zk_context;
+typedef struct zk_r1cs zk_r1cs;
+typedef struct zk_pk zk_pk;
+
+enum zk_status {
+  ZK_OK = 0,
+  ZK_ERR_INVALID = 1,   /* bad argument */
+  ZK_ERR_SIZE = 2,      /* size outside the supported range */
+  ZK_ERR_OOM = 3,       /* device or host allocation failed */
+  ZK_ERR_HIP = 4,       /* HIP runtime error */
+  ZK_ERR_IO = 5,        /* file missing, truncated or malformed */
+  ZK_ERR_WITNESS = 6,   /* witness does not satisfy the R1CS */
+  ZK_ERR_MISMATCH = 7   /* witness / key / circuit sizes disagree */
+};
+
+typedef struct zk_sparse_entry {
+  int32_t row;
+  int32_t col;
+  uint64_t value[4];
+} zk_sparse_entry;
+
+/* ---- context and device memory ---------------------------------------- */
+int zk_create(int device, zk_context** out);
+void zk_destroy(zk_context* ctx);
+const char* zk_status_string(int status);
+const char* zk_last_error(const zk_context* ctx);
+int zk_synchronize(zk_context* ctx);
+void* zk_get_stream(zk_context* ctx);
+int zk_dev_alloc(zk_context* ctx, size_t bytes, void** d_ptr);
+int zk_dev_free(zk_context* ctx, void* d_ptr);
+int zk_memcpy_h2d(zk_context* ctx, void* d_dst, const void* h_src, size_t bytes);
+int zk_memcpy_d2h(zk_context* ctx, void* h_dst, const void* d_src, size_t bytes);
+int zk_memcpy_d2d(zk_context* ctx, void* d_dst, const void* d_src, size_t bytes);
+
+/* Per-kernel timing with HIP events recorded on the stream each kernel is
+ * launched on (off by default).  Names: see zk_kernel_stats_names(). */
+int zk_set_profiling(zk_context* ctx, int enable);
+int zk_kernel_stats(zk_context* ctx, const char* kernel, uint64_t* launches, double* total_ms);
+int zk_reset_kernel_stats(zk_context* ctx);
+const char* zk_kernel_stats_names(zk_context* ctx);
+
+/* ---- NTT over Fr -------------------------------------------------------
+ * Replaces bn254::ntt_gpu(Fr* d_out, const Fr* d_in, int log_n, bool inverse)
+ * (src/ntt/ntt.cuh:49, src/ntt/ntt.cu:354-465) and ntt_gpu_inplace (:467).
+ * out[j] = sum_i in[i] * w^(i*j), w = 5^((r-1)/2^28)^(2^(28-log_n)); the
+ * inverse uses w^-1 and scales by n^-1.  Natural order in and out; d_out may
+ * equal d_in.  1 <= log_n <= 24 (NTT_MAX_LOG, src/common.cuh:78); the reference
+ * returns silently above that, this returns ZK_ERR_SIZE.  `batch` transforms
+ * of n elements each are laid out back to back. */
+int zk_ntt(zk_context* ctx, void* d_out, const void* d_in, int log_n, int inverse, int batch, void* stream);
+
+/* Coset NTT as used by Groth16Prover::compute_h (src/prover/groth16.cu:350-383):
+ * forward: out = NTT(in[i] * g^i); inverse: out[i] = iNTT(in)[i] * g^-i.
+ * g is a small plain integer (the prover uses 5; BASELINE config 2 uses 7). */
+int zk_coset_ntt(zk_context* ctx, void* d_out, const void* d_in, int log_n, uint64_t g, int inverse, int batch,
+                 void* stream);
+
+/* ---- MSM ----------------------------------------------------------------
+ * Replaces bn254::msm_g1 / msm_g2 (src/msm/msm.cuh:67-68, msm.cu:320-598):
+ * result = sum_i scalars[i] * points[i].  Device-resident inputs (points in
+ * zk_g1_affine / zk_g2_affine layout, scalars zk_fr), result written to host
+ * memory as an affine point in the same layout (the reference returns a
+ * Jacobian point whose callers convert it to affine).  n == 0 gives infinity. */
+int zk_msm_g1(zk_context* ctx, const void* d_points, const void* d_scalars, size_t n, void* h_result,
+              void* stream);
+int zk_msm_g2(zk_context* ctx, const void* d_points, const void* d_scalars, size_t n, void* h_result,
+              void* stream);
+
+/* Host-pointer drop-ins with the reference's exact signature semantics:
+ * h_points are reference G1Affine / G2Affine structs (72 / 136 bytes),
+ * h_scalars are Fr, h_result receives a reference G1Jacobian / G2Jacobian
+ * (96 / 192 bytes: x, y, z Montgomery; z = 1, or z = 0 for infinity). */
+int zk_msm_g1_host(zk_context* ctx, const void* h_points, const void* h_scalars, int n, void* h_result_jacobian);
+int zk_msm_g2_host(zk_context* ctx, const void* h_points, const void* h_scalars, int n, void* h_result_jacobian);
+
+/* ---- fixed-base generation (setup and synthetic inputs) -----------------
+ * d_out[i] = k[i] * G for the group generator G (G1 (1,2), G2 EIP-197:
+ * src/curve/g1.cuh:40, g2.cuh:47-65); k in zk_fr layout (Montgomery). */
+int zk_g1_generator_mul(zk_context* ctx, const void* d_scalars, size_t n, void* d_out, void* stream);
+int zk_g2_generator_mul(zk_context* ctx, const void* d_scalars, size_t n, void* d_out, void* stream);
+
+/* ---- R1CS and the quotient polynomial -----------------------------------
+ * zk_r1cs_create uploads the reference's COO matrices (R1CS::A/B/C,
+ * src/prover/circuit.cuh:39-50) once and keeps them on the device in CSR form.
+ * zk_quotient_h replaces Groth16Prover::compute_h (groth16.cu:263-390):
+ * h = (A.w * B.w - C.w) / (x^n - 1) via 3 iNTT, 3 coset NTT (shift 5, or 7
+ * when 5^n = 1), a pointwise step and a coset iNTT, all resident on the
+ * device.  d_h receives n = 2^ceil(log2(max(num_constraints, 4))) elements. */
+int zk_r1cs_create(zk_context* ctx, int num_constraints, int num_variables, int num_public,
+                   const zk_sparse_entry* A, size_t nA, const zk_sparse_entry* B, size_t nB,
+                   const zk_sparse_entry* C, size_t nC, zk_r1cs** out);
+void zk_r1cs_destroy(zk_r1cs* r1cs);
+int zk_r1cs_domain(const zk_r1cs* r1cs, int* log_n);
+int zk_quotient_h(zk_context* ctx, const zk_r1cs* r1cs, const void* d_witness, size_t m, void* d_h, void* stream);
+
+/* ---- proving key, setup and prove ---------------------------------------
+ * zk_pk_load replaces ProvingKey::load_streaming (groth16.cu:1190-1314): reads
+ * a ZKMLPK3 file with the same checks and keeps all queries on the device.
+ * zk_setup replaces Groth16Prover::setup (groth16.cu:446-642) for a given
+ * toxic-waste seed (the reference's deterministic seed is 0xDEADBEEF42) and
+ * writes a ZKMLPK3 proving key and a verification key (verifier.cu:103-148).
+ * zk_prove replaces Groth16Prover::prove (groth16.cu:655-920): r and s are the
+ * first two nonzero Fr::from_uint(std::mt19937_64(blind_seed)()) draws (the
+ * reference's deterministic seed is 0xCAFEBABE); the 256-byte proof is
+ * A.x, A.y, B.x.c0, B.x.c1, B.y.c0, B.y.c1, C.x, C.y in standard form
+ * (Groth16Proof::serialize, groth16.cu:1058-1074).  check_witness mirrors the
+ * ZKML_SKIP_WITNESS_CHECK switch (groth16.cu:687-695).  timings_ms (optional,
+ * 8 doubles): total, quotient, A, B(G2), L, H, B1, host. */
+int zk_pk_load(zk_context* ctx, const char* path, zk_pk** out);
+void zk_pk_destroy(zk_pk* pk);
+int zk_pk_info(const zk_pk* pk, int* num_constraints, int* num_variables, int* num_public);
+int zk_setup(zk_context* ctx, const zk_r1cs* r1cs, uint64_t toxic_seed, const char* pk_path, const char* vk_path);
+int zk_prove(zk_context* ctx, const zk_pk* pk, const zk_r1cs* r1cs, const void* h_witness, size_t m,
+             int num_public, uint64_t blind_seed, int check_witness, uint8_t proof_out[256], double* timings_ms);
+
+#ifdef __cplusplus
+}
+#endif
+#endif /* ZKML_GPU_H */
