@@ -8,7 +8,7 @@ using namespace zk;
 int zk_context::ensure(DevBuf& b, size_t bytes) {
   if (b.bytes >= bytes) return ZK_OK;
   if (b.p) {
-    hipFree(b.p);
+    (void)hipFree(b.p);
     b.p = nullptr;
     b.bytes = 0;
   }
@@ -25,27 +25,27 @@ void zk_context::tic(const char* name, hipStream_t st) {
   if (!profiling) return;
   PendingTiming t;
   t.name = name;
-  hipEventCreate(&t.a);
-  hipEventCreate(&t.b);
-  hipEventRecord(t.a, st);
+  (void)hipEventCreate(&t.a);
+  (void)hipEventCreate(&t.b);
+  (void)hipEventRecord(t.a, st);
   pending.push_back(t);
 }
 
 void zk_context::toc(hipStream_t st) {
   if (!profiling || pending.empty()) return;
-  hipEventRecord(pending.back().b, st);
+  (void)hipEventRecord(pending.back().b, st);
 }
 
 void zk_context::collect() {
   for (auto& t : pending) {
-    hipEventSynchronize(t.b);
+    (void)hipEventSynchronize(t.b);
     float ms = 0;
-    hipEventElapsedTime(&ms, t.a, t.b);
+    (void)hipEventElapsedTime(&ms, t.a, t.b);
     KernelStat& k = stats[t.name];
     k.launches++;
     k.total_ms += ms;
-    hipEventDestroy(t.a);
-    hipEventDestroy(t.b);
+    (void)hipEventDestroy(t.a);
+    (void)hipEventDestroy(t.b);
   }
   pending.clear();
 }
@@ -71,17 +71,17 @@ int zk_create(int device, zk_context** out) {
 
 void zk_destroy(zk_context* ctx) {
   if (!ctx) return;
-  hipSetDevice(ctx->device);
-  hipStreamSynchronize(ctx->stream);
+  (void)hipSetDevice(ctx->device);
+  (void)hipStreamSynchronize(ctx->stream);
   ctx->collect();
   ntt_plans_free(ctx);
   if (ctx->msm_ws) msm_workspace_free(ctx->msm_ws);
   if (ctx->msm_ws_g2) msm_workspace_free(ctx->msm_ws_g2);
   for (DevBuf* b : {&ctx->scratch_a, &ctx->scratch_b, &ctx->scratch_c})
-    if (b->p) hipFree(b->p);
-  if (ctx->g1_table) hipFree(ctx->g1_table);
-  if (ctx->g2_table) hipFree(ctx->g2_table);
-  hipStreamDestroy(ctx->stream);
+    if (b->p) (void)hipFree(b->p);
+  if (ctx->g1_table) (void)hipFree(ctx->g1_table);
+  if (ctx->g2_table) (void)hipFree(ctx->g2_table);
+  (void)hipStreamDestroy(ctx->stream);
   delete ctx;
 }
 

@@ -1,0 +1,187 @@
+// BN254 G1 (over Fq) and G2 (over Fq2 = Fq[u]/(u^2+1)) group arithmetic for
+// the MSM kernels, in XYZZ coordinates: (X, Y, ZZ, ZZZ) with x = X/ZZ,
+// y = Y/ZZZ, ZZ^3 = ZZZ^2; ZZ = 0 encodes the point at infinity.  Formulas are
+// the a = 0 cases of the EFD "xyzz" family: madd-2008-s (8M+2S),
+// add-2008-s (12M+2S), dbl-2008-s-1 (6M+3S) and mdbl-2008-s-1.  The reference
+// uses Jacobian coordinates (src/curve/g1.cuh:89-187) and affine G2 formulas
+// (src/curve/g2.cuh:103-146); every one of them computes the same group law,
+// and results leave the device as canonical affine points.
+//
+// All functions are generic over the coordinate field F (fq or fq2) through
+// the overloads fmul/fsqr/fadd/fsub/fis_zero/fdbl below.
+#pragma once
+#include "field.hpp"
+
+namespace zk {
+
+// ------------------------------------------------------------------ Fq2
+struct fq2 {
+  fq c0, c1;
+};
+
+ZK_HD fq2 fadd(const fq2& a, const fq2& b) { return fq2{fadd(a.c0, b.c0), fadd(a.c1, b.c1)}; }
+ZK_HD fq2 fsub(const fq2& a, const fq2& b) { return fq2{fsub(a.c0, b.c0), fsub(a.c1, b.c1)}; }
+ZK_HD fq2 fdbl(const fq2& a) { return fq2{fdbl(a.c0), fdbl(a.c1)}; }
+ZK_HD fq2 fneg(const fq2& a) { return fq2{fneg(a.c0), fneg(a.c1)}; }
+// Karatsuba, 3 base multiplies (reference src/field/fp2.cuh:73-78).
+ZK_HD fq2 fmul(const fq2& a, const fq2& b) {
+  fq ac = fmul(a.c0, b.c0);
+  fq bd = fmul(a.c1, b.c1);
+  fq s = fmul(fadd_lazy(a.c0, a.c1), fadd_lazy(b.c0, b.c1));
+  return fq2{fsub(ac, bd), fsub(fsub(s, ac), bd)};
+}
+// (a + bu)^2 = (a+b)(a-b) + 2ab u
+ZK_HD fq2 fsqr(const fq2& a) {
+  fq ab = fmul(a.c0, a.c1);
+  return fq2{fmul(fadd_lazy(a.c0, a.c1), fsub(a.c0, a.c1)), fdbl(ab)};
+}
+ZK_HD bool fis_zero(const fq2& a) { return fis_zero(a.c0) && fis_zero(a.c1); }
+
+ZK_HD void fset_zero(fq& a) { a = fe_zero<FqP>(); }
+ZK_HD void fset_zero(fq2& a) { a = fq2{fe_zero<FqP>(), fe_zero<FqP>()}; }
+ZK_HD void fset_one(fq& a) { a = fe_one<FqP>(); }
+ZK_HD void fset_one(fq2& a) { a = fq2{fe_one<FqP>(), fe_zero<FqP>()}; }
+
+// ------------------------------------------------------------------ XYZZ
+template <class F>
+struct xyzz {
+  F x, y, zz, zzz;
+};
+
+template <class F>
+ZK_HD void xyzz_set_inf(xyzz<F>& p) {
+  fset_zero(p.x);
+  fset_zero(p.y);
+  fset_zero(p.zz);
+  fset_zero(p.zzz);
+}
+
+template <class F>
+ZK_HD bool xyzz_is_inf(const xyzz<F>& p) {
+  return fis_zero(p.zz);
+}
+
+template <class F>
+ZK_HD void xyzz_set_affine(xyzz<F>& p, const F& x, const F& y) {
+  p.x = x;
+  p.y = y;
+  fset_one(p.zz);
+  fset_one(p.zzz);
+}
+
+// p = 2 * (x, y) for an affine point (mdbl-2008-s-1)
+template <class F>
+ZK_HD void xyzz_mdbl(xyzz<F>& p, const F& x, const F& y) {
+  F u = fdbl(y);
+  F v = fsqr(u);
+  F w = fmul(u, v);
+  F s = fmul(x, v);
+  F x2 = fsqr(x);
+  F m = fadd(fdbl(x2), x2);
+  F x3 = fsub(fsub(fsqr(m), s), s);
+  F y3 = fsub(fmul(m, fsub(s, x3)), fmul(w, y));
+  p.x = x3;
+  p.y = y3;
+  p.zz = v;
+  p.zzz = w;
+}
+
+// p = 2p (dbl-2008-s-1)
+template <class F>
+ZK_HD void xyzz_dbl(xyzz<F>& p) {
+  if (xyzz_is_inf(p)) return;
+  F u = fdbl(p.y);
+  F v = fsqr(u);
+  F w = fmul(u, v);
+  F s = fmul(p.x, v);
+  F x2 = fsqr(p.x);
+  F m = fadd(fdbl(x2), x2);
+  F x3 = fsub(fsub(fsqr(m), s), s);
+  F y3 = fsub(fmul(m, fsub(s, x3)), fmul(w, p.y));
+  p.x = x3;
+  p.y = y3;
+  p.zz = fmul(v, p.zz);
+  p.zzz = fmul(w, p.zzz);
+}
+
+// p += (x2, y2) affine, finite (madd-2008-s)
+template <class F>
+ZK_HD void xyzz_madd(xyzz<F>& p, const F& x2, const F& y2) {
+  if (xyzz_is_inf(p)) {
+    xyzz_set_affine(p, x2, y2);
+    return;
+  }
+  F u2 = fmul(x2, p.zz);
+  F s2 = fmul(y2, p.zzz);
+  F P = fsub(u2, p.x);
+  F R = fsub(s2, p.y);
+  if (fis_zero(P)) {
+    if (fis_zero(R)) xyzz_mdbl(p, x2, y2);
+    else xyzz_set_inf(p);
+    return;
+  }
+  F pp = fsqr(P);
+  F ppp = fmul(P, pp);
+  F q = fmul(p.x, pp);
+  F x3 = fsub(fsub(fsqr(R), ppp), fdbl(q));
+  F y3 = fsub(fmul(R, fsub(q, x3)), fmul(p.y, ppp));
+  p.x = x3;
+  p.y = y3;
+  p.zz = fmul(p.zz, pp);
+  p.zzz = fmul(p.zzz, ppp);
+}
+
+// p += q (add-2008-s)
+template <class F>
+ZK_HD void xyzz_add(xyzz<F>& p, const xyzz<F>& q) {
+  if (xyzz_is_inf(q)) return;
+  if (xyzz_is_inf(p)) {
+    p = q;
+    return;
+  }
+  F u1 = fmul(p.x, q.zz);
+  F u2 = fmul(q.x, p.zz);
+  F s1 = fmul(p.y, q.zzz);
+  F s2 = fmul(q.y, p.zzz);
+  F P = fsub(u2, u1);
+  F R = fsub(s2, s1);
+  if (fis_zero(P)) {
+    if (fis_zero(R)) xyzz_dbl(p);
+    else xyzz_set_inf(p);
+    return;
+  }
+  F pp = fsqr(P);
+  F ppp = fmul(P, pp);
+  F qq = fmul(u1, pp);
+  F x3 = fsub(fsub(fsqr(R), ppp), fdbl(qq));
+  F y3 = fsub(fmul(R, fsub(qq, x3)), fmul(s1, ppp));
+  p.x = x3;
+  p.y = y3;
+  p.zz = fmul(fmul(p.zz, q.zz), pp);
+  p.zzz = fmul(fmul(p.zzz, q.zzz), ppp);
+}
+
+template <class F>
+ZK_HD void xyzz_neg(xyzz<F>& p) {
+  p.y = fneg(p.y);
+}
+
+// p = k * p for a small non-negative integer k (double-and-add, MSB first).
+template <class F>
+ZK_HD void xyzz_mul_small(xyzz<F>& p, uint32_t k) {
+  xyzz<F> acc;
+  xyzz_set_inf(acc);
+  if (k == 0 || xyzz_is_inf(p)) {
+    p = acc;
+    return;
+  }
+  int top = 31 - __builtin_clz(k);
+  acc = p;
+  for (int i = top - 1; i >= 0; i--) {
+    xyzz_dbl(acc);
+    if ((k >> i) & 1u) xyzz_add(acc, p);
+  }
+  p = acc;
+}
+
+}  // namespace zk

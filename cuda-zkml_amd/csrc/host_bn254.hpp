@@ -1,0 +1,242 @@
+// Host-side BN254 arithmetic for the serial tails of the prover: MSM window
+// combination (W*c doublings), affine conversion, the r/s blinding scalar
+// multiplications of Groth16Prover::prove (reference src/prover/groth16.cu:
+// 769-840) and file encodings.  A CPU core finishes a serial field multiply
+// far sooner than a single wave64, so these chains stay on the host.
+//
+// Representation: the reference's 4 x u64 Montgomery form (R = 2^256),
+// multiplied with CIOS and one conditional subtraction, as in
+// src/field/montgomery.cuh:330-368.  Values are always canonical.
+#pragma once
+#include <stdint.h>
+#include <string.h>
+
+namespace zkh {
+
+typedef unsigned __int128 u128;
+
+struct QMod {
+  static constexpr uint64_t M[4] = {0x3C208C16D87CFD47ULL, 0x97816A916871CA8DULL, 0xB85045B68181585DULL,
+                                    0x30644E72E131A029ULL};
+  static constexpr uint64_t INV = 0x87D20782E4866389ULL;
+  static constexpr uint64_t ONE[4] = {0xD35D438DC58F0D9DULL, 0x0A78EB28F5C70B3DULL, 0x666EA36F7879462CULL,
+                                      0x0E0A77C19A07DF2FULL};
+  static constexpr uint64_t R2[4] = {0xF32CFC5B538AFA89ULL, 0xB5E71911D44501FBULL, 0x47AB1EFF0A417FF6ULL,
+                                     0x06D89F71CAB8351FULL};
+};
+struct RMod {
+  static constexpr uint64_t M[4] = {0x43E1F593F0000001ULL, 0x2833E84879B97091ULL, 0xB85045B68181585DULL,
+                                    0x30644E72E131A029ULL};
+  static constexpr uint64_t INV = 0xC2E1F593EFFFFFFFULL;
+  static constexpr uint64_t ONE[4] = {0xAC96341C4FFFFFFBULL, 0x36FC76959F60CD29ULL, 0x666EA36F7879462EULL,
+                                      0x0E0A77C19A07DF2FULL};
+  static constexpr uint64_t R2[4] = {0x1BB8E645AE216DA7ULL, 0x53FE3AB1E35C59E3ULL, 0x8C49833D53BB8085ULL,
+                                     0x0216D0B17F4E44A5ULL};
+};
+
+template <class M>
+struct F {
+  uint64_t v[4];
+
+  static F zero() { return F{{0, 0, 0, 0}}; }
+  static F one() { return F{{M::ONE[0], M::ONE[1], M::ONE[2], M::ONE[3]}}; }
+  static F raw(const void* p) {
+    F r;
+    memcpy(r.v, p, 32);
+    return r;
+  }
+  bool is_zero() const { return (v[0] | v[1] | v[2] | v[3]) == 0; }
+  bool operator==(const F& o) const { return memcmp(v, o.v, 32) == 0; }
+
+  static inline uint64_t sub4(uint64_t* r, const uint64_t* a, const uint64_t* b) {
+    uint64_t br = 0;
+    for (int i = 0; i < 4; i++) {
+      u128 d = (u128)a[i] - b[i] - br;
+      r[i] = (uint64_t)d;
+      br = (uint64_t)(d >> 127);
+    }
+    return br;
+  }
+  static inline void mont(uint64_t* r, const uint64_t* a, const uint64_t* b) {
+    uint64_t t0 = 0, t1 = 0, t2 = 0, t3 = 0, t4 = 0;
+    for (int i = 0; i < 4; i++) {
+      u128 c = (u128)a[i] * b[0] + t0;
+      t0 = (uint64_t)c;
+      c = (c >> 64) + (u128)a[i] * b[1] + t1;
+      t1 = (uint64_t)c;
+      c = (c >> 64) + (u128)a[i] * b[2] + t2;
+      t2 = (uint64_t)c;
+      c = (c >> 64) + (u128)a[i] * b[3] + t3;
+      t3 = (uint64_t)c;
+      t4 += (uint64_t)(c >> 64);
+      uint64_t m = t0 * M::INV;
+      c = ((u128)m * M::M[0] + t0) >> 64;
+      c += (u128)m * M::M[1] + t1;
+      t0 = (uint64_t)c;
+      c = (c >> 64) + (u128)m * M::M[2] + t2;
+      t1 = (uint64_t)c;
+      c = (c >> 64) + (u128)m * M::M[3] + t3;
+      t2 = (uint64_t)c;
+      c = (c >> 64) + t4;
+      t3 = (uint64_t)c;
+      t4 = (uint64_t)(c >> 64);
+    }
+    uint64_t t[4] = {t0, t1, t2, t3}, s[4];
+    if (!sub4(s, t, M::M)) memcpy(r, s, 32);
+    else memcpy(r, t, 32);
+  }
+  F operator*(const F& o) const {
+    F r;
+    mont(r.v, v, o.v);
+    return r;
+  }
+  F sqr() const { return *this * *this; }
+  F operator+(const F& o) const {
+    F r, t;
+    u128 c = 0;
+    for (int i = 0; i < 4; i++) {
+      c += (u128)v[i] + o.v[i];
+      r.v[i] = (uint64_t)c;
+      c >>= 64;
+    }
+    if (!sub4(t.v, r.v, M::M)) return t;  // sums stay below 2^256 since 2m < 2^255
+    return r;
+  }
+  F operator-(const F& o) const {
+    F r;
+    if (sub4(r.v, v, o.v)) {
+      u128 c = 0;
+      for (int i = 0; i < 4; i++) {
+        c += (u128)r.v[i] + M::M[i];
+        r.v[i] = (uint64_t)c;
+        c >>= 64;
+      }
+    }
+    return r;
+  }
+  F operator-() const { return zero() - *this; }
+  F dbl() const { return *this + *this; }
+  static F from_std(const uint64_t* s) {
+    F r;
+    mont(r.v, s, M::R2);
+    return r;
+  }
+  static F from_u64(uint64_t x) {
+    uint64_t s[4] = {x, 0, 0, 0};
+    return from_std(s);
+  }
+  void to_std(uint64_t* out) const {
+    uint64_t one[4] = {1, 0, 0, 0};
+    mont(out, v, one);
+  }
+  F pow(const uint64_t* e) const {
+    F r = one();
+    for (int i = 255; i >= 0; i--) {
+      r = r.sqr();
+      if ((e[i >> 6] >> (i & 63)) & 1) r = r * *this;
+    }
+    return r;
+  }
+  F inv() const {
+    uint64_t e[4] = {M::M[0] - 2, M::M[1], M::M[2], M::M[3]};
+    return pow(e);
+  }
+};
+
+typedef F<QMod> Fq;
+typedef F<RMod> Fr;
+
+struct Fq2 {
+  Fq c0, c1;
+  static Fq2 zero() { return Fq2{Fq::zero(), Fq::zero()}; }
+  static Fq2 one() { return Fq2{Fq::one(), Fq::zero()}; }
+  bool is_zero() const { return c0.is_zero() && c1.is_zero(); }
+  bool operator==(const Fq2& o) const { return c0 == o.c0 && c1 == o.c1; }
+  Fq2 operator+(const Fq2& o) const { return Fq2{c0 + o.c0, c1 + o.c1}; }
+  Fq2 operator-(const Fq2& o) const { return Fq2{c0 - o.c0, c1 - o.c1}; }
+  Fq2 operator-() const { return Fq2{-c0, -c1}; }
+  Fq2 operator*(const Fq2& o) const {
+    Fq a = c0 * o.c0, b = c1 * o.c1;
+    return Fq2{a - b, (c0 + c1) * (o.c0 + o.c1) - a - b};
+  }
+  Fq2 sqr() const { return *this * *this; }
+  Fq2 dbl() const { return *this + *this; }
+  Fq2 inv() const {
+    Fq n = (c0.sqr() + c1.sqr()).inv();
+    return Fq2{c0 * n, -(c1 * n)};
+  }
+};
+
+// Jacobian point (x = X/Z^2, y = Y/Z^3), Z = 0 at infinity.
+template <class E>
+struct Jac {
+  E x, y, z;
+  static Jac inf() { return Jac{E::zero(), E::one(), E::zero()}; }
+  bool is_inf() const { return z.is_zero(); }
+  static Jac affine(const E& x, const E& y) { return Jac{x, y, E::one()}; }
+  Jac dbl() const {
+    if (is_inf()) return *this;
+    E a = x.sqr(), b = y.sqr(), c = b.sqr();
+    E d = ((x + b).sqr() - a - c).dbl();
+    E e = a.dbl() + a;
+    E f = e.sqr();
+    Jac r;
+    r.x = f - d.dbl();
+    r.y = e * (d - r.x) - c.dbl().dbl().dbl();
+    r.z = (y * z).dbl();
+    return r;
+  }
+  Jac add(const Jac& o) const {
+    if (is_inf()) return o;
+    if (o.is_inf()) return *this;
+    E z1z1 = z.sqr(), z2z2 = o.z.sqr();
+    E u1 = x * z2z2, u2 = o.x * z1z1;
+    E s1 = y * o.z * z2z2, s2 = o.y * z * z1z1;
+    E h = u2 - u1, rr = s2 - s1;
+    if (h.is_zero()) return rr.is_zero() ? dbl() : inf();
+    E hh = h.sqr(), hhh = hh * h, v = u1 * hh;
+    Jac r;
+    r.x = rr.sqr() - hhh - v.dbl();
+    r.y = rr * (v - r.x) - s1 * hhh;
+    r.z = z * o.z * h;
+    return r;
+  }
+  Jac neg() const { return Jac{x, -y, z}; }
+  // k given as 4 little-endian u64 words in standard form
+  Jac mul_std(const uint64_t* k) const {
+    Jac r = inf();
+    int top = -1;
+    for (int i = 255; i >= 0; i--)
+      if ((k[i >> 6] >> (i & 63)) & 1) {
+        top = i;
+        break;
+      }
+    for (int i = top; i >= 0; i--) {
+      r = r.dbl();
+      if ((k[i >> 6] >> (i & 63)) & 1) r = r.add(*this);
+    }
+    return r;
+  }
+  Jac mul(const Fr& k) const {
+    uint64_t s[4];
+    k.to_std(s);
+    return mul_std(s);
+  }
+  // canonical affine; returns false for infinity (x = y = 0 then)
+  bool to_affine(E& ax, E& ay) const {
+    if (is_inf()) {
+      ax = E::zero();
+      ay = E::zero();
+      return false;
+    }
+    E zi = z.inv(), zi2 = zi.sqr();
+    ax = x * zi2;
+    ay = y * zi2 * zi;
+    return true;
+  }
+};
+
+typedef Jac<Fq> G1;
+typedef Jac<Fq2> G2;
+
+}  // namespace zkh

@@ -1,17 +1,7 @@
 // Entry points not yet implemented in this build step.
 #include "zk_internal.hpp"
-namespace zk {
-struct MsmWorkspace {};
-void msm_workspace_free(MsmWorkspace* ws) { delete ws; }
-}
 extern "C" {
 #define NI(ctx) ((ctx) ? (ctx)->fail(ZK_ERR_INVALID, "not implemented") : ZK_ERR_INVALID)
-int zk_msm_g1(zk_context* ctx, const void*, const void*, size_t, void*, void*) { return NI(ctx); }
-int zk_msm_g2(zk_context* ctx, const void*, const void*, size_t, void*, void*) { return NI(ctx); }
-int zk_msm_g1_host(zk_context* ctx, const void*, const void*, int, void*) { return NI(ctx); }
-int zk_msm_g2_host(zk_context* ctx, const void*, const void*, int, void*) { return NI(ctx); }
-int zk_g1_generator_mul(zk_context* ctx, const void*, size_t, void*, void*) { return NI(ctx); }
-int zk_g2_generator_mul(zk_context* ctx, const void*, size_t, void*, void*) { return NI(ctx); }
 int zk_r1cs_create(zk_context* ctx, int, int, int, const zk_sparse_entry*, size_t, const zk_sparse_entry*, size_t,
                    const zk_sparse_entry*, size_t, zk_r1cs**) { return NI(ctx); }
 void zk_r1cs_destroy(zk_r1cs*) {}
