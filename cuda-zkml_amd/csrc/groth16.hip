@@ -1,0 +1,774 @@
+// Groth16 prover core: R1CS on the device, quotient polynomial h(x), proving
+// key loading, trusted setup and prove, behind the C ABI.
+//
+// Reference: src/prover/groth16.cu (compute_h :263-390, setup :446-642,
+// prove :655-920, ZKMLPK3 save/load :1104-1314), src/prover/circuit.cuh
+// (R1CS, verify_witness :93-124), src/verifier/verifier.cu (VK layout).
+#include <stdio.h>
+#include <string.h>
+
+#include <algorithm>
+#include <random>
+#include <vector>
+
+#include "curve.hpp"
+#include "host_bn254.hpp"
+#include "zk_internal.hpp"
+
+using namespace zk;
+
+struct zk_r1cs {
+  int nc = 0, nv = 0, npub = 0, log_n = 0;
+  size_t n = 0;
+  // CSR per matrix (A, B, C), rows < n; values are the reference's Montgomery
+  // words multiplied by 32 so that fmul(w, v') = w v in Montgomery form.
+  uint32_t* rowptr[3] = {nullptr, nullptr, nullptr};
+  uint32_t* col[3] = {nullptr, nullptr, nullptr};
+  uint4* val[3] = {nullptr, nullptr, nullptr};
+  size_t nnz[3] = {0, 0, 0};
+  // host COO copies for setup (QAP evaluation at tau)
+  std::vector<zk_sparse_entry> coo[3];
+};
+
+struct zk_pk {
+  int n = 0, m = 0, npub = 0;
+  // fixed points, Montgomery words, x = y = 0 at infinity
+  uint64_t alpha1[8], beta1[8], delta1[8];
+  uint64_t beta2[16], gamma2[16], delta2[16];
+  size_t nA = 0, nB1 = 0, nB2 = 0, nL = 0, nH = 0, ntau1 = 0, ntau2 = 0;
+  void *A = nullptr, *B1 = nullptr, *B2 = nullptr, *L = nullptr, *H = nullptr;  // device point records
+};
+
+namespace {
+
+// ------------------------------------------------------------------ kernels
+__device__ __forceinline__ fr ld_fr(const uint4* __restrict__ p, size_t i) {
+  uint4 a = p[2 * i], b = p[2 * i + 1];
+  uint32_t w[8] = {a.x, a.y, a.z, a.w, b.x, b.y, b.z, b.w};
+  return repack_in<FrP>(w);
+}
+
+__device__ __forceinline__ void st_fr(uint4* __restrict__ p, size_t i, const fr& x) {
+  uint32_t w[8];
+  repack_out(x, w);
+  p[2 * i] = make_uint4(w[0], w[1], w[2], w[3]);
+  p[2 * i + 1] = make_uint4(w[4], w[5], w[6], w[7]);
+}
+
+struct Csr3 {
+  const uint32_t* rowptr[3];
+  const uint32_t* col[3];
+  const uint4* val[3];
+};
+
+// out[mat * n + row] = sum_e w[col_e] * v_e  (A.w, B.w, C.w in evaluation form,
+// groth16.cu:275-294).  One thread per (row, matrix).
+__global__ void k_spmv3(uint4* __restrict__ out, const uint4* __restrict__ w, Csr3 m, size_t n) {
+  const size_t row = blockIdx.x * (size_t)blockDim.x + threadIdx.x;
+  const int mat = blockIdx.y;
+  if (row >= n) return;
+  const uint32_t b = m.rowptr[mat][row], e = m.rowptr[mat][row + 1];
+  fr acc = fe_zero<FrP>();
+  for (uint32_t k = b; k < e; k++) acc = fadd(acc, fmul(ld_fr(w, m.col[mat][k]), ld_fr(m.val[mat], k)));
+  st_fr(out, (size_t)mat * n + row, acc);
+}
+
+// Row check (A.w)(B.w) = C.w for rows < nc (circuit.cuh:93-124).  With raw
+// Montgomery words fmul(a, b) = ab 2^251 and fmul(c, 2^256) = c 2^251.
+__global__ void k_check_rows(const uint4* __restrict__ abc, size_t n, size_t nc, uint32_t* __restrict__ bad) {
+  const size_t row = blockIdx.x * (size_t)blockDim.x + threadIdx.x;
+  if (row >= nc) return;
+  const uint32_t K256[8] = {0x4ffffffbu, 0xac96341cu, 0x9f60cd29u, 0x36fc7695u,
+                            0x7879462eu, 0x666ea36fu, 0x9a07df2fu, 0x0e0a77c1u};
+  fr lhs = fmul(ld_fr(abc, row), ld_fr(abc, n + row));
+  fr rhs = fmul(ld_fr(abc, 2 * n + row), repack_in<FrP>(K256));
+  if (!feq(lhs, rhs)) atomicAdd(bad, 1u);
+}
+
+// Montgomery words (R = 2^256) -> standard form, in place.  fmul(x 2^256, 32)
+// in the internal radix 2^261 gives x.
+template <class P>
+__global__ void k_mont_to_std(uint4* __restrict__ p, size_t count) {
+  const size_t i = blockIdx.x * (size_t)blockDim.x + threadIdx.x;
+  if (i >= count) return;
+  uint4 a = p[2 * i], b = p[2 * i + 1];
+  uint32_t w[8] = {a.x, a.y, a.z, a.w, b.x, b.y, b.z, b.w};
+  fe<P> k32 = fe_zero<P>();
+  k32.l[0] = 32;
+  repack_out(fmul(repack_in<P>(w), k32), w);
+  p[2 * i] = make_uint4(w[0], w[1], w[2], w[3]);
+  p[2 * i + 1] = make_uint4(w[4], w[5], w[6], w[7]);
+}
+
+// ------------------------------------------------------------------ host helpers
+using zkh::Fq;
+using zkh::Fq2;
+using zkh::Fr;
+using zkh::G1;
+using zkh::G2;
+
+struct DevMem {
+  zk_context* ctx;
+  std::vector<void*> ptrs;
+  explicit DevMem(zk_context* c) : ctx(c) {}
+  ~DevMem() {
+    for (void* p : ptrs) (void)hipFree(p);
+  }
+  int alloc(void** p, size_t bytes) {
+    if (hipMalloc(p, bytes ? bytes : 1) != hipSuccess) return ctx->fail(ZK_ERR_OOM, "device allocation failed");
+    ptrs.push_back(*p);
+    return ZK_OK;
+  }
+};
+
+G1 g1_from_words(const uint64_t* w) {
+  bool inf = true;
+  for (int i = 0; i < 8; i++) inf = inf && w[i] == 0;
+  if (inf) return G1::inf();
+  return G1::affine(Fq::raw(w), Fq::raw(w + 4));
+}
+G2 g2_from_words(const uint64_t* w) {
+  bool inf = true;
+  for (int i = 0; i < 16; i++) inf = inf && w[i] == 0;
+  if (inf) return G2::inf();
+  return G2::affine(Fq2{Fq::raw(w), Fq::raw(w + 4)}, Fq2{Fq::raw(w + 8), Fq::raw(w + 12)});
+}
+void g1_to_words(const G1& p, uint64_t* w) {
+  Fq x, y;
+  memset(w, 0, 64);
+  if (!p.to_affine(x, y)) return;
+  memcpy(w, x.v, 32);
+  memcpy(w + 4, y.v, 32);
+}
+void g2_to_words(const G2& p, uint64_t* w) {
+  Fq2 x, y;
+  memset(w, 0, 128);
+  if (!p.to_affine(x, y)) return;
+  memcpy(w, x.c0.v, 32);
+  memcpy(w + 4, x.c1.v, 32);
+  memcpy(w + 8, y.c0.v, 32);
+  memcpy(w + 12, y.c1.v, 32);
+}
+
+// Fr::from_uint(rng()) until nonzero (groth16.cu:48-58)
+Fr random_nonzero(std::mt19937_64& rng) {
+  Fr v = Fr::from_u64(rng());
+  while (v.is_zero()) v = Fr::from_u64(rng());
+  return v;
+}
+
+int log2_domain(int nc) {  // QAP::from_r1cs, groth16.cu:225-242
+  int log_n = 0, n = 1;
+  while (n < nc) {
+    n <<= 1;
+    log_n++;
+  }
+  if (n < 4) log_n = 2;
+  return log_n;
+}
+
+// Coset shift: 5 unless 5^n = 1, then 7 (groth16.cu:329-342).  Returns g and
+// (g^n - 1)^-1 in Montgomery words.
+uint64_t coset_shift(int log_n, Fr& zinv) {
+  for (uint64_t g : {5ull, 7ull}) {
+    Fr z = Fr::from_u64(g);
+    for (int i = 0; i < log_n; i++) z = z.sqr();
+    z = z - Fr::one();
+    if (!z.is_zero()) {
+      zinv = z.inv();
+      return g;
+    }
+  }
+  zinv = Fr::zero();
+  return 0;
+}
+
+int quotient_run(zk_context* ctx, const zk_r1cs* c, const void* d_w, void* d_h, void* d_abc, hipStream_t st,
+                 bool check, uint32_t* d_bad) {
+  const size_t n = c->n;
+  Csr3 m;
+  for (int k = 0; k < 3; k++) {
+    m.rowptr[k] = c->rowptr[k];
+    m.col[k] = c->col[k];
+    m.val[k] = c->val[k];
+  }
+  ZK_LAUNCH(ctx, st, "quotient_spmv", k_spmv3, dim3(cdiv(n, 256), 3), dim3(256), 0, (uint4*)d_abc,
+            (const uint4*)d_w, m, n);
+  if (check) {
+    ZK_HIP(ctx, hipMemsetAsync(d_bad, 0, 4, st));
+    ZK_LAUNCH(ctx, st, "witness_check", k_check_rows, dim3(cdiv((size_t)c->nc, 256)), dim3(256), 0,
+              (const uint4*)d_abc, n, (size_t)c->nc, d_bad);
+  }
+  Fr zinv;
+  const uint64_t g = coset_shift(c->log_n, zinv);
+  if (!g) return ctx->fail(ZK_ERR_INVALID, "no valid coset shift");
+  uint4* abc = (uint4*)d_abc;
+  // 3 iNTT -> coefficients; 3 coset NTT -> evaluations on g*H (groth16.cu:321-363)
+  ZK_TRY(ntt_run(ctx, abc, abc, c->log_n, 1, 3, 0, st));
+  ZK_TRY(ntt_run(ctx, abc, abc, c->log_n, 0, 3, g, st));
+  ZK_TRY(quotient_pointwise(ctx, d_h, abc, abc + 2 * n, abc + 4 * n, n, zinv.v, st));
+  // coset iNTT: h_i = iNTT(H)_i g^-i (groth16.cu:372-383)
+  ZK_TRY(ntt_run(ctx, d_h, d_h, c->log_n, 1, 1, g, st));
+  return ZK_OK;
+}
+
+// ------------------------------------------------------------------ ZKMLPK3
+struct FileBuf {
+  std::vector<uint8_t> d;
+  size_t off = 0;
+  bool ok = true;
+  bool read(const char* path) {
+    FILE* f = fopen(path, "rb");
+    if (!f) return false;
+    fseek(f, 0, SEEK_END);
+    long sz = ftell(f);
+    fseek(f, 0, SEEK_SET);
+    if (sz < 0) {
+      fclose(f);
+      return false;
+    }
+    d.resize((size_t)sz);
+    ok = fread(d.data(), 1, d.size(), f) == d.size();
+    fclose(f);
+    return ok;
+  }
+  bool take(void* p, size_t n) {
+    if (!ok || off + n > d.size()) return ok = false;
+    memcpy(p, d.data() + off, n);
+    off += n;
+    return true;
+  }
+  int32_t i32() {
+    int32_t v = 0;
+    take(&v, 4);
+    return v;
+  }
+};
+
+// One record: u8 infinity + `coords` standard-form 32-byte coordinates.
+void parse_point(FileBuf& f, int coords, uint64_t* std_out, uint8_t* flag) {
+  uint8_t inf = 0;
+  f.take(&inf, 1);
+  f.take(std_out, 32 * coords);
+  *flag = inf;
+}
+
+void fixed_g1(const uint64_t* s, uint8_t inf, uint64_t* w) {
+  memset(w, 0, 64);
+  if (inf) return;
+  Fq x = Fq::from_std(s), y = Fq::from_std(s + 4);
+  memcpy(w, x.v, 32);
+  memcpy(w + 4, y.v, 32);
+}
+void fixed_g2(const uint64_t* s, uint8_t inf, uint64_t* w) {
+  memset(w, 0, 128);
+  if (inf) return;
+  for (int k = 0; k < 4; k++) {
+    Fq v = Fq::from_std(s + 4 * k);
+    memcpy(w + 4 * k, v.v, 32);
+  }
+}
+
+int upload_query(zk_context* ctx, FileBuf& f, bool g2, size_t count, void** d_recs) {
+  const int coords = g2 ? 4 : 2;
+  std::vector<uint64_t> std_words(count * coords * 4);
+  std::vector<uint8_t> flags(count);
+  for (size_t i = 0; i < count; i++) parse_point(f, coords, &std_words[i * coords * 4], &flags[i]);
+  if (!f.ok) return ctx->fail(ZK_ERR_IO, "proving key truncated");
+  void *d_std = nullptr, *d_flags = nullptr;
+  if (hipMalloc(d_recs, std::max<size_t>(count, 1) * rec_bytes(g2)) != hipSuccess)
+    return ctx->fail(ZK_ERR_OOM, "proving key allocation failed");
+  if (count == 0) return ZK_OK;
+  DevMem tmp(ctx);
+  ZK_TRY(tmp.alloc(&d_std, std_words.size() * 8));
+  ZK_TRY(tmp.alloc(&d_flags, count));
+  ZK_HIP(ctx, hipMemcpyAsync(d_std, std_words.data(), std_words.size() * 8, hipMemcpyHostToDevice, ctx->stream));
+  ZK_HIP(ctx, hipMemcpyAsync(d_flags, flags.data(), count, hipMemcpyHostToDevice, ctx->stream));
+  ZK_TRY(recs_from_std(ctx, g2, *d_recs, d_std, d_flags, count, ctx->stream));
+  ZK_HIP(ctx, hipStreamSynchronize(ctx->stream));
+  return ZK_OK;
+}
+
+void skip_query(FileBuf& f, bool g2, size_t count) {
+  const size_t rec = g2 ? 129 : 65;
+  if (f.off + rec * count > f.d.size()) f.ok = false;
+  else f.off += rec * count;
+}
+
+// ------------------------------------------------------------------ file writers
+struct Bytes {
+  std::vector<uint8_t> b;
+  void u32(uint32_t v) { b.insert(b.end(), (uint8_t*)&v, (uint8_t*)&v + 4); }
+  void raw(const void* p, size_t n) { b.insert(b.end(), (const uint8_t*)p, (const uint8_t*)p + n); }
+  bool write(const char* path) const {
+    FILE* f = fopen(path, "wb");
+    if (!f) return false;
+    bool ok = fwrite(b.data(), 1, b.size(), f) == b.size();
+    return fclose(f) == 0 && ok;
+  }
+};
+
+void put_std(Bytes& o, const Fq& v) {
+  uint64_t s[4];
+  v.to_std(s);
+  o.raw(s, 32);
+}
+void put_g1_rec(Bytes& o, const G1& p) {
+  Fq x, y;
+  uint8_t inf = p.to_affine(x, y) ? 0 : 1;
+  o.raw(&inf, 1);
+  put_std(o, x);
+  put_std(o, y);
+}
+void put_g2_rec(Bytes& o, const G2& p) {
+  Fq2 x, y;
+  uint8_t inf = p.to_affine(x, y) ? 0 : 1;
+  o.raw(&inf, 1);
+  put_std(o, x.c0);
+  put_std(o, x.c1);
+  put_std(o, y.c0);
+  put_std(o, y.c1);
+}
+
+// Points generated on the device (standard-form words after k_mont_to_std)
+// appended as ZKMLPK3 records.
+void put_std_points(Bytes& o, const std::vector<uint64_t>& w, size_t count, int coords) {
+  for (size_t i = 0; i < count; i++) {
+    const uint64_t* p = &w[i * coords * 4];
+    bool inf = true;
+    for (int k = 0; k < coords * 4; k++) inf = inf && p[k] == 0;
+    uint8_t f = inf ? 1 : 0;
+    o.raw(&f, 1);
+    o.raw(p, 32 * coords);
+  }
+}
+
+// k_i * G on the device for a host vector of Fr scalars; returns
+// standard-form coordinates (zeros at infinity).
+int gen_points_std(zk_context* ctx, const std::vector<Fr>& k, bool g2, std::vector<uint64_t>& out) {
+  const size_t n = k.size();
+  const int words = g2 ? 16 : 8;
+  out.assign(n * words, 0);
+  if (n == 0) return ZK_OK;
+  DevMem tmp(ctx);
+  void *d_k = nullptr, *d_p = nullptr;
+  ZK_TRY(tmp.alloc(&d_k, n * 32));
+  ZK_TRY(tmp.alloc(&d_p, n * words * 8));
+  ZK_HIP(ctx, hipMemcpyAsync(d_k, k.data(), n * 32, hipMemcpyHostToDevice, ctx->stream));
+  if (g2) ZK_TRY(g2_generator_mul(ctx, d_k, n, d_p, ctx->stream));
+  else ZK_TRY(g1_generator_mul(ctx, d_k, n, d_p, ctx->stream));
+  const size_t elems = n * words / 4;
+  ZK_LAUNCH(ctx, ctx->stream, "pk_convert", k_mont_to_std<FqP>, dim3(cdiv(elems, 256)), dim3(256), 0,
+            (uint4*)d_p, elems);
+  ZK_HIP(ctx, hipMemcpyAsync(out.data(), d_p, n * words * 8, hipMemcpyDeviceToHost, ctx->stream));
+  ZK_HIP(ctx, hipStreamSynchronize(ctx->stream));
+  // the point at infinity comes out as x = y = 0 in either form
+  return ZK_OK;
+}
+
+}  // namespace
+
+// ======================================================================
+extern "C" {
+
+int zk_r1cs_create(zk_context* ctx, int num_constraints, int num_variables, int num_public,
+                   const zk_sparse_entry* A, size_t nA, const zk_sparse_entry* B, size_t nB,
+                   const zk_sparse_entry* C, size_t nC, zk_r1cs** out) {
+  if (!ctx || !out) return ZK_ERR_INVALID;
+  *out = nullptr;
+  if (num_constraints < 0 || num_variables <= 0 || num_public < 0 || num_public + 1 > num_variables)
+    return ctx->fail(ZK_ERR_INVALID, "r1cs: bad sizes");
+  if ((nA && !A) || (nB && !B) || (nC && !C)) return ctx->fail(ZK_ERR_INVALID, "r1cs: null matrix");
+  const int log_n = log2_domain(num_constraints);
+  if (log_n > 24) return ctx->fail(ZK_ERR_SIZE, "r1cs: domain above 2^24");
+  zk_r1cs* c = new zk_r1cs();
+  c->nc = num_constraints;
+  c->nv = num_variables;
+  c->npub = num_public;
+  c->log_n = log_n;
+  c->n = (size_t)1 << log_n;
+  const zk_sparse_entry* mats[3] = {A, B, C};
+  const size_t cnts[3] = {nA, nB, nC};
+  int st = ZK_OK;
+  for (int k = 0; k < 3 && st == ZK_OK; k++) {
+    c->coo[k].assign(mats[k], mats[k] + cnts[k]);
+    // CSR over rows < n; entries outside [0, n) x [0, m) are dropped as in
+    // compute_h (groth16.cu:282-293)
+    std::vector<uint32_t> rowptr(c->n + 1, 0);
+    for (size_t i = 0; i < cnts[k]; i++) {
+      const zk_sparse_entry& e = mats[k][i];
+      if (e.row >= 0 && (size_t)e.row < c->n && e.col >= 0 && e.col < num_variables) rowptr[e.row + 1]++;
+    }
+    for (size_t r = 0; r < c->n; r++) rowptr[r + 1] += rowptr[r];
+    const size_t nnz = rowptr[c->n];
+    std::vector<uint32_t> fill(rowptr.begin(), rowptr.end() - 1), col(nnz);
+    std::vector<uint64_t> val(nnz * 4);
+    for (size_t i = 0; i < cnts[k]; i++) {
+      const zk_sparse_entry& e = mats[k][i];
+      if (!(e.row >= 0 && (size_t)e.row < c->n && e.col >= 0 && e.col < num_variables)) continue;
+      const uint32_t p = fill[e.row]++;
+      col[p] = (uint32_t)e.col;
+      Fr v = Fr::raw(e.value);
+      for (int d = 0; d < 5; d++) v = v.dbl();  // x 32
+      memcpy(&val[(size_t)p * 4], v.v, 32);
+    }
+    c->nnz[k] = nnz;
+    if (hipMalloc(&c->rowptr[k], rowptr.size() * 4) != hipSuccess ||
+        hipMalloc(&c->col[k], std::max<size_t>(nnz, 1) * 4) != hipSuccess ||
+        hipMalloc(&c->val[k], std::max<size_t>(nnz, 1) * 32) != hipSuccess) {
+      st = ctx->fail(ZK_ERR_OOM, "r1cs allocation failed");
+      break;
+    }
+    if (hipMemcpy(c->rowptr[k], rowptr.data(), rowptr.size() * 4, hipMemcpyHostToDevice) != hipSuccess ||
+        (nnz && hipMemcpy(c->col[k], col.data(), nnz * 4, hipMemcpyHostToDevice) != hipSuccess) ||
+        (nnz && hipMemcpy(c->val[k], val.data(), nnz * 32, hipMemcpyHostToDevice) != hipSuccess))
+      st = ctx->fail(ZK_ERR_HIP, "r1cs upload failed");
+  }
+  if (st != ZK_OK) {
+    zk_r1cs_destroy(c);
+    return st;
+  }
+  *out = c;
+  return ZK_OK;
+}
+
+void zk_r1cs_destroy(zk_r1cs* c) {
+  if (!c) return;
+  for (int k = 0; k < 3; k++) {
+    if (c->rowptr[k]) (void)hipFree(c->rowptr[k]);
+    if (c->col[k]) (void)hipFree(c->col[k]);
+    if (c->val[k]) (void)hipFree(c->val[k]);
+  }
+  delete c;
+}
+
+int zk_r1cs_domain(const zk_r1cs* c, int* log_n) {
+  if (!c || !log_n) return ZK_ERR_INVALID;
+  *log_n = c->log_n;
+  return ZK_OK;
+}
+
+int zk_quotient_h(zk_context* ctx, const zk_r1cs* c, const void* d_witness, size_t m, void* d_h, void* stream) {
+  if (!ctx || !c || !d_witness || !d_h) return ZK_ERR_INVALID;
+  if (m != (size_t)c->nv) return ctx->fail(ZK_ERR_MISMATCH, "quotient: witness length != num_variables");
+  ZK_TRY(ctx->ensure(ctx->scratch_b, c->n * 32 * 3));
+  return quotient_run(ctx, c, d_witness, d_h, ctx->scratch_b.p, ctx->s(stream), false, nullptr);
+}
+
+int zk_pk_load(zk_context* ctx, const char* path, zk_pk** out) {
+  if (!ctx || !path || !out) return ZK_ERR_INVALID;
+  *out = nullptr;
+  FileBuf f;
+  if (!f.read(path)) return ctx->fail(ZK_ERR_IO, "cannot read proving key", path);
+  char magic[8] = {0};
+  f.take(magic, 8);
+  if (!f.ok || memcmp(magic, "ZKMLPK3", 7) != 0) return ctx->fail(ZK_ERR_IO, "not a ZKMLPK3 proving key", path);
+  uint32_t ver = 0;
+  f.take(&ver, 4);
+  if (!f.ok || ver != 3) return ctx->fail(ZK_ERR_IO, "unsupported proving-key version");
+  zk_pk* pk = new zk_pk();
+  pk->n = f.i32();
+  pk->m = f.i32();
+  pk->npub = f.i32();
+  if (!f.ok || pk->n < 0 || pk->m <= 0 || pk->npub < 0) {
+    delete pk;
+    return ctx->fail(ZK_ERR_IO, "invalid proving-key metadata");
+  }
+  uint64_t s[16];
+  uint8_t inf;
+  parse_point(f, 2, s, &inf);
+  fixed_g1(s, inf, pk->alpha1);
+  parse_point(f, 2, s, &inf);
+  fixed_g1(s, inf, pk->beta1);
+  parse_point(f, 2, s, &inf);
+  fixed_g1(s, inf, pk->delta1);
+  parse_point(f, 4, s, &inf);
+  fixed_g2(s, inf, pk->beta2);
+  parse_point(f, 4, s, &inf);
+  fixed_g2(s, inf, pk->gamma2);
+  parse_point(f, 4, s, &inf);
+  fixed_g2(s, inf, pk->delta2);
+  int st = ZK_OK;
+  auto count = [&](size_t& dst) {
+    int32_t k = f.i32();
+    if (!f.ok || k < 0 || k > (1 << 28)) {
+      f.ok = false;
+      return false;
+    }
+    dst = (size_t)k;
+    return true;
+  };
+  // tau powers (not used by prove), then A, B1, B2, L, H
+  if (count(pk->ntau1)) skip_query(f, false, pk->ntau1);
+  if (f.ok && count(pk->ntau2)) skip_query(f, true, pk->ntau2);
+  if (f.ok && count(pk->nA)) st = upload_query(ctx, f, false, pk->nA, &pk->A);
+  if (st == ZK_OK && f.ok && count(pk->nB1)) st = upload_query(ctx, f, false, pk->nB1, &pk->B1);
+  if (st == ZK_OK && f.ok && count(pk->nB2)) st = upload_query(ctx, f, true, pk->nB2, &pk->B2);
+  if (st == ZK_OK && f.ok && count(pk->nL)) st = upload_query(ctx, f, false, pk->nL, &pk->L);
+  if (st == ZK_OK && f.ok && count(pk->nH)) st = upload_query(ctx, f, false, pk->nH, &pk->H);
+  if (st == ZK_OK && !f.ok) st = ctx->fail(ZK_ERR_IO, "proving key truncated or malformed");
+  if (st == ZK_OK && ((int)pk->nA < pk->m || (int)pk->nB1 < pk->m || (int)pk->nB2 < pk->m))
+    st = ctx->fail(ZK_ERR_IO, "incomplete proving key (A/B queries shorter than num_variables)");
+  if (st != ZK_OK) {
+    zk_pk_destroy(pk);
+    return st;
+  }
+  *out = pk;
+  return ZK_OK;
+}
+
+void zk_pk_destroy(zk_pk* pk) {
+  if (!pk) return;
+  for (void* p : {pk->A, pk->B1, pk->B2, pk->L, pk->H})
+    if (p) (void)hipFree(p);
+  delete pk;
+}
+
+int zk_pk_info(const zk_pk* pk, int* n, int* m, int* npub) {
+  if (!pk) return ZK_ERR_INVALID;
+  if (n) *n = pk->n;
+  if (m) *m = pk->m;
+  if (npub) *npub = pk->npub;
+  return ZK_OK;
+}
+
+int zk_prove(zk_context* ctx, const zk_pk* pk, const zk_r1cs* c, const void* h_witness, size_t m, int num_public,
+             uint64_t blind_seed, int check_witness, uint8_t proof_out[256], double* timings) {
+  if (!ctx || !pk || !c || !proof_out || (m && !h_witness)) return ZK_ERR_INVALID;
+  hipEvent_t ev[8];
+  for (auto& e : ev) ZK_HIP(ctx, hipEventCreate(&e));
+  struct EvGuard {
+    hipEvent_t* e;
+    ~EvGuard() {
+      for (int i = 0; i < 8; i++) (void)hipEventDestroy(e[i]);
+    }
+  } guard{ev};
+  hipStream_t st = ctx->stream;
+  // preconditions (groth16.cu:665-697)
+  if (m == 0) return ctx->fail(ZK_ERR_MISMATCH, "empty witness");
+  if ((int)m != c->nv) return ctx->fail(ZK_ERR_MISMATCH, "witness size != circuit variables");
+  if (num_public != pk->npub) return ctx->fail(ZK_ERR_MISMATCH, "witness public count != proving key");
+  if ((size_t)(1 + pk->npub) > m) return ctx->fail(ZK_ERR_MISMATCH, "public inputs exceed witness");
+  const size_t n = c->n;
+  ZK_TRY(ctx->ensure(ctx->scratch_b, n * 32 * 3));
+  ZK_TRY(ctx->ensure(ctx->scratch_c, n * 32 + m * 32 + 64));
+  uint8_t* base = (uint8_t*)ctx->scratch_c.p;
+  void* d_h = base;
+  void* d_w = base + n * 32;
+  uint32_t* d_bad = (uint32_t*)(base + n * 32 + m * 32);
+  ZK_HIP(ctx, hipEventRecord(ev[0], st));
+  ZK_HIP(ctx, hipMemcpyAsync(d_w, h_witness, m * 32, hipMemcpyHostToDevice, st));
+  ZK_TRY(quotient_run(ctx, c, d_w, d_h, ctx->scratch_b.p, st, check_witness != 0, d_bad));
+  if (check_witness) {
+    uint32_t bad = 0;
+    ZK_HIP(ctx, hipMemcpyAsync(&bad, d_bad, 4, hipMemcpyDeviceToHost, st));
+    ZK_HIP(ctx, hipStreamSynchronize(st));
+    if (bad) return ctx->fail(ZK_ERR_WITNESS, "witness does not satisfy the R1CS");
+  }
+  ZK_HIP(ctx, hipEventRecord(ev[1], st));
+  // blinding factors (groth16.cu:708-718)
+  std::mt19937_64 rng(blind_seed);
+  Fr r = random_nonzero(rng);
+  Fr s = random_nonzero(rng);
+  const uint8_t* w8 = (const uint8_t*)d_w;
+  uint64_t a_msm[8], b2_msm[16], l_msm[8], h_msm[8], b1_msm[8];
+  const size_t na = std::min(m, pk->nA);
+  ZK_TRY(msm_g1_recs(ctx, pk->A, d_w, na, a_msm, st));
+  ZK_HIP(ctx, hipEventRecord(ev[2], st));
+  const size_t nb2 = std::min(m, pk->nB2);
+  ZK_TRY(msm_g2_recs(ctx, pk->B2, d_w, nb2, b2_msm, st));
+  ZK_HIP(ctx, hipEventRecord(ev[3], st));
+  const long npriv_l = std::min<long>((long)pk->nL, (long)m - 1 - pk->npub);
+  if (npriv_l > 0) ZK_TRY(msm_g1_recs(ctx, pk->L, w8 + 32 * (1 + pk->npub), (size_t)npriv_l, l_msm, st));
+  else memset(l_msm, 0, 64);
+  ZK_HIP(ctx, hipEventRecord(ev[4], st));
+  const size_t nh = std::min(n, pk->nH);
+  ZK_TRY(msm_g1_recs(ctx, pk->H, d_h, nh, h_msm, st));
+  ZK_HIP(ctx, hipEventRecord(ev[5], st));
+  const size_t nb1 = std::min(m, pk->nB1);
+  ZK_TRY(msm_g1_recs(ctx, pk->B1, d_w, nb1, b1_msm, st));
+  ZK_HIP(ctx, hipEventRecord(ev[6], st));
+  ZK_HIP(ctx, hipEventSynchronize(ev[6]));
+  // host assembly (groth16.cu:769-840): C = L + H + s A + r (beta1 + B1)
+  G1 A = g1_from_words(pk->alpha1).add(na > 0 ? g1_from_words(a_msm) : G1::inf());
+  A = A.add(g1_from_words(pk->delta1).mul(r));
+  G2 B = g2_from_words(pk->beta2).add(nb2 > 0 ? g2_from_words(b2_msm) : G2::inf());
+  B = B.add(g2_from_words(pk->delta2).mul(s));
+  uint64_t Aw[8], Bw[16], Cw[8];
+  g1_to_words(A, Aw);
+  g2_to_words(B, Bw);
+  G1 Cj = G1::inf();
+  if (npriv_l > 0) Cj = Cj.add(g1_from_words(l_msm));
+  if (nh > 0) Cj = Cj.add(g1_from_words(h_msm));
+  Cj = Cj.add(g1_from_words(Aw).mul(s));
+  if (nb1 > 0) Cj = Cj.add(g1_from_words(pk->beta1).add(g1_from_words(b1_msm)).mul(r));
+  g1_to_words(Cj, Cw);
+  // 256-byte serialization in standard form (groth16.cu:1058-1074)
+  uint8_t* o = proof_out;
+  auto put = [&](const uint64_t* mont) {
+    uint64_t sdt[4];
+    Fq::raw(mont).to_std(sdt);
+    memcpy(o, sdt, 32);
+    o += 32;
+  };
+  put(Aw);
+  put(Aw + 4);
+  put(Bw);
+  put(Bw + 4);
+  put(Bw + 8);
+  put(Bw + 12);
+  put(Cw);
+  put(Cw + 4);
+  ZK_HIP(ctx, hipEventRecord(ev[7], st));
+  ZK_HIP(ctx, hipEventSynchronize(ev[7]));
+  if (timings) {
+    float t[8] = {0};
+    for (int i = 1; i < 8; i++) (void)hipEventElapsedTime(&t[i], ev[i - 1], ev[i]);
+    float total = 0;
+    (void)hipEventElapsedTime(&total, ev[0], ev[7]);
+    timings[0] = total;  // total
+    timings[1] = t[1];   // quotient (incl. witness upload / check)
+    timings[2] = t[2];   // A  (G1 MSM, m)
+    timings[3] = t[3];   // B  (G2 MSM, m)
+    timings[4] = t[4];   // L  (G1 MSM, m - npub - 1)
+    timings[5] = t[5];   // H  (G1 MSM, n)
+    timings[6] = t[6];   // B1 (G1 MSM, m)
+    timings[7] = t[7];   // host assembly
+  }
+  return ZK_OK;
+}
+
+int zk_setup(zk_context* ctx, const zk_r1cs* c, uint64_t toxic_seed, const char* pk_path, const char* vk_path) {
+  if (!ctx || !c || !pk_path || !vk_path) return ZK_ERR_INVALID;
+  const int log_n = c->log_n;
+  const size_t n = c->n, m = c->nv;
+  const int npub = c->npub;
+  // toxic waste (groth16.cu:456-472)
+  std::mt19937_64 rng(toxic_seed);
+  Fr tau = random_nonzero(rng), alpha = random_nonzero(rng), beta = random_nonzero(rng);
+  Fr gamma = random_nonzero(rng), delta = random_nonzero(rng);
+  // Lagrange basis at tau and QAP columns (groth16.cu:97-189)
+  static const uint64_t W28[4] = {0x636E735580D13D9CULL, 0xA22BF3742445FFD6ULL, 0x56452AC01EB203D8ULL,
+                                  0x1860EF942963F9E7ULL};
+  Fr w = Fr::raw(W28);
+  for (int i = 0; i < 28 - log_n; i++) w = w.sqr();
+  Fr tn = tau;
+  for (int i = 0; i < log_n; i++) tn = tn.sqr();
+  const Fr vanish = tn - Fr::one();
+  Fr two_inv = Fr::from_u64(2).inv(), ninv = Fr::one();
+  for (int i = 0; i < log_n; i++) ninv = ninv * two_inv;
+  std::vector<Fr> Lt(n), den(n), pre(n);
+  Fr wj = Fr::one();
+  for (size_t j = 0; j < n; j++) {
+    Lt[j] = vanish * wj * ninv;
+    den[j] = tau - wj;
+    wj = wj * w;
+  }
+  pre[0] = den[0];
+  for (size_t i = 1; i < n; i++) pre[i] = pre[i - 1] * den[i];
+  Fr ti = pre[n - 1].inv();
+  for (size_t i = n - 1; i > 0; i--) {
+    Fr di = pre[i - 1] * ti;
+    ti = ti * den[i];
+    Lt[i] = Lt[i] * di;
+  }
+  Lt[0] = Lt[0] * ti;
+  std::vector<Fr> At(m, Fr::zero()), Bt(m, Fr::zero()), Ct(m, Fr::zero());
+  std::vector<Fr>* cols[3] = {&At, &Bt, &Ct};
+  for (int k = 0; k < 3; k++)
+    for (const zk_sparse_entry& e : c->coo[k])
+      if (e.row >= 0 && (size_t)e.row < n && e.col >= 0 && (size_t)e.col < m)
+        (*cols[k])[e.col] = (*cols[k])[e.col] + Fr::raw(e.value) * Lt[e.row];
+  Lt.clear();
+  den.clear();
+  pre.clear();
+  // query scalars (groth16.cu:540-606)
+  const Fr dinv = delta.inv(), ginv = gamma.inv();
+  long l = (long)m - npub - 1;
+  if (l < 0) l = 0;
+  std::vector<Fr> ls((size_t)l);
+  for (long i = 0; i < l; i++) {
+    const size_t v = (size_t)i + 1 + npub;
+    ls[i] = (beta * At[v] + alpha * Bt[v] + Ct[v]) * dinv;
+  }
+  std::vector<Fr> hs(n);
+  Fr tp = vanish * dinv;
+  for (size_t i = 0; i < n; i++) {
+    hs[i] = tp;
+    tp = tp * tau;
+  }
+  std::vector<Fr> ic(npub + 1);
+  for (int i = 0; i <= npub; i++)
+    ic[i] = (size_t)i < m ? (beta * At[i] + alpha * Bt[i] + Ct[i]) * ginv : Fr::zero();
+  // group elements: fixed points on the host, queries on the device
+  const G1 g1 = G1::affine(Fq::from_u64(1), Fq::from_u64(2));
+  std::vector<uint64_t> gen2_std;
+  ZK_TRY(gen_points_std(ctx, std::vector<Fr>{Fr::one()}, true, gen2_std));
+  const G2 g2 = G2::affine(Fq2{Fq::from_std(&gen2_std[0]), Fq::from_std(&gen2_std[4])},
+                           Fq2{Fq::from_std(&gen2_std[8]), Fq::from_std(&gen2_std[12])});
+  std::vector<uint64_t> qa, qb1, qb2, ql, qh, qic;
+  ZK_TRY(gen_points_std(ctx, At, false, qa));
+  ZK_TRY(gen_points_std(ctx, Bt, false, qb1));
+  ZK_TRY(gen_points_std(ctx, Bt, true, qb2));
+  ZK_TRY(gen_points_std(ctx, ls, false, ql));
+  ZK_TRY(gen_points_std(ctx, hs, false, qh));
+  ZK_TRY(gen_points_std(ctx, ic, false, qic));
+  // ZKMLPK3 (groth16.cu:1104-1188)
+  Bytes pkb;
+  const char magic[8] = {'Z', 'K', 'M', 'L', 'P', 'K', '3', 0};
+  pkb.raw(magic, 8);
+  pkb.u32(3);
+  pkb.u32((uint32_t)n);
+  pkb.u32((uint32_t)m);
+  pkb.u32((uint32_t)npub);
+  const G1 alpha1 = g1.mul(alpha), beta1 = g1.mul(beta), delta1 = g1.mul(delta);
+  const G2 beta2 = g2.mul(beta), gamma2 = g2.mul(gamma), delta2 = g2.mul(delta);
+  put_g1_rec(pkb, alpha1);
+  put_g1_rec(pkb, beta1);
+  put_g1_rec(pkb, delta1);
+  put_g2_rec(pkb, beta2);
+  put_g2_rec(pkb, gamma2);
+  put_g2_rec(pkb, delta2);
+  pkb.u32(0);  // tau powers in G1: empty
+  pkb.u32(2);  // tau powers in G2: [G2, tau G2]
+  put_g2_rec(pkb, g2);
+  put_g2_rec(pkb, g2.mul(tau));
+  pkb.u32((uint32_t)m);
+  put_std_points(pkb, qa, m, 2);
+  pkb.u32((uint32_t)m);
+  put_std_points(pkb, qb1, m, 2);
+  pkb.u32((uint32_t)m);
+  put_std_points(pkb, qb2, m, 4);
+  pkb.u32((uint32_t)l);
+  put_std_points(pkb, ql, (size_t)l, 2);
+  pkb.u32((uint32_t)n);
+  put_std_points(pkb, qh, n, 2);
+  if (!pkb.write(pk_path)) return ctx->fail(ZK_ERR_IO, "cannot write proving key", pk_path);
+  // verification key (verifier.cu:103-148): no infinity flags
+  Bytes vkb;
+  vkb.u32((uint32_t)npub);
+  auto put_aff_g1 = [&](const G1& p) {
+    Fq x, y;
+    p.to_affine(x, y);
+    put_std(vkb, x);
+    put_std(vkb, y);
+  };
+  auto put_aff_g2 = [&](const G2& p) {
+    Fq2 x, y;
+    p.to_affine(x, y);
+    put_std(vkb, x.c0);
+    put_std(vkb, x.c1);
+    put_std(vkb, y.c0);
+    put_std(vkb, y.c1);
+  };
+  put_aff_g1(alpha1);
+  put_aff_g2(beta2);
+  put_aff_g2(gamma2);
+  put_aff_g2(delta2);
+  vkb.u32((uint32_t)(npub + 1));
+  for (int i = 0; i <= npub; i++) vkb.raw(&qic[(size_t)i * 8], 64);
+  if (!vkb.write(vk_path)) return ctx->fail(ZK_ERR_IO, "cannot write verification key", vk_path);
+  return ZK_OK;
+}
+
+}  // extern "C"

@@ -109,6 +109,14 @@ __device__ __forceinline__ void ext_to_coord(const uint32_t* e, fq2& a) {
   a.c1 = from_mont256<FqP>(e + 8);
 }
 
+__device__ __forceinline__ void std_to_coord(const uint32_t* e, fq& a) { a = from_std<FqP>(e); }
+__device__ __forceinline__ void std_to_coord(const uint32_t* e, fq2& a) {
+  a.c0 = from_std<FqP>(e);
+  a.c1 = from_std<FqP>(e + 8);
+}
+__device__ __forceinline__ fq fcanon_coord(const fq& a) { return fcanon(a); }
+__device__ __forceinline__ fq2 fcanon_coord(const fq2& a) { return fq2{fcanon(a.c0), fcanon(a.c1)}; }
+
 template <class F>
 __global__ void k_msm_convert(uint4* __restrict__ recs, const uint32_t* __restrict__ ext, size_t n) {
   size_t i = blockIdx.x * (size_t)blockDim.x + threadIdx.x;
@@ -479,25 +487,20 @@ static void host_finish(const std::vector<xyzz<F>>& parts, int W, int per_w, int
   HostSide<F>::out(ax, ay, out);
 }
 
+// MSM over prepared point records (internal form, see Rec<F>).  `recs` may be
+// the workspace's own conversion buffer or a proving key's resident queries.
 template <class F>
-static int msm_run(zk_context* ctx, MsmWorkspace*& wsp, const void* d_points, const void* d_scalars, size_t n,
-                   uint64_t* out, hipStream_t st) {
+static int msm_run_recs(zk_context* ctx, MsmWorkspace& ws, const uint4* recs, const void* d_scalars, size_t n,
+                        uint64_t* out, hipStream_t st) {
   constexpr int OUTW = sizeof(F) == sizeof(fq) ? 8 : 16;
   memset(out, 0, OUTW * 8);
   if (n == 0) return ZK_OK;
-  if (!d_points || !d_scalars) return ctx->fail(ZK_ERR_INVALID, "msm: null buffer");
-  if (n > (1u << 28)) return ctx->fail(ZK_ERR_SIZE, "msm: n above 2^28");
-  if (!wsp) wsp = new MsmWorkspace();
-  MsmWorkspace& ws = *wsp;
   const int c = choose_c(n);
   const int W = (254 + c - 1) / c;
   const size_t total = (size_t)W * n;
   const size_t nkeys = ((size_t)W + 1) << c;
   const size_t nbuckets = (size_t)W << (c - 1);
   const uint32_t nchunks = (uint32_t)((total + MSM_L0 - 1) / MSM_L0);
-  constexpr int RW = Rec<F>::WORDS;
-
-  ZK_TRY(ctx->ensure(ws.recs, n * RW * 4));
   ZK_TRY(ctx->ensure(ws.keys_in, total * 4));
   ZK_TRY(ctx->ensure(ws.vals_in, total * 4));
   ZK_TRY(ctx->ensure(ws.keys_out, total * 4));
@@ -512,7 +515,6 @@ static int msm_run(zk_context* ctx, MsmWorkspace*& wsp, const void* d_points, co
   ZK_TRY(ctx->ensure(ws.tpt, (size_t)nchunks * sizeof(xyzz<F>)));
   if (!ws.h_stat) ZK_HIP(ctx, hipHostMalloc((void**)&ws.h_stat, 16, hipHostMallocDefault));
 
-  uint4* recs = (uint4*)ws.recs.p;
   uint32_t* kin = (uint32_t*)ws.keys_in.p;
   uint32_t* vin = (uint32_t*)ws.vals_in.p;
   uint32_t* kout = (uint32_t*)ws.keys_out.p;
@@ -522,8 +524,6 @@ static int msm_run(zk_context* ctx, MsmWorkspace*& wsp, const void* d_points, co
   uint32_t* stat = (uint32_t*)ws.stat.p;
   xyzz<F>* buckets = (xyzz<F>*)ws.buckets.p;
 
-  ZK_LAUNCH(ctx, st, "msm_convert", k_msm_convert<F>, dim3(cdiv(n, 256)), dim3(256), 0, recs,
-            (const uint32_t*)d_points, n);
   ZK_LAUNCH(ctx, st, "msm_digits", k_msm_digits, dim3(cdiv(n, 256)), dim3(256), 0, kin, vin,
             (const uint4*)d_scalars, n, c, W);
 
@@ -574,6 +574,22 @@ static int msm_run(zk_context* ctx, MsmWorkspace*& wsp, const void* d_points, co
   return ZK_OK;
 }
 
+template <class F>
+static int msm_run(zk_context* ctx, MsmWorkspace*& wsp, const void* d_points, const void* d_scalars, size_t n,
+                   uint64_t* out, hipStream_t st) {
+  constexpr int OUTW = sizeof(F) == sizeof(fq) ? 8 : 16;
+  memset(out, 0, OUTW * 8);
+  if (n == 0) return ZK_OK;
+  if (!d_points || !d_scalars) return ctx->fail(ZK_ERR_INVALID, "msm: null buffer");
+  if (n > (1u << 28)) return ctx->fail(ZK_ERR_SIZE, "msm: n above 2^28");
+  if (!wsp) wsp = new MsmWorkspace();
+  MsmWorkspace& ws = *wsp;
+  ZK_TRY(ctx->ensure(ws.recs, n * Rec<F>::WORDS * 4));
+  ZK_LAUNCH(ctx, st, "msm_convert", k_msm_convert<F>, dim3(cdiv(n, 256)), dim3(256), 0, (uint4*)ws.recs.p,
+            (const uint32_t*)d_points, n);
+  return msm_run_recs<F>(ctx, ws, (const uint4*)ws.recs.p, d_scalars, n, out, st);
+}
+
 int msm_g1_run(zk_context* ctx, const void* d_points, const void* d_scalars, size_t n, uint64_t out[8],
                hipStream_t st) {
   return msm_run<fq>(ctx, ctx->msm_ws, d_points, d_scalars, n, out, st);
@@ -583,6 +599,61 @@ int msm_g2_run(zk_context* ctx, const void* d_points, const void* d_scalars, siz
                hipStream_t st) {
   return msm_run<fq2>(ctx, ctx->msm_ws_g2, d_points, d_scalars, n, out, st);
 }
+
+int msm_g1_recs(zk_context* ctx, const void* d_recs, const void* d_scalars, size_t n, uint64_t out[8],
+                hipStream_t st) {
+  if (!ctx->msm_ws) ctx->msm_ws = new MsmWorkspace();
+  return msm_run_recs<fq>(ctx, *ctx->msm_ws, (const uint4*)d_recs, d_scalars, n, out, st);
+}
+
+int msm_g2_recs(zk_context* ctx, const void* d_recs, const void* d_scalars, size_t n, uint64_t out[16],
+                hipStream_t st) {
+  if (!ctx->msm_ws_g2) ctx->msm_ws_g2 = new MsmWorkspace();
+  return msm_run_recs<fq2>(ctx, *ctx->msm_ws_g2, (const uint4*)d_recs, d_scalars, n, out, st);
+}
+
+// Point records from standard-form coordinates (proving-key files store
+// x, y in standard form, src/prover/groth16.cu:1131-1150).  flags[i] != 0
+// marks the point at infinity.
+template <class F>
+__global__ void k_recs_from_std(uint4* __restrict__ recs, const uint32_t* __restrict__ std_words,
+                                const uint8_t* __restrict__ flags, size_t n) {
+  size_t i = blockIdx.x * (size_t)blockDim.x + threadIdx.x;
+  if (i >= n) return;
+  constexpr int EW = Rec<F>::EXT_WORDS, W = Rec<F>::WORDS, CW = coord_words<F>();
+  uint32_t e[EW];
+#pragma unroll
+  for (int k = 0; k < EW; k++) e[k] = std_words[i * EW + k];
+  const bool inf = flags[i] != 0;
+  uint32_t w[W];
+#pragma unroll
+  for (int k = 0; k < W; k++) w[k] = 0;
+  if (!inf) {
+    F x, y;
+    std_to_coord(e, x);
+    std_to_coord(e + EW / 2, y);
+    store_coord(w, fcanon_coord(x));
+    store_coord(w + CW, fcanon_coord(y));
+  }
+  w[2 * CW] = inf ? 1u : 0u;
+  uint4* p = recs + i * (W / 4);
+#pragma unroll
+  for (int k = 0; k < W / 4; k++) p[k] = make_uint4(w[4 * k], w[4 * k + 1], w[4 * k + 2], w[4 * k + 3]);
+}
+
+int recs_from_std(zk_context* ctx, bool g2, void* d_recs, const void* d_std, const void* d_flags, size_t n,
+                  hipStream_t st) {
+  if (n == 0) return ZK_OK;
+  if (g2)
+    ZK_LAUNCH(ctx, st, "pk_convert", k_recs_from_std<fq2>, dim3(cdiv(n, 256)), dim3(256), 0, (uint4*)d_recs,
+              (const uint32_t*)d_std, (const uint8_t*)d_flags, n);
+  else
+    ZK_LAUNCH(ctx, st, "pk_convert", k_recs_from_std<fq>, dim3(cdiv(n, 256)), dim3(256), 0, (uint4*)d_recs,
+              (const uint32_t*)d_std, (const uint8_t*)d_flags, n);
+  return ZK_OK;
+}
+
+size_t rec_bytes(bool g2) { return g2 ? Rec<fq2>::WORDS * 4 : Rec<fq>::WORDS * 4; }
 
 }  // namespace zk
 

@@ -106,6 +106,14 @@ int msm_g1_run(zk_context* ctx, const void* d_points, const void* d_scalars, siz
                hipStream_t st);
 int msm_g2_run(zk_context* ctx, const void* d_points, const void* d_scalars, size_t n, uint64_t out_affine[16],
                hipStream_t st);
+// MSM over prepared point records (proving-key queries stay in this form)
+int msm_g1_recs(zk_context* ctx, const void* d_recs, const void* d_scalars, size_t n, uint64_t out_affine[8],
+                hipStream_t st);
+int msm_g2_recs(zk_context* ctx, const void* d_recs, const void* d_scalars, size_t n, uint64_t out_affine[16],
+                hipStream_t st);
+int recs_from_std(zk_context* ctx, bool g2, void* d_recs, const void* d_std, const void* d_flags, size_t n,
+                  hipStream_t st);
+size_t rec_bytes(bool g2);
 void msm_workspace_free(MsmWorkspace* ws);
 
 // ---- fixed base (pointgen.hip)

@@ -98,6 +98,18 @@ def random_fr(n, rng):
     return out
 
 
+SPARSE_DTYPE = np.dtype([("row", "<i4"), ("col", "<i4"), ("value", "<u8", (4,))])  # 40 bytes
+
+
+def sparse_entries(rows, cols, vals):
+    """reference SparseEntry array (src/prover/circuit.cuh:32-36)."""
+    e = np.zeros(len(rows), dtype=SPARSE_DTYPE)
+    e["row"] = rows
+    e["col"] = cols
+    e["value"] = np.asarray(vals, dtype=np.uint64).reshape(-1, 4)
+    return e
+
+
 class DeviceBuffer:
     def __init__(self, ctx, nbytes):
         self.ctx = ctx
@@ -205,3 +217,76 @@ class Context:
 
     def g2_generator_mul(self, d_scalars, n, d_out):
         self._check(lib().zk_g2_generator_mul(self.h, vp(d_scalars.ptr), n, vp(d_out.ptr), None), "g2_generator_mul")
+
+    # ---- Groth16
+    def r1cs(self, num_constraints, num_variables, num_public, A, B, C):
+        """A, B, C: SPARSE_DTYPE arrays (or (rows, cols, vals) triples)."""
+        mats = []
+        for M in (A, B, C):
+            if not isinstance(M, np.ndarray):
+                M = sparse_entries(*M)
+            mats.append(np.ascontiguousarray(M))
+        h = vp()
+        self._check(lib().zk_r1cs_create(self.h, num_constraints, num_variables, num_public,
+                                         _np_ptr(mats[0]), len(mats[0]), _np_ptr(mats[1]), len(mats[1]),
+                                         _np_ptr(mats[2]), len(mats[2]), ctypes.byref(h)), "zk_r1cs_create")
+        return R1CS(self, h, num_constraints, num_variables, num_public)
+
+    def load_pk(self, path):
+        h = vp()
+        self._check(lib().zk_pk_load(self.h, str(path).encode(), ctypes.byref(h)), "zk_pk_load")
+        return ProvingKey(self, h)
+
+    def setup(self, r1cs, seed, pk_path, vk_path):
+        self._check(lib().zk_setup(self.h, r1cs.h, seed, str(pk_path).encode(), str(vk_path).encode()), "zk_setup")
+
+    def prove(self, pk, r1cs, witness, num_public, seed, check_witness=True):
+        """witness: (m, 4) uint64 Montgomery words.  Returns (256 bytes, timings)."""
+        w = np.ascontiguousarray(witness, dtype=np.uint64)
+        out = np.zeros(256, dtype=np.uint8)
+        t = np.zeros(8, dtype=np.float64)
+        self._check(lib().zk_prove(self.h, pk.h, r1cs.h, _np_ptr(w), w.shape[0], num_public, seed,
+                                   int(check_witness), _np_ptr(out), _np_ptr(t)), "zk_prove")
+        names = ("total", "quotient", "A", "B_g2", "L", "H", "B_g1", "host")
+        return out.tobytes(), dict(zip(names, t.tolist()))
+
+    def quotient_h(self, r1cs, d_witness, m, d_h):
+        self._check(lib().zk_quotient_h(self.h, r1cs.h, vp(d_witness.ptr), m, vp(d_h.ptr), None), "zk_quotient_h")
+
+
+class R1CS:
+    def __init__(self, ctx, h, nc, nv, npub):
+        self.ctx, self.h, self.nc, self.nv, self.npub = ctx, h, nc, nv, npub
+        ln = ctypes.c_int()
+        lib().zk_r1cs_domain(h, ctypes.byref(ln))
+        self.log_n = ln.value
+
+    def close(self):
+        if self.h:
+            lib().zk_r1cs_destroy(self.h)
+            self.h = None
+
+    def __del__(self):
+        try:
+            self.close()
+        except Exception:
+            pass
+
+
+class ProvingKey:
+    def __init__(self, ctx, h):
+        self.ctx, self.h = ctx, h
+        n, m, p = ctypes.c_int(), ctypes.c_int(), ctypes.c_int()
+        lib().zk_pk_info(h, ctypes.byref(n), ctypes.byref(m), ctypes.byref(p))
+        self.n, self.m, self.npub = n.value, m.value, p.value
+
+    def close(self):
+        if self.h:
+            lib().zk_pk_destroy(self.h)
+            self.h = None
+
+    def __del__(self):
+        try:
+            self.close()
+        except Exception:
+            pass

@@ -1,0 +1,156 @@
+"""GPU quotient polynomial, trusted setup and prove through the C ABI.
+
+Pins:
+  * h (zk_quotient_h) bit-exact against the oracle's compute_h
+    (groth16.cu:263-390) and the quotient identity at a random point;
+  * proving and verification key files byte-identical to the oracle's
+    restatement of Groth16Prover::setup (groth16.cu:446-642) for the same
+    R1CS and toxic-waste seed;
+  * 256-byte proofs byte-identical to the oracle's restatement of prove
+    (groth16.cu:655-920) for the same key, witness and blinding seed;
+  * every proof accepted by the reference's own verifier (pairing code
+    compiled from the reference sources into oracle/_ref), a wrong public
+    input rejected, an unsatisfying witness refused;
+  * the reference's own T4 proving keys load with the reference checks.
+"""
+import os
+import struct
+
+import numpy as np
+import pytest
+
+import zkpy as Z
+from bindings import OracleR1CS, ref, ref_available
+from r1cs_gen import mul_circuit, random_r1cs
+from test_oracle import check_quotient
+
+pytestmark = pytest.mark.gpu
+GOLD = os.path.join(os.path.dirname(os.path.abspath(__file__)), "golden")
+SETUP_SEED = 0xDEADBEEF42
+PROVE_SEED = 0xCAFEBABE
+
+
+@pytest.fixture(scope="module")
+def ctx():
+    import zkml_amd
+    c = zkml_amd.Context(0)
+    yield c
+    c.close()
+
+
+def gpu_r1cs(ctx, circ):
+    return ctx.r1cs(circ.nc, circ.nv, circ.npub, *circ.mats())
+
+
+def write_public(path, vals):
+    with open(path, "wb") as f:
+        f.write(struct.pack("<i", len(vals)))
+        for v in vals:
+            f.write(v.to_bytes(32, "little"))
+
+
+@pytest.mark.parametrize("rows", [2, 100, 1000, 5000])
+def test_quotient_h_matches_oracle(ctx, rows):
+    circ = mul_circuit() if rows == 2 else random_r1cs(rows, seed=rows)
+    r = gpu_r1cs(ctx, circ)
+    n = 1 << r.log_n
+    w = circ.witness_words()
+    dw = ctx.upload(w)
+    dh = ctx.alloc(n * 32)
+    ctx.quotient_h(r, dw, circ.nv, dh)
+    got = ctx.d2h(dh, (n, 4))
+    oc = OracleR1CS(circ.nc, circ.nv, circ.npub, circ.npriv, circ.mats())
+    assert np.array_equal(got, oc.compute_h(w, threads=8))
+    if rows <= 1000:
+        check_quotient(circ, got, seed=rows)
+
+
+@pytest.mark.parametrize("kind", ["mul", "r300", "r3000"])
+def test_setup_and_prove_match_oracle_and_verify(ctx, tmp_path, kind):
+    circ = {"mul": lambda: mul_circuit(7, 9), "r300": lambda: random_r1cs(300, npub=3, seed=5),
+            "r3000": lambda: random_r1cs(3000, npub=6, seed=6, small_frac=0.7)}[kind]()
+    r = gpu_r1cs(ctx, circ)
+    oc = OracleR1CS(circ.nc, circ.nv, circ.npub, circ.npriv, circ.mats())
+    pk_g, vk_g = tmp_path / "pk_gpu.bin", tmp_path / "vk_gpu.bin"
+    pk_o, vk_o = str(tmp_path / "pk_orc.bin"), str(tmp_path / "vk_orc.bin")
+    ctx.setup(r, SETUP_SEED, pk_g, vk_g)
+    oc.setup(SETUP_SEED, pk_o, vk_o, threads=8)
+    assert pk_g.read_bytes() == open(pk_o, "rb").read()
+    assert vk_g.read_bytes() == open(vk_o, "rb").read()
+    pk = ctx.load_pk(pk_g)
+    assert (pk.n, pk.m, pk.npub) == (1 << r.log_n, circ.nv, circ.npub)
+    proof, t = ctx.prove(pk, r, circ.witness_words(), circ.npub, PROVE_SEED)
+    rc, proof_o, _ = oc.prove(pk_o, circ.witness_words(), PROVE_SEED, threads=8)
+    assert rc == 0
+    assert proof == proof_o
+    assert t["total"] > 0
+    if ref_available():
+        pf = tmp_path / "proof.bin"
+        pf.write_bytes(proof)
+        pub = tmp_path / "pub.bin"
+        write_public(pub, circ.public())
+        assert ref().ref_verify_files(str(vk_g).encode(), str(pf).encode(), str(pub).encode()) == 1
+        bad = list(circ.public())
+        bad[-1] = (bad[-1] + 1) % Z.R
+        write_public(pub, bad)
+        assert ref().ref_verify_files(str(vk_g).encode(), str(pf).encode(), str(pub).encode()) == 0
+
+
+def test_prove_rejects_bad_witness_and_sizes(ctx, tmp_path):
+    import zkml_amd
+    circ = random_r1cs(64, seed=9)
+    r = gpu_r1cs(ctx, circ)
+    ctx.setup(r, SETUP_SEED, tmp_path / "pk.bin", tmp_path / "vk.bin")
+    pk = ctx.load_pk(tmp_path / "pk.bin")
+    w = circ.witness_words()
+    bad = w.copy()
+    bad[-1] = np.array(Z.fr_words(3), dtype=np.uint64)
+    with pytest.raises(zkml_amd.ZkError, match="satisfy"):
+        ctx.prove(pk, r, bad, circ.npub, PROVE_SEED)
+    with pytest.raises(zkml_amd.ZkError):
+        ctx.prove(pk, r, w[:-1], circ.npub, PROVE_SEED)
+    with pytest.raises(zkml_amd.ZkError):
+        ctx.prove(pk, r, w, circ.npub + 1, PROVE_SEED)
+    # ZKML_SKIP_WITNESS_CHECK path: proof produced, but it does not verify
+    proof, _ = ctx.prove(pk, r, bad, circ.npub, PROVE_SEED, check_witness=False)
+    assert len(proof) == 256
+
+
+def test_loads_reference_t4_proving_keys(ctx):
+    import zkml_amd
+    for d, (n, m, npub) in (("t4_p16", (128, 140, 75)), ("t4_p160", (1024, 716, 75))):
+        pk = ctx.load_pk(os.path.join(GOLD, d, "pk.bin"))
+        assert (pk.n, pk.m, pk.npub) == (n, m, npub)
+        pk.close()
+    with pytest.raises(zkml_amd.ZkError):
+        ctx.load_pk(os.path.join(GOLD, "t4_p16", "vk.bin"))
+
+
+def test_truncated_pk_rejected(ctx, tmp_path):
+    import zkml_amd
+    data = open(os.path.join(GOLD, "t4_p16", "pk.bin"), "rb").read()
+    p = tmp_path / "trunc.bin"
+    p.write_bytes(data[: len(data) // 2])
+    with pytest.raises(zkml_amd.ZkError):
+        ctx.load_pk(p)
+
+
+def test_prove_2_16_matches_oracle(ctx, tmp_path):
+    """Full-size parity: 2^16-domain synthetic R1CS (BASELINE config-5 shape),
+    GPU setup and prove against the oracle on the same key."""
+    circ = random_r1cs((1 << 16) - 40, inputs=16, npub=4, seed=16, small_frac=0.7)
+    r = gpu_r1cs(ctx, circ)
+    assert r.log_n == 16
+    pk_path, vk_path = tmp_path / "pk.bin", tmp_path / "vk.bin"
+    ctx.setup(r, SETUP_SEED, pk_path, vk_path)
+    pk = ctx.load_pk(pk_path)
+    proof, t = ctx.prove(pk, r, circ.witness_words(), circ.npub, PROVE_SEED)
+    oc = OracleR1CS(circ.nc, circ.nv, circ.npub, circ.npriv, circ.mats())
+    rc, proof_o, _ = oc.prove(str(pk_path), circ.witness_words(), PROVE_SEED, threads=16)
+    assert rc == 0 and proof == proof_o
+    if ref_available():
+        pf = tmp_path / "proof.bin"
+        pf.write_bytes(proof)
+        pub = tmp_path / "pub.bin"
+        write_public(pub, circ.public())
+        assert ref().ref_verify_files(str(vk_path).encode(), str(pf).encode(), str(pub).encode()) == 1
