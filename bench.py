@@ -1,0 +1,215 @@
+"""Benchmark of the MI355X Groth16 prover core (BASELINE.json metric:
+"Groth16 prove ms at 2^16 constraints; G1 MSM Mpoints/s at 2^20").
+
+A step is one G1 MSM over 2^20 points (P_i = k_i G1 for
+seeded k_i, scalars uniform in [0, r)), with points and scalars resident in
+HBM.  `value` is that MSM's throughput in Mpoints/s.  The same run also times a
+full Groth16 prove on a 2^16-domain synthetic R1CS (config-5 shape) and the
+2^22 NTT of config 2, and the CPU oracle's restatement of the reference MSM on
+the host cores (cpu_baseline).  Prints one JSON line.
+
+    python bench.py [--gpus 1] [--steps K] [--warmup W]
+"""
+import argparse
+import json
+import os
+import sys
+import time
+
+import numpy as np
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+sys.path.insert(0, os.path.join(ROOT, "cuda-zkml_amd"))
+sys.path.insert(0, os.path.join(ROOT, "tests"))
+
+# MI355X peaks: full-rate 32-bit mad (v_mad_u64_u32 issues at the VALU rate on
+# gfx950, measured) = 256 CU x 64 lanes x 2.4 GHz; HBM3E 8 TB/s.
+PEAK_MAD_TOPS = 256 * 64 * 2.4e9 / 1e12
+PEAK_HBM_GBS = 8000.0
+MADS_PER_FIELD_MUL = 136  # 8x32-bit CIOS: 2*8^2 + 8
+
+
+def log(msg):
+    print(msg, file=sys.stderr, flush=True)
+
+
+def msm_algorithmic_mults(n, c):
+    """BASELINE.md F(N) with W = ceil(255/c) signed windows."""
+    w = -(-255 // c)
+    return n * w * 10 + w * (1 << (c - 1)) * 2 * 14 + w * (6 * c + 14)
+
+
+def best_c(n):
+    return min(range(8, 22), key=lambda c: msm_algorithmic_mults(n, c))
+
+
+def main():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=20)
+    ap.add_argument("--warmup", type=int, default=3)
+    ap.add_argument("--log-n", type=int, default=20)
+    ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
+    ap.add_argument("--no-prove", action="store_true")
+    args = ap.parse_args()
+    if args.gpus != 1:
+        print(f"bench.py measures one GPU only (asked for --gpus {args.gpus}); this build has no multi-GPU path",
+              file=sys.stderr)
+        sys.exit(2)
+
+    import zkml_amd
+    ctx = zkml_amd.Context(0)
+    rng = np.random.default_rng(20260601)
+    n = 1 << args.log_n
+
+    # ---------------- MSM 2^20 (the step)
+    log(f"[bench] generating {n} points P_i = k_i G1 on the GPU")
+    k = zkml_amd.random_fr(n, rng)
+    s = zkml_amd.random_fr(n, rng)
+    dk = ctx.upload(k)
+    dp = ctx.alloc(n * 64)
+    ctx.g1_generator_mul(dk, n, dp)
+    ds = ctx.upload(s)
+    ctx.sync()
+    for _ in range(args.warmup):
+        res = ctx.msm_g1(dp, ds, n)
+    ctx.sync()
+    ctx.set_profiling(True)
+    ctx.reset_kernel_stats()
+    t0 = time.perf_counter()
+    for _ in range(args.steps):
+        res = ctx.msm_g1(dp, ds, n)
+    ctx.sync()
+    t1 = time.perf_counter()
+    ms_step = (t1 - t0) * 1e3 / args.steps
+    kernels = {}
+    for name in ctx.kernel_names():
+        cnt, ms = ctx.kernel_stats(name)
+        kernels[name] = {"ms_per_step": ms / args.steps, "launches_per_step": cnt / args.steps}
+    ctx.set_profiling(False)
+    mpoints = n / (ms_step * 1e-3) / 1e6
+    log(f"[bench] MSM 2^{args.log_n}: {ms_step:.3f} ms/step, {mpoints:.1f} Mpoints/s")
+
+    # roofline of the dominant kernel (bucket accumulation): every sorted
+    # (window, point) entry costs one mixed XYZZ addition = 10 field mults.
+    c = zkml_amd_window_bits(n)
+    windows = -(-254 // c)
+    acc = kernels.get("msm_accumulate", {"ms_per_step": float("nan"), "launches_per_step": 1})
+    acc_ms = acc["ms_per_step"] / max(acc["launches_per_step"], 1)
+    acc_mads = n * windows * 10 * MADS_PER_FIELD_MUL
+    achieved = acc_mads / (acc_ms * 1e-3) / 1e12
+    # whole-MSM VALU fraction with BASELINE.md's algorithmic count
+    f_mults = msm_algorithmic_mults(n, best_c(n))
+    msm_frac = f_mults * MADS_PER_FIELD_MUL / (ms_step * 1e-3) / 1e12 / PEAK_MAD_TOPS
+
+    # ---------------- NTT 2^22 (config 2)
+    ntt = {}
+    ln = 22
+    a = zkml_amd.random_fr(1 << ln, rng)
+    da = ctx.upload(a)
+    do = ctx.alloc((1 << ln) * 32)
+    ctx.ntt(do, da, ln)
+    ctx.sync()
+    ctx.set_profiling(True)
+    ctx.reset_kernel_stats()
+    reps = 10
+    t0 = time.perf_counter()
+    for _ in range(reps):
+        ctx.ntt(do, da, ln)
+    ctx.sync()
+    wall = (time.perf_counter() - t0) * 1e3 / reps
+    _, kms = ctx.kernel_stats("ntt_pass")
+    ctx.set_profiling(False)
+    kms /= reps
+    ntt = {"log_n": ln, "ms": round(kms, 4), "wall_ms": round(wall, 4),
+           "hbm_GBps_alg": round(64 * (1 << ln) / (kms * 1e-3) / 1e9, 1),
+           "hbm_frac": round(64 * (1 << ln) / (kms * 1e-3) / 1e9 / PEAK_HBM_GBS, 4),
+           "valu_frac": round(((1 << ln) // 2 * ln) * MADS_PER_FIELD_MUL / (kms * 1e-3) / 1e12 / PEAK_MAD_TOPS, 4)}
+    log(f"[bench] NTT 2^22: {kms:.3f} ms")
+    del da, do
+
+    # ---------------- full prove at 2^16
+    prove = None
+    if not args.no_prove:
+        from r1cs_gen import random_r1cs
+        import tempfile
+        log("[bench] building a 2^16-domain synthetic R1CS and running GPU setup")
+        circ = random_r1cs((1 << 16) - 40, inputs=16, npub=4, seed=16, small_frac=0.7)
+        r = ctx.r1cs(circ.nc, circ.nv, circ.npub, *circ.mats())
+        w = circ.witness_words()
+        with tempfile.TemporaryDirectory() as td:
+            ctx.setup(r, 0xDEADBEEF42, os.path.join(td, "pk.bin"), os.path.join(td, "vk.bin"))
+            pk = ctx.load_pk(os.path.join(td, "pk.bin"))
+        for _ in range(2):
+            ctx.prove(pk, r, w, circ.npub, 0xCAFEBABE)
+        times = []
+        parts = None
+        for _ in range(5):
+            t0 = time.perf_counter()
+            _, t = ctx.prove(pk, r, w, circ.npub, 0xCAFEBABE)
+            times.append((time.perf_counter() - t0) * 1e3)
+            parts = t
+        prove = {"constraints": circ.nc, "variables": circ.nv, "domain": 1 << r.log_n,
+                 "ms": round(float(np.median(times)), 3),
+                 "breakdown_ms": {k_: round(v, 3) for k_, v in parts.items()}}
+        log(f"[bench] prove 2^16: {prove['ms']:.3f} ms")
+
+    # ---------------- CPU baseline (oracle restatement of the reference MSM)
+    cpu = None
+    if not args.no_cpu:
+        from bindings import oracle, ptr
+        lib = oracle()
+        sample = 1 << 18
+        pts = ctx.d2h(dp, (n, 8))[:sample].copy()
+        sc = np.ascontiguousarray(s[:sample])
+        out = np.zeros(8, dtype=np.uint64)
+        threads = 1
+        t0 = time.perf_counter()
+        lib.orc_msm_g1(ptr(pts), ptr(sc), sample, 0, threads, ptr(out))
+        dt = time.perf_counter() - t0
+        cpu = {"value": round(sample / dt / 1e6, 4), "unit": "Mpoints/s", "cores": threads, "kind": "port",
+               "sample": f"G1 MSM over the first 2^18 of the same points/scalars, reference Pippenger "
+                         f"(MSMConfig windows, Jacobian mixed adds, serial running sums), {dt:.2f} s"}
+        log(f"[bench] CPU baseline: {cpu['value']} Mpoints/s ({dt:.2f} s)")
+
+    line = {
+        "metric": "Groth16 prove ms at 2^16 constraints; G1 MSM Mpoints/s at 2^20",
+        "value": round(mpoints, 2),
+        "unit": "Mpoints/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(ms_step, 4),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "u32 (BN254 Fq/Fr 256-bit modular, 9x29-bit limbs)",
+        "data": "synthetic, seeded (P_i = k_i G1, k_i and s_i uniform in [0, r))",
+        "config": {"workload": f"G1 MSM, n = 2^{args.log_n}, BASELINE config 3 (uniform scalars)",
+                   "window_bits": c, "windows": windows},
+        "roofline": {"bound": "valu", "achieved": round(achieved, 3), "peak": round(PEAK_MAD_TOPS, 2),
+                     "unit": "T mad32/s", "frac": round(achieved / PEAK_MAD_TOPS, 4), "traffic": None,
+                     "kernel": "msm_accumulate", "kernel_ms": round(acc_ms, 4)},
+        "msm_valu_frac_whole": round(msm_frac, 4),
+        "kernels_ms_per_step": {k_: round(v["ms_per_step"], 4) for k_, v in kernels.items()},
+        "prove_2_16": prove,
+        "ntt_2_22": ntt,
+        "cpu_baseline": cpu,
+    }
+    print(json.dumps(line), flush=True)
+    ctx.close()
+
+
+def zkml_amd_window_bits(n):
+    """Window size the library picks (csrc/msm.hip choose_c)."""
+    best, bestv = 8, None
+    for c in range(8, 19):
+        w = -(-254 // c)
+        v = w * (n + 1.5 * (1 << c))
+        if bestv is None or v < bestv:
+            best, bestv = c, v
+    return best
+
+
+if __name__ == "__main__":
+    main()
