@@ -28,7 +28,6 @@
 #include <string.h>
 
 #include <algorithm>
-#include <rocprim/rocprim.hpp>
 #include <vector>
 
 #include "curve.hpp"
@@ -38,9 +37,8 @@
 namespace zk {
 
 constexpr uint32_t KEY_INVALID = 0xffffffffu;
-constexpr int MSM_L0 = 32;         // sorted entries per accumulation thread
-constexpr int MSM_SEG = 16;        // buckets per reduction segment
-constexpr int MSM_GROUP = 256;     // segments per reduction workgroup (G1)
+constexpr int MSM_L0 = 64;         // sorted entries per accumulation thread
+constexpr int MSM_G = 8;           // buckets per reduction thread
 
 // ------------------------------------------------------------------ point records
 // G1 record: x[9], y[9], inf, pad  (80 bytes);  G2 record: x0,x1,y0,y1 [9 each],
@@ -227,13 +225,13 @@ __global__ void k_msm_bounds(const uint32_t* __restrict__ sk, size_t total, uint
   }
 }
 
-// run length per key, after bounds are complete
+// longest run, after bounds are complete; one atomic per wave
 __global__ void k_msm_maxrun(const uint32_t* __restrict__ start, const uint32_t* __restrict__ end, size_t nkeys,
                              uint32_t* __restrict__ stat) {
   size_t k = blockIdx.x * (size_t)blockDim.x + threadIdx.x;
-  if (k >= nkeys) return;
-  uint32_t len = end[k] - start[k];
-  if (len > 1) atomicMax(&stat[1], len);
+  uint32_t len = k < nkeys ? end[k] - start[k] : 0;
+  for (int off = 32; off >= 1; off >>= 1) len = max(len, (uint32_t)__shfl_xor((int)len, off));
+  if ((threadIdx.x & 63) == 0 && len > 1) atomicMax(&stat[1], len);
 }
 
 // ------------------------------------------------------------------ accumulate
@@ -333,65 +331,119 @@ __global__ __launch_bounds__(256) void k_msm_finalize(ChunkSlots<F> slots, uint3
 }
 
 // ------------------------------------------------------------------ bucket reduction
-// Segment s of window w covers buckets b in [s*G+1, (s+1)*G]:
-//   run = sum S_b, acc = sum (b - s*G) S_b, out = acc + (s*G) run.
-template <class F>
-__global__ __launch_bounds__(256) void k_msm_segments(const xyzz<F>* __restrict__ buckets,
-                                                      const uint32_t* __restrict__ start,
-                                                      const uint32_t* __restrict__ end, int c, int W,
-                                                      xyzz<F>* __restrict__ seg_out) {
+// Window sum  sum_{b=1..B} b S_b,  B = 2^(c-1).
+//
+// Level 1: a workgroup of T threads owns T*G consecutive buckets (base k*T*G);
+// thread t owns buckets base + t*G + i, i = 1..G, and forms
+//   run_t = sum_i S,  acc_t = sum_i i S      (2G additions, from the top).
+// With the inclusive suffix sums SR_t = sum_{u >= t} run_u (Hillis-Steele scan
+// in LDS),  sum_{b in group} (b - base) S_b = sum_t acc_t + G sum_{t >= 1} SR_t,
+// so each thread adds G*SR_t (log2 G doublings) to acc_t and a tree sums the
+// group.  Outputs per group: P_k (that sum) and RUN_k = SR_0.
+// Level 2 (one workgroup per window, K groups):
+//   sum_b b S_b = sum_k P_k + T G sum_{s >= 1} SRUN_s,  same scan and tree.
+
+// Inclusive suffix scan over the T values held by the threads of a
+// workgroup; returns this thread's sum_{u >= t} v_u.
+template <class F, int T>
+__device__ __forceinline__ xyzz<F> wg_suffix_scan(xyzz<F> v, xyzz<F>* sh) {
+  const int t = threadIdx.x;
+  sh[t] = v;
+  __syncthreads();
+  for (int d = 1; d < T; d <<= 1) {
+    xyzz<F> o;
+    const bool has = t + d < T;
+    if (has) o = sh[t + d];
+    __syncthreads();
+    if (has) {
+      xyzz_add(v, o);
+      sh[t] = v;
+    }
+    __syncthreads();
+  }
+  return v;
+}
+
+template <class F, int T>
+__device__ __forceinline__ xyzz<F> wg_sum(xyzz<F> v, xyzz<F>* sh) {
+  const int t = threadIdx.x;
+  __syncthreads();
+  sh[t] = v;
+  __syncthreads();
+  for (int h = T / 2; h >= 1; h >>= 1) {
+    if (t < h) {
+      xyzz_add(v, sh[t + h]);
+      sh[t] = v;
+    }
+    __syncthreads();
+  }
+  return v;
+}
+
+template <class F, int T>
+__global__ __launch_bounds__(T) void k_msm_reduce1(const xyzz<F>* __restrict__ buckets,
+                                                   const uint32_t* __restrict__ start,
+                                                   const uint32_t* __restrict__ end, int c, uint32_t K,
+                                                   xyzz<F>* __restrict__ P, xyzz<F>* __restrict__ RUN) {
+  __shared__ xyzz<F> sh[T];
   const uint32_t B1 = 1u << (c - 1);
-  const uint32_t nseg = B1 / MSM_SEG;
-  const uint32_t t = blockIdx.x * blockDim.x + threadIdx.x;
-  if (t >= nseg * (uint32_t)W) return;
-  const uint32_t w = t / nseg, s = t % nseg;
+  const uint32_t w = blockIdx.x / K, k = blockIdx.x % K;
+  const uint32_t t = threadIdx.x;
+  const uint32_t b0 = k * T * MSM_G + t * MSM_G;  // bucket index offset of this thread
   xyzz<F> run, acc;
   xyzz_set_inf(run);
   xyzz_set_inf(acc);
-  for (int k = MSM_SEG; k >= 1; k--) {
-    const uint32_t b = s * MSM_SEG + k;
+  for (int i = MSM_G; i >= 1; i--) {
+    const uint32_t b = b0 + i;
     const uint32_t key = (w << c) | b;
     if (end[key] > start[key]) xyzz_add(run, buckets[w * B1 + b - 1]);
     xyzz_add(acc, run);
   }
-  xyzz_mul_small(run, s * MSM_SEG);
-  xyzz_add(acc, run);
-  seg_out[t] = acc;
+  xyzz<F> sr = wg_suffix_scan<F, T>(run, sh);
+  if (t >= 1) {
+    for (int d = 1; d < MSM_G; d <<= 1) xyzz_dbl(sr);
+    xyzz_add(acc, sr);
+  } else {
+    RUN[blockIdx.x] = sr;  // thread 0 holds the group total
+  }
+  xyzz<F> tot = wg_sum<F, T>(acc, sh);
+  if (t == 0) P[blockIdx.x] = tot;
 }
 
-// LDS tree over groups of `gsz` segments: out[w*ngroups + g].
-template <class F, int GSZ>
-__global__ __launch_bounds__(GSZ) void k_msm_group_sum(const xyzz<F>* __restrict__ seg, uint32_t nseg_per_w,
-                                                       xyzz<F>* __restrict__ out) {
-  __shared__ xyzz<F> sh[GSZ];
-  const uint32_t ngroups = (nseg_per_w + GSZ - 1) / GSZ;
-  const uint32_t w = blockIdx.x / ngroups, g = blockIdx.x % ngroups;
-  const uint32_t s = g * GSZ + threadIdx.x;
-  if (s < nseg_per_w) sh[threadIdx.x] = seg[w * nseg_per_w + s];
-  else xyzz_set_inf(sh[threadIdx.x]);
-  __syncthreads();
-  for (int h = GSZ / 2; h >= 1; h >>= 1) {
-    if (threadIdx.x < (uint32_t)h) {
-      xyzz<F> a = sh[threadIdx.x];
-      xyzz_add(a, sh[threadIdx.x + h]);
-      sh[threadIdx.x] = a;
-    }
-    __syncthreads();
+// One workgroup of K threads per window; log2tg = log2(T*G).
+template <class F, int KMAX>
+__global__ __launch_bounds__(KMAX) void k_msm_reduce2(const xyzz<F>* __restrict__ P, const xyzz<F>* __restrict__ RUN,
+                                                      uint32_t K, int log2tg, xyzz<F>* __restrict__ out) {
+  __shared__ xyzz<F> sh[KMAX];
+  const uint32_t w = blockIdx.x, t = threadIdx.x;
+  xyzz<F> run, acc;
+  xyzz_set_inf(run);
+  xyzz_set_inf(acc);
+  if (t < K) {
+    run = RUN[w * K + t];
+    acc = P[w * K + t];
   }
-  if (threadIdx.x == 0) out[blockIdx.x] = sh[0];
+  xyzz<F> sr = wg_suffix_scan<F, KMAX>(run, sh);
+  if (t >= 1 && t < K) {
+    for (int d = 0; d < log2tg; d++) xyzz_dbl(sr);
+    xyzz_add(acc, sr);
+  }
+  xyzz<F> tot = wg_sum<F, KMAX>(acc, sh);
+  if (t == 0) out[w] = tot;
 }
 
 // ------------------------------------------------------------------ workspace
 struct MsmWorkspace {
   DevBuf recs, keys_in, vals_in, keys_out, vals_out, sort_tmp, start, end, stat, buckets, hkey, tkey, hpt, tpt, seg,
-      grp;
+      grp, win;
   uint32_t* h_stat = nullptr;  // pinned
 };
 
 void msm_workspace_free(MsmWorkspace* ws) {
   if (!ws) return;
   for (DevBuf* b : {&ws->recs, &ws->keys_in, &ws->vals_in, &ws->keys_out, &ws->vals_out, &ws->sort_tmp, &ws->start,
-                    &ws->end, &ws->stat, &ws->buckets, &ws->hkey, &ws->tkey, &ws->hpt, &ws->tpt, &ws->seg, &ws->grp})
+                    &ws->end, &ws->stat, &ws->buckets, &ws->hkey, &ws->tkey, &ws->hpt, &ws->tpt, &ws->seg, &ws->grp,
+                    &ws->win})
     if (b->p) (void)hipFree(b->p);
   if (ws->h_stat) (void)hipHostFree(ws->h_stat);
   delete ws;
@@ -528,12 +580,7 @@ static int msm_run_recs(zk_context* ctx, MsmWorkspace& ws, const uint4* recs, co
             (const uint4*)d_scalars, n, c, W);
 
   const unsigned end_bit = 32 - __builtin_clz((unsigned)((W << c) | 1));
-  size_t tmp_bytes = 0;
-  ZK_HIP(ctx, rocprim::radix_sort_pairs(nullptr, tmp_bytes, kin, kout, vin, vout, total, 0u, end_bit, st));
-  ZK_TRY(ctx->ensure(ws.sort_tmp, tmp_bytes));
-  ctx->tic("msm_sort", st);
-  ZK_HIP(ctx, rocprim::radix_sort_pairs(ws.sort_tmp.p, tmp_bytes, kin, kout, vin, vout, total, 0u, end_bit, st));
-  ctx->toc(st);
+  ZK_TRY(sort_pairs_u32(ctx, ws.sort_tmp, kin, kout, vin, vout, total, end_bit, st));
 
   ZK_HIP(ctx, hipMemsetAsync(start, 0, nkeys * 4, st));
   ZK_HIP(ctx, hipMemsetAsync(end, 0, nkeys * 4, st));
@@ -558,19 +605,44 @@ static int msm_run_recs(zk_context* ctx, MsmWorkspace& ws, const uint4* recs, co
   ZK_LAUNCH(ctx, st, "msm_combine", k_msm_finalize<F>, dim3(cdiv(used_chunks, 256)), dim3(256), 0, slots,
             used_chunks, c, buckets);
 
-  const uint32_t nseg = (1u << (c - 1)) / MSM_SEG;
-  ZK_TRY(ctx->ensure(ws.seg, (size_t)nseg * W * sizeof(xyzz<F>)));
-  ZK_LAUNCH(ctx, st, "msm_reduce", k_msm_segments<F>, dim3(cdiv((size_t)nseg * W, 256)), dim3(256), 0, buckets,
-            start, end, c, W, (xyzz<F>*)ws.seg.p);
-  constexpr int GSZ = sizeof(F) == sizeof(fq) ? MSM_GROUP : MSM_GROUP / 2;
-  const uint32_t ngroups = (nseg + GSZ - 1) / GSZ;
-  ZK_TRY(ctx->ensure(ws.grp, (size_t)ngroups * W * sizeof(xyzz<F>)));
-  ZK_LAUNCH(ctx, st, "msm_reduce", (k_msm_group_sum<F, GSZ>), dim3(ngroups * W), dim3(GSZ), 0,
-            (const xyzz<F>*)ws.seg.p, nseg, (xyzz<F>*)ws.grp.p);
-  std::vector<xyzz<F>> parts((size_t)ngroups * W);
-  ZK_HIP(ctx, hipMemcpyAsync(parts.data(), ws.grp.p, parts.size() * sizeof(xyzz<F>), hipMemcpyDeviceToHost, st));
+  // bucket reduction: level 1 (T threads x G buckets per group), level 2 per window
+  constexpr int T1 = sizeof(F) == sizeof(fq) ? 256 : 128;
+  const uint32_t B1 = 1u << (c - 1);
+  int t1 = (int)std::min<uint32_t>(T1, B1 / MSM_G);
+  const uint32_t K = B1 / (t1 * MSM_G);
+  ZK_TRY(ctx->ensure(ws.seg, (size_t)K * W * sizeof(xyzz<F>)));
+  ZK_TRY(ctx->ensure(ws.grp, (size_t)K * W * sizeof(xyzz<F>)));
+  ZK_TRY(ctx->ensure(ws.win, (size_t)W * sizeof(xyzz<F>)));
+  xyzz<F>* Pk = (xyzz<F>*)ws.seg.p;
+  xyzz<F>* RUNk = (xyzz<F>*)ws.grp.p;
+  xyzz<F>* win = (xyzz<F>*)ws.win.p;
+  switch (t1) {
+#define ZK_R1(TT)                                                                                              \
+  case TT:                                                                                                     \
+    ZK_LAUNCH(ctx, st, "msm_reduce", (k_msm_reduce1<F, TT>), dim3(K * W), dim3(TT), 0, buckets, start, end, c, K, \
+              Pk, RUNk);                                                                                       \
+    break;
+    ZK_R1(256)
+    ZK_R1(128)
+    ZK_R1(64)
+    ZK_R1(32)
+    ZK_R1(16)
+#undef ZK_R1
+    default:
+      return ctx->fail(ZK_ERR_INVALID, "msm: unsupported reduction shape");
+  }
+  int log2tg = 0;
+  while ((1 << log2tg) < t1 * MSM_G) log2tg++;
+  if (K <= 32)
+    ZK_LAUNCH(ctx, st, "msm_reduce", (k_msm_reduce2<F, 32>), dim3(W), dim3(32), 0, Pk, RUNk, K, log2tg, win);
+  else if (K <= 128)
+    ZK_LAUNCH(ctx, st, "msm_reduce", (k_msm_reduce2<F, 128>), dim3(W), dim3(128), 0, Pk, RUNk, K, log2tg, win);
+  else
+    return ctx->fail(ZK_ERR_INVALID, "msm: too many reduction groups");
+  std::vector<xyzz<F>> parts((size_t)W);
+  ZK_HIP(ctx, hipMemcpyAsync(parts.data(), win, parts.size() * sizeof(xyzz<F>), hipMemcpyDeviceToHost, st));
   ZK_HIP(ctx, hipStreamSynchronize(st));
-  host_finish<F>(parts, W, (int)ngroups, c, out);
+  host_finish<F>(parts, W, 1, c, out);
   return ZK_OK;
 }
 
