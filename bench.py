@@ -92,8 +92,7 @@ def main():
 
     # roofline of the dominant kernel (bucket accumulation): every sorted
     # (window, point) entry costs one mixed XYZZ addition = 10 field mults.
-    c = zkml_amd_window_bits(n)
-    windows = -(-254 // c)
+    c, windows = zkml_amd.Context.msm_config(n)
     acc = kernels.get("msm_accumulate", {"ms_per_step": float("nan"), "launches_per_step": 1})
     acc_ms = acc["ms_per_step"] / max(acc["launches_per_step"], 1)
     acc_mads = n * windows * 10 * MADS_PER_FIELD_MUL
@@ -198,17 +197,6 @@ def main():
     }
     print(json.dumps(line), flush=True)
     ctx.close()
-
-
-def zkml_amd_window_bits(n):
-    """Window size the library picks (csrc/msm.hip choose_c)."""
-    best, bestv = 8, None
-    for c in range(8, 19):
-        w = -(-254 // c)
-        v = w * (n + 1.5 * (1 << c))
-        if bestv is None or v < bestv:
-            best, bestv = c, v
-    return best
 
 
 if __name__ == "__main__":

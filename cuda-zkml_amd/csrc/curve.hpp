@@ -42,6 +42,15 @@ ZK_HD void fset_zero(fq2& a) { a = fq2{fe_zero<FqP>(), fe_zero<FqP>()}; }
 ZK_HD void fset_one(fq& a) { a = fe_one<FqP>(); }
 ZK_HD void fset_one(fq2& a) { a = fq2{fe_one<FqP>(), fe_zero<FqP>()}; }
 
+// a*b - c*d.  Over Fq one Montgomery reduction serves both products (fmul2
+// with 2m - d); over Fq2 the Karatsuba products are formed separately.
+// b may be a lazy difference (fsub_m), the other inputs are reduced.
+ZK_HD fq fmul_sub(const fq& a, const fq& b, const fq& c, const fq& d) { return fmul2(a, b, c, fneg_lazy(d)); }
+ZK_HD fq2 fmul_sub(const fq2& a, const fq2& b, const fq2& c, const fq2& d) { return fsub(fmul(a, b), fmul(c, d)); }
+// a - b left in (0, 4m): only for the second factor of fmul_sub.
+ZK_HD fq fsub_m(const fq& a, const fq& b) { return fsub_lazy(a, b); }
+ZK_HD fq2 fsub_m(const fq2& a, const fq2& b) { return fq2{fsub_lazy(a.c0, b.c0), fsub_lazy(a.c1, b.c1)}; }
+
 // ------------------------------------------------------------------ XYZZ
 template <class F>
 struct xyzz {
@@ -79,7 +88,7 @@ ZK_HD void xyzz_mdbl(xyzz<F>& p, const F& x, const F& y) {
   F x2 = fsqr(x);
   F m = fadd(fdbl(x2), x2);
   F x3 = fsub(fsub(fsqr(m), s), s);
-  F y3 = fsub(fmul(m, fsub(s, x3)), fmul(w, y));
+  F y3 = fmul_sub(m, fsub_m(s, x3), w, y);
   p.x = x3;
   p.y = y3;
   p.zz = v;
@@ -97,7 +106,7 @@ ZK_HD void xyzz_dbl(xyzz<F>& p) {
   F x2 = fsqr(p.x);
   F m = fadd(fdbl(x2), x2);
   F x3 = fsub(fsub(fsqr(m), s), s);
-  F y3 = fsub(fmul(m, fsub(s, x3)), fmul(w, p.y));
+  F y3 = fmul_sub(m, fsub_m(s, x3), w, p.y);
   p.x = x3;
   p.y = y3;
   p.zz = fmul(v, p.zz);
@@ -124,7 +133,7 @@ ZK_HD void xyzz_madd(xyzz<F>& p, const F& x2, const F& y2) {
   F ppp = fmul(P, pp);
   F q = fmul(p.x, pp);
   F x3 = fsub(fsub(fsqr(R), ppp), fdbl(q));
-  F y3 = fsub(fmul(R, fsub(q, x3)), fmul(p.y, ppp));
+  F y3 = fmul_sub(R, fsub_m(q, x3), p.y, ppp);
   p.x = x3;
   p.y = y3;
   p.zz = fmul(p.zz, pp);
@@ -154,7 +163,7 @@ ZK_HD void xyzz_add(xyzz<F>& p, const xyzz<F>& q) {
   F ppp = fmul(P, pp);
   F qq = fmul(u1, pp);
   F x3 = fsub(fsub(fsqr(R), ppp), fdbl(qq));
-  F y3 = fsub(fmul(R, fsub(qq, x3)), fmul(s1, ppp));
+  F y3 = fmul_sub(R, fsub_m(qq, x3), s1, ppp);
   p.x = x3;
   p.y = y3;
   p.zz = fmul(fmul(p.zz, q.zz), pp);

@@ -131,6 +131,42 @@ ZK_HD fe<P> fmul(const fe<P>& a, const fe<P>& b) {
   return r;
 }
 
+// (a*b + c*e) * 2^-261 mod m with one Montgomery reduction for both
+// products.  Inputs: normalized limbs (< 2^29), values < 4m; then every
+// column holds at most 27 products below 2^58 plus a carry below 2^35, which
+// stays below 2^64, and the result is below 32m^2 / 2^261 + m < 2m.
+template <class P>
+ZK_HD fe<P> fmul2(const fe<P>& a, const fe<P>& b, const fe<P>& c, const fe<P>& e) {
+  uint32_t q[NL];
+  fe<P> r;
+  uint64_t acc = 0;
+#pragma unroll
+  for (int k = 0; k < 2 * NL - 1; k++) {
+#pragma unroll
+    for (int i = 0; i < NL; i++) {
+      const int j = k - i;
+      if (j >= 0 && j < NL) {
+        acc += (uint64_t)a.l[i] * b.l[j];
+        acc += (uint64_t)c.l[i] * e.l[j];
+      }
+    }
+#pragma unroll
+    for (int i = 0; i < NL; i++) {
+      const int j = k - i;
+      if (i < k && j >= 1 && j < NL) acc += (uint64_t)q[i] * P::MOD[j];
+    }
+    if (k < NL) {
+      q[k] = ((uint32_t)acc * P::INV) & LMASK;
+      acc += (uint64_t)q[k] * P::MOD[0];
+    } else {
+      r.l[k - NL] = (uint32_t)acc & LMASK;
+    }
+    acc >>= 29;
+  }
+  r.l[NL - 1] = (uint32_t)acc;
+  return r;
+}
+
 // Squaring: cross products are summed once and doubled per column.
 template <class P>
 ZK_HD fe<P> fsqr(const fe<P>& a) {
@@ -206,6 +242,36 @@ ZK_HD fe<P> fsub(const fe<P>& a, const fe<P>& b) {
     uint32_t v = d.l[i] + (P::MOD2[i] & mask) + c;
     c = v >> 29;
     d.l[i] = v & LMASK;
+  }
+  return d;
+}
+
+// a - b + 2m without the final correction: value in (0, 4m) for a, b in
+// [0, 2m), normalized limbs.  Valid only as a multiplication input.
+template <class P>
+ZK_HD fe<P> fsub_lazy(const fe<P>& a, const fe<P>& b) {
+  fe<P> d;
+  int32_t c = 0;
+#pragma unroll
+  for (int i = 0; i < NL; i++) {
+    int32_t v = (int32_t)a.l[i] + (int32_t)P::MOD2[i] - (int32_t)b.l[i] + c;
+    c = v >> 29;
+    d.l[i] = (uint32_t)v & LMASK;
+  }
+  return d;
+}
+
+// 2m - a for a in [0, 2m]: value in [0, 2m], normalized limbs (congruent to
+// -a; not reduced, so a valid multiplication input only).
+template <class P>
+ZK_HD fe<P> fneg_lazy(const fe<P>& a) {
+  fe<P> d;
+  int32_t c = 0;
+#pragma unroll
+  for (int i = 0; i < NL; i++) {
+    int32_t v = (int32_t)P::MOD2[i] - (int32_t)a.l[i] + c;
+    c = v >> 29;
+    d.l[i] = (uint32_t)v & LMASK;
   }
   return d;
 }

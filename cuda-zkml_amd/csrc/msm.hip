@@ -7,22 +7,26 @@
 //
 //  1. convert    points -> internal records (29-bit limbs, radix 2^261), once.
 //  2. digits     scalar -> standard form; if s > (r-1)/2 use r - s and -P;
-//                signed c-bit digits d_w in [-2^(c-1), 2^(c-1)]; one
-//                (key = w<<c | |d_w|, value = point | sign<<31) per window,
-//                key SKIP for d_w = 0.
-//  3. sort       rocPRIM radix sort of the W*n (key, value) pairs.
-//  4. bounds     [start, end) of every key in the sorted order, and the count
-//                of real entries (SKIP keys sort last).
-//  5. accumulate every thread sums exactly L0 consecutive sorted entries
+//                signed c-bit digits d_w in [-2^(c-1), 2^(c-1)], stored as
+//                |d_w| | sign<<31 per (window, point); d_w = 0 is skipped.
+//  3. sort       counting sort by bucket (w, |d_w|), per window: LDS
+//                histograms per (window, slice of points), a column scan
+//                over slices and a per-window scan give every bucket its
+//                [start, end) in a window-major array (window w owns the
+//                region [w*n_pad, w*n_pad + n_pad)); a scatter pass with LDS
+//                cursors writes (bucket, point | sign<<31) pairs.  The order
+//                inside a bucket is arbitrary, which cannot change the sum.
+//  4. accumulate every thread sums exactly L0 consecutive sorted entries
 //                with mixed XYZZ additions (perfect load balance whatever the
 //                bucket sizes); runs that cross a chunk edge leave a head /
 //                tail partial.
-//  6. combine    log-depth tree over the chunk partials of each bucket that
+//  5. combine    log-depth tree over the chunk partials of each bucket that
 //                spans chunks (one level for ordinary buckets, ~log2(size/L0)
 //                levels for hot buckets such as many scalars equal to 1).
-//  7. reduce     sum_b b*S_b per window: G-bucket segments with running sums
-//                plus (segment offset)*run, then an LDS tree per 256 segments.
-//  8. host       remaining per-window partials are summed and combined with
+//  6. reduce     sum_b b*S_b per window: G-bucket segments with running sums
+//                plus (segment offset)*run, then LDS scans and trees per
+//                group of T segments and per window.
+//  7. host       remaining per-window partials are summed and combined with
 //                W*c doublings on the CPU (serial chain: a CPU core beats a
 //                lone wave64 by an order of magnitude on it).
 #include <string.h>
@@ -37,8 +41,15 @@
 namespace zk {
 
 constexpr uint32_t KEY_INVALID = 0xffffffffu;
-constexpr int MSM_L0 = 64;         // sorted entries per accumulation thread
-constexpr int MSM_G = 8;           // buckets per reduction thread
+constexpr int MSM_L0 = 64;         // sorted entries per accumulation thread (largest)
+constexpr int MSM_CMAX = 16;       // widest window: 2^15 LDS counters (128 KB)
+constexpr int SORT_T = 1024;       // threads of the histogram / scatter blocks
+constexpr int SORT_U = 8;          // loads in flight per thread in the sort passes
+constexpr int SCAN_T = 128;        // buckets per column-scan block (<= the smallest B)
+constexpr size_t MSM_MAX_N = (size_t)1 << 26;  // keeps W * n_pad below 2^32
+// Bits covered by the windows.  After the optional negation s <= (r-1)/2 <
+// 2^253, and signed digits need one more bit for the final carry.
+constexpr int MSM_BITS = 254;
 
 // ------------------------------------------------------------------ point records
 // G1 record: x[9], y[9], inf, pad  (80 bytes);  G2 record: x0,x1,y0,y1 [9 each],
@@ -148,8 +159,15 @@ __constant__ uint32_t HALF_R[8] = {0xf8000000u, 0xa1f0fac9u, 0x3cdcb848u, 0x9419
 __constant__ uint32_t R_WORDS[8] = {0xf0000001u, 0x43e1f593u, 0x79b97091u, 0x2833e848u,
                                     0x8181585du, 0xb85045b6u, 0xe131a029u, 0x30644e72u};
 
-__global__ void k_msm_digits(uint32_t* __restrict__ keys, uint32_t* __restrict__ vals,
-                             const uint4* __restrict__ scalars, size_t n, int c, int W) {
+// W windows cover MSM_BITS bits; the first MSM_BITS % W are one bit wider than
+// the rest, so no window is left with a few top bits only (a window of k bits
+// has 2^(k-1) buckets: a narrow top window would pile its entries into few,
+// very large buckets).
+__host__ __device__ __forceinline__ int window_width(int w, int W) {
+  return MSM_BITS / W + (w < MSM_BITS % W ? 1 : 0);
+}
+
+__global__ void k_msm_digits(uint32_t* __restrict__ dig, const uint4* __restrict__ scalars, size_t n, int W) {
   size_t i = blockIdx.x * (size_t)blockDim.x + threadIdx.x;
   if (i >= n) return;
   uint4 a = scalars[2 * i], b = scalars[2 * i + 1];
@@ -178,60 +196,186 @@ __global__ void k_msm_digits(uint32_t* __restrict__ keys, uint32_t* __restrict__
     }
     neg = 1;
   }
-  const uint32_t mask = (1u << c) - 1u, half = 1u << (c - 1);
-  const uint32_t skip = (uint32_t)W << c;
   uint32_t carry = 0;
+  int bit = 0;
   for (int w = 0; w < W; w++) {
-    const int bit = w * c, wd = bit >> 5, sh = bit & 31;
+    const int cw = window_width(w, W);
+    const uint32_t mask = (1u << cw) - 1u, half = 1u << (cw - 1);
+    const int wd = bit >> 5, sh = bit & 31;
     uint64_t v = wd < 8 ? s[wd] : 0;
     if (wd + 1 < 8) v |= (uint64_t)s[wd + 1] << 32;
     uint32_t d = ((uint32_t)(v >> sh) & mask) + carry;
     uint32_t sign = neg;
     if (d > half) {
-      d = (1u << c) - d;
+      d = (1u << cw) - d;
       carry = 1;
       sign ^= 1u;
     } else {
       carry = 0;
     }
-    const size_t o = (size_t)w * n + i;
-    if (d == 0) {
-      keys[o] = skip;
-      vals[o] = 0;
-    } else {
-      keys[o] = ((uint32_t)w << c) | d;
-      vals[o] = (uint32_t)i | (sign << 31);
+    dig[(size_t)w * n + i] = d == 0 ? 0u : (d | (sign << 31));
+    bit += cw;
+  }
+}
+
+// ------------------------------------------------------------------ counting sort
+// Bucket b in [0, B) of window w holds the entries with |d_w| = b + 1; its
+// global key is w*B + b.  Slices: window w's points are cut into S slices of
+// `slice` points; block (s, w) owns one.
+
+// Per-(window, slice) histogram -> H[(w*S + s)*B + b].
+template <int BMAX>
+__global__ __launch_bounds__(SORT_T) void k_msm_hist(const uint32_t* __restrict__ dig, size_t n, uint32_t slice,
+                                                     uint32_t S, uint32_t B, uint32_t* __restrict__ H) {
+  __shared__ uint32_t h[BMAX];
+  const uint32_t s = blockIdx.x, w = blockIdx.y, t = threadIdx.x;
+  for (uint32_t i = t; i < B; i += SORT_T) h[i] = 0;
+  __syncthreads();
+  const size_t lo = (size_t)s * slice, hi = min(n, lo + slice);
+  const uint32_t* d = dig + (size_t)w * n;
+  for (size_t p0 = lo + t; p0 < hi; p0 += (size_t)SORT_T * SORT_U) {
+    uint32_t v[SORT_U];
+#pragma unroll
+    for (int u = 0; u < SORT_U; u++) {
+      const size_t p = p0 + (size_t)u * SORT_T;
+      v[u] = p < hi ? d[p] : 0u;
+    }
+#pragma unroll
+    for (int u = 0; u < SORT_U; u++) {
+      const uint32_t m = v[u] & 0x7fffffffu;
+      if (m) atomicAdd(&h[m - 1], 1u);
     }
   }
+  __syncthreads();
+  uint32_t* out = H + ((size_t)w * S + s) * B;
+  for (uint32_t i = t; i < B; i += SORT_T) out[i] = h[i];
 }
 
-// ------------------------------------------------------------------ bounds
-// stat[0] = number of non-SKIP entries, stat[1] = longest run.
-__global__ void k_msm_bounds(const uint32_t* __restrict__ sk, size_t total, uint32_t skip, uint32_t* __restrict__ start,
-                             uint32_t* __restrict__ end, uint32_t* __restrict__ stat) {
-  size_t p = blockIdx.x * (size_t)blockDim.x + threadIdx.x;
-  if (p >= total) return;
-  const uint32_t k = sk[p];
-  const bool first = p == 0 || sk[p - 1] != k;
-  const bool last = p + 1 == total || sk[p + 1] != k;
-  if (k == skip) {
-    if (first) stat[0] = (uint32_t)p;
-    return;
+// Column scan over slices, one thread per bucket k = w*B + b, blocks of
+// SCAN_T consecutive buckets (B >= SCAN_T, so a block never spans windows):
+//  - H becomes the exclusive prefix over s of every bucket's counts;
+//  - tot[k] = bucket size, lex[k] = exclusive prefix of tot inside the block;
+//  - bsum/bmax[block] = the block's entry count and largest bucket.
+__global__ __launch_bounds__(SCAN_T) void k_msm_colscan(uint32_t* __restrict__ H, uint32_t S, uint32_t B,
+                                                        uint32_t* __restrict__ tot, uint32_t* __restrict__ lex,
+                                                        uint32_t* __restrict__ bsum, uint32_t* __restrict__ bmax) {
+  __shared__ uint32_t wsum[SCAN_T / 64], wmx[SCAN_T / 64];
+  const uint32_t t = threadIdx.x, lane = t & 63, wv = t >> 6;
+  const uint32_t k = blockIdx.x * SCAN_T + t;
+  const uint32_t w = k / B, b = k % B;
+  uint32_t acc = 0;
+  uint32_t* col = H + (size_t)w * S * B + b;
+  for (uint32_t s0 = 0; s0 < S; s0 += SORT_U) {
+    uint32_t v[SORT_U];
+#pragma unroll
+    for (int u = 0; u < SORT_U; u++) v[u] = s0 + u < S ? col[(size_t)(s0 + u) * B] : 0u;
+#pragma unroll
+    for (int u = 0; u < SORT_U; u++)
+      if (s0 + u < S) {
+        col[(size_t)(s0 + u) * B] = acc;
+        acc += v[u];
+      }
   }
-  if (first) start[k] = (uint32_t)p;
-  if (last) {
-    end[k] = (uint32_t)(p + 1);
-    if (p + 1 == total) stat[0] = (uint32_t)total;
+  tot[k] = acc;
+  uint32_t inc = acc, mx = acc;
+  for (int off = 1; off < 64; off <<= 1) {
+    const uint32_t o = (uint32_t)__shfl_up((int)inc, off);
+    if (lane >= (uint32_t)off) inc += o;
+  }
+  for (int off = 32; off >= 1; off >>= 1) mx = max(mx, (uint32_t)__shfl_xor((int)mx, off));
+  if (lane == 63) wsum[wv] = inc;
+  if (lane == 0) wmx[wv] = mx;
+  __syncthreads();
+  uint32_t base = 0, total = 0, m = 0;
+#pragma unroll
+  for (int v = 0; v < SCAN_T / 64; v++) {
+    if ((uint32_t)v < wv) base += wsum[v];
+    total += wsum[v];
+    m = max(m, wmx[v]);
+  }
+  lex[k] = base + inc - acc;
+  if (t == 0) {
+    bsum[blockIdx.x] = total;
+    bmax[blockIdx.x] = m;
   }
 }
 
-// longest run, after bounds are complete; one atomic per wave
-__global__ void k_msm_maxrun(const uint32_t* __restrict__ start, const uint32_t* __restrict__ end, size_t nkeys,
-                             uint32_t* __restrict__ stat) {
-  size_t k = blockIdx.x * (size_t)blockDim.x + threadIdx.x;
-  uint32_t len = k < nkeys ? end[k] - start[k] : 0;
-  for (int off = 32; off >= 1; off >>= 1) len = max(len, (uint32_t)__shfl_xor((int)len, off));
-  if ((threadIdx.x & 63) == 0 && len > 1) atomicMax(&stat[1], len);
+// Per window (one block of nb = B / SCAN_T <= 256 threads): exclusive scan of
+// the block sums -> boff; wstat[2w] = entries of window w, wstat[2w+1] = its
+// largest bucket.
+__global__ __launch_bounds__(256) void k_msm_bscan(const uint32_t* __restrict__ bsum, const uint32_t* __restrict__ bmax,
+                                                   uint32_t nb, uint32_t* __restrict__ boff,
+                                                   uint32_t* __restrict__ wstat) {
+  __shared__ uint32_t wsum[4], wmx[4];
+  const uint32_t w = blockIdx.x, t = threadIdx.x, lane = t & 63, wv = t >> 6;
+  const uint32_t v = t < nb ? bsum[w * nb + t] : 0u;
+  uint32_t mx = t < nb ? bmax[w * nb + t] : 0u;
+  uint32_t inc = v;
+  for (int off = 1; off < 64; off <<= 1) {
+    const uint32_t o = (uint32_t)__shfl_up((int)inc, off);
+    if (lane >= (uint32_t)off) inc += o;
+  }
+  for (int off = 32; off >= 1; off >>= 1) mx = max(mx, (uint32_t)__shfl_xor((int)mx, off));
+  if (lane == 63) wsum[wv] = inc;
+  if (lane == 0) wmx[wv] = mx;
+  __syncthreads();
+  uint32_t base = 0, total = 0, m = 0;
+  for (uint32_t u = 0; u < 4; u++) {
+    if (u < wv) base += wsum[u];
+    total += wsum[u];
+    m = max(m, wmx[u]);
+  }
+  if (t < nb) boff[w * nb + t] = base + inc - v;
+  if (t == 0) {
+    wstat[2 * w] = total;
+    wstat[2 * w + 1] = m;
+  }
+}
+
+// Scatter: LDS cursors = bucket start + slice prefix, one LDS atomic per
+// entry; out[pos] = (key, point | sign<<31).  Bucket start = w*n_pad +
+// boff[k / SCAN_T] + lex[k]; the blocks of slice 0 also store start/end.
+template <int BMAX>
+__global__ __launch_bounds__(SORT_T) void k_msm_scatter(const uint32_t* __restrict__ dig, size_t n, uint32_t slice,
+                                                        uint32_t S, uint32_t B, uint32_t n_pad,
+                                                        const uint32_t* __restrict__ H,
+                                                        const uint32_t* __restrict__ boff,
+                                                        const uint32_t* __restrict__ lex,
+                                                        const uint32_t* __restrict__ tot,
+                                                        uint32_t* __restrict__ start, uint32_t* __restrict__ end,
+                                                        uint2* __restrict__ out) {
+  __shared__ uint32_t cur[BMAX];
+  const uint32_t s = blockIdx.x, w = blockIdx.y, t = threadIdx.x;
+  const uint32_t* hp = H + ((size_t)w * S + s) * B;
+  for (uint32_t i = t; i < B; i += SORT_T) {
+    const uint32_t k = w * B + i;
+    const uint32_t st = w * n_pad + boff[k / SCAN_T] + lex[k];
+    cur[i] = st + hp[i];
+    if (s == 0) {
+      start[k] = st;
+      end[k] = st + tot[k];
+    }
+  }
+  __syncthreads();
+  const size_t lo = (size_t)s * slice, hi = min(n, lo + slice);
+  const uint32_t* d = dig + (size_t)w * n;
+  const uint32_t kb = w * B - 1;
+  for (size_t p0 = lo + t; p0 < hi; p0 += (size_t)SORT_T * SORT_U) {
+    uint32_t v[SORT_U];
+#pragma unroll
+    for (int u = 0; u < SORT_U; u++) {
+      const size_t p = p0 + (size_t)u * SORT_T;
+      v[u] = p < hi ? d[p] : 0u;
+    }
+#pragma unroll
+    for (int u = 0; u < SORT_U; u++) {
+      const uint32_t m = v[u] & 0x7fffffffu;
+      if (m) {
+        const uint32_t pos = atomicAdd(&cur[m - 1], 1u);
+        out[pos] = make_uint2(kb + m, (uint32_t)(p0 + (size_t)u * SORT_T) | (v[u] & 0x80000000u));
+      }
+    }
+  }
 }
 
 // ------------------------------------------------------------------ accumulate
@@ -243,42 +387,42 @@ struct ChunkSlots {
   xyzz<F>* tpt;
 };
 
+// Chunk ch covers sorted positions [ch*L0, ch*L0 + L0) of window
+// ch / chunks_per_window; positions past the window's entry count are empty.
 template <class F>
-__device__ __forceinline__ uint32_t bucket_id(uint32_t key, int c) {
-  return (key >> c) * (1u << (c - 1)) + (key & ((1u << c) - 1u)) - 1u;
-}
-
-template <class F>
-__global__ __launch_bounds__(256) void k_msm_accumulate(const uint32_t* __restrict__ sk, const uint32_t* __restrict__ sv,
+__global__ __launch_bounds__(256) void k_msm_accumulate(const uint2* __restrict__ sorted,
                                                         const uint4* __restrict__ recs,
                                                         const uint32_t* __restrict__ start,
                                                         const uint32_t* __restrict__ end,
-                                                        const uint32_t* __restrict__ stat, uint32_t nchunks, int c,
+                                                        const uint32_t* __restrict__ wstat, uint32_t nchunks,
+                                                        uint32_t chunks_per_window, uint32_t n_pad, uint32_t L0,
                                                         xyzz<F>* __restrict__ buckets, ChunkSlots<F> slots) {
   const uint32_t ch = blockIdx.x * blockDim.x + threadIdx.x;
   if (ch >= nchunks) return;
-  const uint32_t total = stat[0];
-  const uint32_t lo = ch * MSM_L0;
+  const uint32_t w = ch / chunks_per_window;
+  const uint32_t total = w * n_pad + wstat[2 * w];
+  const uint32_t lo = ch * L0;
   uint32_t hk = KEY_INVALID, tk = KEY_INVALID;
   if (lo < total) {
-    const uint32_t hi = min(lo + (uint32_t)MSM_L0, total);
+    const uint32_t hi = min(lo + L0, total);
     xyzz<F> acc;
     xyzz_set_inf(acc);
-    uint32_t cur = sk[lo];
+    uint32_t cur = sorted[lo].x;
     for (uint32_t p = lo; p < hi; p++) {
-      const uint32_t key = sk[p];
+      const uint2 e = sorted[p];
+      const uint32_t key = e.x;
       if (key != cur) {
         // run `cur` ended inside the chunk
         if (start[cur] < lo) {
           hk = cur;
           slots.hpt[ch] = acc;
         } else {
-          buckets[bucket_id<F>(cur, c)] = acc;
+          buckets[cur] = acc;
         }
         cur = key;
         xyzz_set_inf(acc);
       }
-      const uint32_t v = sv[p];
+      const uint32_t v = e.y;
       F x, y;
       if (!load_rec(recs, v & 0x7fffffffu, x, y)) {
         if (v >> 31) y = fneg(y);
@@ -287,8 +431,8 @@ __global__ __launch_bounds__(256) void k_msm_accumulate(const uint32_t* __restri
     }
     // last run of the chunk
     const uint32_t rs = start[cur], re = end[cur];
-    if (rs >= lo && re <= lo + (uint32_t)MSM_L0) {
-      buckets[bucket_id<F>(cur, c)] = acc;
+    if (rs >= lo && re <= lo + L0) {
+      buckets[cur] = acc;
     } else if (rs < lo) {
       hk = cur;
       slots.hpt[ch] = acc;
@@ -305,29 +449,29 @@ __global__ __launch_bounds__(256) void k_msm_accumulate(const uint32_t* __restri
 template <class F>
 __global__ __launch_bounds__(256) void k_msm_combine(ChunkSlots<F> slots, const uint32_t* __restrict__ start,
                                                      const uint32_t* __restrict__ end, uint32_t nchunks,
-                                                     uint32_t step) {
+                                                     uint32_t L0, uint32_t step) {
   const uint32_t ch = blockIdx.x * blockDim.x + threadIdx.x;
   if (ch >= nchunks) return;
   const uint32_t tk = slots.tkey[ch];
   if (tk != KEY_INVALID) {
-    const uint32_t c1 = (end[tk] - 1) / MSM_L0;
+    const uint32_t c1 = (end[tk] - 1) / L0;
     if (ch + step <= c1) xyzz_add(slots.tpt[ch], slots.hpt[ch + step]);
   }
   const uint32_t hk = slots.hkey[ch];
   if (hk != KEY_INVALID) {
-    const uint32_t c0 = start[hk] / MSM_L0, c1 = (end[hk] - 1) / MSM_L0;
+    const uint32_t c0 = start[hk] / L0, c1 = (end[hk] - 1) / L0;
     const uint32_t j = ch - c0;
     if ((j % (2 * step)) == 0 && ch + step <= c1) xyzz_add(slots.hpt[ch], slots.hpt[ch + step]);
   }
 }
 
 template <class F>
-__global__ __launch_bounds__(256) void k_msm_finalize(ChunkSlots<F> slots, uint32_t nchunks, int c,
+__global__ __launch_bounds__(256) void k_msm_finalize(ChunkSlots<F> slots, uint32_t nchunks,
                                                       xyzz<F>* __restrict__ buckets) {
   const uint32_t ch = blockIdx.x * blockDim.x + threadIdx.x;
   if (ch >= nchunks) return;
   const uint32_t tk = slots.tkey[ch];
-  if (tk != KEY_INVALID) buckets[bucket_id<F>(tk, c)] = slots.tpt[ch];
+  if (tk != KEY_INVALID) buckets[tk] = slots.tpt[ch];
 }
 
 // ------------------------------------------------------------------ bucket reduction
@@ -344,9 +488,9 @@ __global__ __launch_bounds__(256) void k_msm_finalize(ChunkSlots<F> slots, uint3
 //   sum_b b S_b = sum_k P_k + T G sum_{s >= 1} SRUN_s,  same scan and tree.
 
 // Inclusive suffix scan over the T values held by the threads of a
-// workgroup; returns this thread's sum_{u >= t} v_u.
-template <class F, int T>
-__device__ __forceinline__ xyzz<F> wg_suffix_scan(xyzz<F> v, xyzz<F>* sh) {
+// workgroup (T = blockDim.x); returns this thread's sum_{u >= t} v_u.
+template <class F>
+__device__ __forceinline__ xyzz<F> wg_suffix_scan(xyzz<F> v, xyzz<F>* sh, int T) {
   const int t = threadIdx.x;
   sh[t] = v;
   __syncthreads();
@@ -364,8 +508,9 @@ __device__ __forceinline__ xyzz<F> wg_suffix_scan(xyzz<F> v, xyzz<F>* sh) {
   return v;
 }
 
-template <class F, int T>
-__device__ __forceinline__ xyzz<F> wg_sum(xyzz<F> v, xyzz<F>* sh) {
+// Sum of the T values of a workgroup (T a power of two), valid in thread 0.
+template <class F>
+__device__ __forceinline__ xyzz<F> wg_sum(xyzz<F> v, xyzz<F>* sh, int T) {
   const int t = threadIdx.x;
   __syncthreads();
   sh[t] = v;
@@ -380,37 +525,39 @@ __device__ __forceinline__ xyzz<F> wg_sum(xyzz<F> v, xyzz<F>* sh) {
   return v;
 }
 
-template <class F, int T>
-__global__ __launch_bounds__(T) void k_msm_reduce1(const xyzz<F>* __restrict__ buckets,
-                                                   const uint32_t* __restrict__ start,
-                                                   const uint32_t* __restrict__ end, int c, uint32_t K,
-                                                   xyzz<F>* __restrict__ P, xyzz<F>* __restrict__ RUN) {
-  __shared__ xyzz<F> sh[T];
-  const uint32_t B1 = 1u << (c - 1);
+// Level 1: block k of window w (blockIdx.x = w*K + k), T = blockDim.x threads
+// of G buckets each (G = 2^log2g).
+template <class F, int TMAX>
+__global__ __launch_bounds__(TMAX) void k_msm_reduce1(const xyzz<F>* __restrict__ buckets,
+                                                      const uint32_t* __restrict__ start,
+                                                      const uint32_t* __restrict__ end, uint32_t B1, uint32_t K,
+                                                      int log2g, xyzz<F>* __restrict__ P, xyzz<F>* __restrict__ RUN) {
+  __shared__ xyzz<F> sh[TMAX];
+  const int T = blockDim.x, G = 1 << log2g;
   const uint32_t w = blockIdx.x / K, k = blockIdx.x % K;
   const uint32_t t = threadIdx.x;
-  const uint32_t b0 = k * T * MSM_G + t * MSM_G;  // bucket index offset of this thread
+  const uint32_t kb = w * B1 + (k * T + t) * G;  // key of this thread's first bucket
   xyzz<F> run, acc;
   xyzz_set_inf(run);
   xyzz_set_inf(acc);
-  for (int i = MSM_G; i >= 1; i--) {
-    const uint32_t b = b0 + i;
-    const uint32_t key = (w << c) | b;
-    if (end[key] > start[key]) xyzz_add(run, buckets[w * B1 + b - 1]);
+  for (int i = G - 1; i >= 0; i--) {
+    const uint32_t key = kb + i;
+    if (end[key] > start[key]) xyzz_add(run, buckets[key]);
     xyzz_add(acc, run);
   }
-  xyzz<F> sr = wg_suffix_scan<F, T>(run, sh);
+  xyzz<F> sr = wg_suffix_scan<F>(run, sh, T);
   if (t >= 1) {
-    for (int d = 1; d < MSM_G; d <<= 1) xyzz_dbl(sr);
+    for (int d = 0; d < log2g; d++) xyzz_dbl(sr);
     xyzz_add(acc, sr);
   } else {
     RUN[blockIdx.x] = sr;  // thread 0 holds the group total
   }
-  xyzz<F> tot = wg_sum<F, T>(acc, sh);
+  xyzz<F> tot = wg_sum<F>(acc, sh, T);
   if (t == 0) P[blockIdx.x] = tot;
 }
 
-// One workgroup of K threads per window; log2tg = log2(T*G).
+// Level 2: one workgroup per window over its K group results (blockDim.x a
+// power of two >= K); log2tg = log2(T*G) of level 1.
 template <class F, int KMAX>
 __global__ __launch_bounds__(KMAX) void k_msm_reduce2(const xyzz<F>* __restrict__ P, const xyzz<F>* __restrict__ RUN,
                                                       uint32_t K, int log2tg, xyzz<F>* __restrict__ out) {
@@ -423,46 +570,45 @@ __global__ __launch_bounds__(KMAX) void k_msm_reduce2(const xyzz<F>* __restrict_
     run = RUN[w * K + t];
     acc = P[w * K + t];
   }
-  xyzz<F> sr = wg_suffix_scan<F, KMAX>(run, sh);
+  xyzz<F> sr = wg_suffix_scan<F>(run, sh, blockDim.x);
   if (t >= 1 && t < K) {
     for (int d = 0; d < log2tg; d++) xyzz_dbl(sr);
     xyzz_add(acc, sr);
   }
-  xyzz<F> tot = wg_sum<F, KMAX>(acc, sh);
+  xyzz<F> tot = wg_sum<F>(acc, sh, blockDim.x);
   if (t == 0) out[w] = tot;
 }
 
 // ------------------------------------------------------------------ workspace
 struct MsmWorkspace {
-  DevBuf recs, keys_in, vals_in, keys_out, vals_out, sort_tmp, start, end, stat, buckets, hkey, tkey, hpt, tpt, seg,
+  DevBuf recs, dig, hist, tot, lex, bsum, bmax, boff, sorted, start, end, wstat, buckets, hkey, tkey, hpt, tpt, seg,
       grp, win;
-  uint32_t* h_stat = nullptr;  // pinned
+  uint32_t* h_stat = nullptr;  // pinned, 2 words per window
+  hipEvent_t stat_ready = nullptr;
 };
 
 void msm_workspace_free(MsmWorkspace* ws) {
   if (!ws) return;
-  for (DevBuf* b : {&ws->recs, &ws->keys_in, &ws->vals_in, &ws->keys_out, &ws->vals_out, &ws->sort_tmp, &ws->start,
-                    &ws->end, &ws->stat, &ws->buckets, &ws->hkey, &ws->tkey, &ws->hpt, &ws->tpt, &ws->seg, &ws->grp,
-                    &ws->win})
+  for (DevBuf* b : {&ws->recs, &ws->dig, &ws->hist, &ws->tot, &ws->lex, &ws->bsum, &ws->bmax, &ws->boff,
+                    &ws->sorted, &ws->start, &ws->end, &ws->wstat, &ws->buckets, &ws->hkey, &ws->tkey, &ws->hpt,
+                    &ws->tpt, &ws->seg, &ws->grp, &ws->win})
     if (b->p) (void)hipFree(b->p);
   if (ws->h_stat) (void)hipHostFree(ws->h_stat);
+  if (ws->stat_ready) (void)hipEventDestroy(ws->stat_ready);
   delete ws;
 }
 
-// Window size minimizing W(c) * (n + 1.5 * 2^c) additions (accumulation plus
-// bucket reduction), with W(c) = ceil(254 / c) signed windows.
-static int choose_c(size_t n) {
-  int best = 8;
-  double bestv = 1e300;
-  for (int c = 8; c <= 18; c++) {
-    const int W = (254 + c - 1) / c;
-    const double v = (double)W * ((double)n + 1.5 * (double)(1u << c));
-    if (v < bestv) {
-      bestv = v;
-      best = c;
-    }
-  }
-  return best;
+// Window size by input size (index: ceil(log2 n)), from measurements on
+// gfx950 with uniform scalars.  Below ~2^19 points the accumulation and the
+// bucket reduction are latency-bound, so fewer buckets pay off well beyond
+// what operation counts suggest; G2 operations are ~3x longer still.
+static int choose_c(size_t n, bool g2) {
+  int lg = 0;
+  while (((size_t)1 << lg) < n) lg++;
+  static const int g1_table[20] = {8, 8, 8, 8, 8, 8, 8, 8, 8, 8, 8, 8, 8, 9, 9, 10, 11, 12, 13, 14};
+  static const int g2_table[20] = {8, 8, 8, 8, 8, 8, 8, 8, 8, 8, 8, 8, 8, 9, 9, 9, 10, 12, 13, 14};
+  if (lg >= 20) return MSM_CMAX;
+  return g2 ? g2_table[lg] : g1_table[lg];
 }
 
 // ------------------------------------------------------------------ host tail
@@ -501,7 +647,7 @@ struct HostSide<fq2> {
 // XYZZ partials (device layout, copied to the host) -> affine via one batch
 // inversion -> per-window sums -> Horner over windows.
 template <class F>
-static void host_finish(const std::vector<xyzz<F>>& parts, int W, int per_w, int c, uint64_t* out) {
+static void host_finish(const std::vector<xyzz<F>>& parts, int W, int per_w, uint64_t* out) {
   typedef typename HostSide<F>::E E;
   typedef zkh::Jac<E> J;
   const size_t m = parts.size();
@@ -529,9 +675,9 @@ static void host_finish(const std::vector<xyzz<F>>& parts, int W, int per_w, int
     const int w = (int)(i / per_w);
     win[w] = win[w].add(J::affine(x, y));
   }
-  J r = J::inf();
-  for (int w = W - 1; w >= 0; w--) {
-    for (int k = 0; k < c; k++) r = r.dbl();
+  J r = win[W - 1];
+  for (int w = W - 2; w >= 0; w--) {
+    for (int k = 0; k < window_width(w, W); k++) r = r.dbl();
     r = r.add(win[w]);
   }
   E ax, ay;
@@ -547,102 +693,122 @@ static int msm_run_recs(zk_context* ctx, MsmWorkspace& ws, const uint4* recs, co
   constexpr int OUTW = sizeof(F) == sizeof(fq) ? 8 : 16;
   memset(out, 0, OUTW * 8);
   if (n == 0) return ZK_OK;
-  const int c = choose_c(n);
-  const int W = (254 + c - 1) / c;
-  const size_t total = (size_t)W * n;
-  const size_t nkeys = ((size_t)W + 1) << c;
-  const size_t nbuckets = (size_t)W << (c - 1);
-  const uint32_t nchunks = (uint32_t)((total + MSM_L0 - 1) / MSM_L0);
-  ZK_TRY(ctx->ensure(ws.keys_in, total * 4));
-  ZK_TRY(ctx->ensure(ws.vals_in, total * 4));
-  ZK_TRY(ctx->ensure(ws.keys_out, total * 4));
-  ZK_TRY(ctx->ensure(ws.vals_out, total * 4));
-  ZK_TRY(ctx->ensure(ws.start, nkeys * 4));
-  ZK_TRY(ctx->ensure(ws.end, nkeys * 4));
-  ZK_TRY(ctx->ensure(ws.stat, 16));
+  if (n > MSM_MAX_N) return ctx->fail(ZK_ERR_SIZE, "msm: n above 2^26");
+  constexpr bool G2 = sizeof(F) != sizeof(fq);
+  const int c = choose_c(n, G2);
+  const int W = (MSM_BITS + c - 1) / c;
+  const uint32_t B = 1u << (c - 1);  // buckets per window
+  const size_t nbuckets = (size_t)W * B;
+  // entries per accumulation thread: MSM_L0, halved below 2^23 entries so
+  // that small inputs still spread over enough threads (measured: shorter
+  // chunks deepen the chunk-combine tree and cost more than they save)
+  const uint32_t L0 = (size_t)W * n >= ((size_t)1 << 23) ? MSM_L0 : MSM_L0 / 2;
+  const uint32_t n_pad = (uint32_t)((n + L0 - 1) / L0 * L0);
+  const uint32_t cpw = n_pad / L0;  // chunks per window
+  const uint32_t nchunks = cpw * (uint32_t)W;
+  // slices per window: about 256 blocks, each slice at least B points
+  uint32_t S = (uint32_t)std::max<size_t>(1, std::min<size_t>({(size_t)cdiv(256, W), (size_t)64, n / B}));
+  const uint32_t slice = (uint32_t)cdiv(n, S);
+  ZK_TRY(ctx->ensure(ws.dig, (size_t)W * n * 4));
+  ZK_TRY(ctx->ensure(ws.hist, (size_t)W * S * B * 4));
+  ZK_TRY(ctx->ensure(ws.tot, nbuckets * 4));
+  ZK_TRY(ctx->ensure(ws.lex, nbuckets * 4));
+  ZK_TRY(ctx->ensure(ws.bsum, nbuckets / SCAN_T * 4));
+  ZK_TRY(ctx->ensure(ws.bmax, nbuckets / SCAN_T * 4));
+  ZK_TRY(ctx->ensure(ws.boff, nbuckets / SCAN_T * 4));
+  ZK_TRY(ctx->ensure(ws.sorted, (size_t)W * n_pad * 8));
+  ZK_TRY(ctx->ensure(ws.start, nbuckets * 4));
+  ZK_TRY(ctx->ensure(ws.end, nbuckets * 4));
+  ZK_TRY(ctx->ensure(ws.wstat, (size_t)W * 8));
   ZK_TRY(ctx->ensure(ws.buckets, nbuckets * sizeof(xyzz<F>)));
   ZK_TRY(ctx->ensure(ws.hkey, (size_t)nchunks * 4));
   ZK_TRY(ctx->ensure(ws.tkey, (size_t)nchunks * 4));
   ZK_TRY(ctx->ensure(ws.hpt, (size_t)nchunks * sizeof(xyzz<F>)));
   ZK_TRY(ctx->ensure(ws.tpt, (size_t)nchunks * sizeof(xyzz<F>)));
-  if (!ws.h_stat) ZK_HIP(ctx, hipHostMalloc((void**)&ws.h_stat, 16, hipHostMallocDefault));
+  if (!ws.h_stat) ZK_HIP(ctx, hipHostMalloc((void**)&ws.h_stat, 2 * 32 * 4, hipHostMallocDefault));
+  if (!ws.stat_ready) ZK_HIP(ctx, hipEventCreateWithFlags(&ws.stat_ready, hipEventDisableTiming));
 
-  uint32_t* kin = (uint32_t*)ws.keys_in.p;
-  uint32_t* vin = (uint32_t*)ws.vals_in.p;
-  uint32_t* kout = (uint32_t*)ws.keys_out.p;
-  uint32_t* vout = (uint32_t*)ws.vals_out.p;
+  uint32_t* dig = (uint32_t*)ws.dig.p;
+  uint32_t* hist = (uint32_t*)ws.hist.p;
+  uint32_t* tot = (uint32_t*)ws.tot.p;
+  uint32_t* lex = (uint32_t*)ws.lex.p;
+  uint32_t* bsum = (uint32_t*)ws.bsum.p;
+  uint32_t* bmax = (uint32_t*)ws.bmax.p;
+  uint32_t* boff = (uint32_t*)ws.boff.p;
+  uint2* sorted = (uint2*)ws.sorted.p;
   uint32_t* start = (uint32_t*)ws.start.p;
   uint32_t* end = (uint32_t*)ws.end.p;
-  uint32_t* stat = (uint32_t*)ws.stat.p;
+  uint32_t* wstat = (uint32_t*)ws.wstat.p;
   xyzz<F>* buckets = (xyzz<F>*)ws.buckets.p;
 
-  ZK_LAUNCH(ctx, st, "msm_digits", k_msm_digits, dim3(cdiv(n, 256)), dim3(256), 0, kin, vin,
-            (const uint4*)d_scalars, n, c, W);
-
-  const unsigned end_bit = 32 - __builtin_clz((unsigned)((W << c) | 1));
-  ZK_TRY(sort_pairs_u32(ctx, ws.sort_tmp, kin, kout, vin, vout, total, end_bit, st));
-
-  ZK_HIP(ctx, hipMemsetAsync(start, 0, nkeys * 4, st));
-  ZK_HIP(ctx, hipMemsetAsync(end, 0, nkeys * 4, st));
-  ZK_HIP(ctx, hipMemsetAsync(stat, 0, 16, st));
-  ZK_LAUNCH(ctx, st, "msm_bounds", k_msm_bounds, dim3(cdiv(total, 256)), dim3(256), 0, kout, total,
-            (uint32_t)(W << c), start, end, stat);
-  ZK_LAUNCH(ctx, st, "msm_bounds", k_msm_maxrun, dim3(cdiv(nkeys, 256)), dim3(256), 0, start, end, nkeys, stat);
-  ZK_HIP(ctx, hipMemcpyAsync(ws.h_stat, stat, 8, hipMemcpyDeviceToHost, st));
-  ZK_HIP(ctx, hipStreamSynchronize(st));
-  const uint32_t real = ws.h_stat[0];
-  const uint32_t maxrun = std::max(1u, ws.h_stat[1]);
+  ZK_LAUNCH(ctx, st, "msm_digits", k_msm_digits, dim3(cdiv(n, 256)), dim3(256), 0, dig, (const uint4*)d_scalars, n,
+            W);
+  if (B <= 4096) {
+    ZK_LAUNCH(ctx, st, "msm_hist", k_msm_hist<4096>, dim3(S, W), dim3(SORT_T), 0, dig, n, slice, S, B, hist);
+  } else {
+    ZK_LAUNCH(ctx, st, "msm_hist", k_msm_hist<32768>, dim3(S, W), dim3(SORT_T), 0, dig, n, slice, S, B, hist);
+  }
+  const uint32_t nb = B / SCAN_T;  // column-scan blocks per window
+  ZK_LAUNCH(ctx, st, "msm_scan", k_msm_colscan, dim3((uint32_t)(nbuckets / SCAN_T)), dim3(SCAN_T), 0, hist, S, B,
+            tot, lex, bsum, bmax);
+  ZK_LAUNCH(ctx, st, "msm_scan", k_msm_bscan, dim3(W), dim3(256), 0, bsum, bmax, nb, boff, wstat);
+  ZK_HIP(ctx, hipMemcpyAsync(ws.h_stat, wstat, (size_t)W * 8, hipMemcpyDeviceToHost, st));
+  ZK_HIP(ctx, hipEventRecord(ws.stat_ready, st));
+  if (B <= 4096) {
+    ZK_LAUNCH(ctx, st, "msm_scatter", k_msm_scatter<4096>, dim3(S, W), dim3(SORT_T), 0, dig, n, slice, S, B, n_pad,
+              hist, boff, lex, tot, start, end, sorted);
+  } else {
+    ZK_LAUNCH(ctx, st, "msm_scatter", k_msm_scatter<32768>, dim3(S, W), dim3(SORT_T), 0, dig, n, slice, S, B, n_pad,
+              hist, boff, lex, tot, start, end, sorted);
+  }
 
   ChunkSlots<F> slots{(uint32_t*)ws.hkey.p, (uint32_t*)ws.tkey.p, (xyzz<F>*)ws.hpt.p, (xyzz<F>*)ws.tpt.p};
-  const uint32_t used_chunks = std::max(1u, (real + MSM_L0 - 1) / MSM_L0);
-  ZK_LAUNCH(ctx, st, "msm_accumulate", k_msm_accumulate<F>, dim3(cdiv(used_chunks, 256)), dim3(256), 0, kout, vout,
-            recs, start, end, stat, used_chunks, c, buckets, slots);
-  // chunks spanned by the longest run
-  const uint32_t max_span = (maxrun + MSM_L0 - 2) / MSM_L0 + 1;
+  ZK_LAUNCH(ctx, st, "msm_accumulate", k_msm_accumulate<F>, dim3(cdiv(nchunks, 256)), dim3(256), 0, sorted, recs,
+            start, end, wstat, nchunks, cpw, n_pad, L0, buckets, slots);
+  // the largest bucket decides the depth of the chunk-combine tree; its
+  // read-back overlaps the accumulation
+  ZK_HIP(ctx, hipEventSynchronize(ws.stat_ready));
+  uint32_t maxrun = 1;
+  for (int w = 0; w < W; w++) maxrun = std::max(maxrun, ws.h_stat[2 * w + 1]);
+  const uint32_t max_span = (maxrun + L0 - 2) / L0 + 1;  // chunks spanned by the largest bucket
   for (uint32_t step = 1; step < max_span; step <<= 1)
-    ZK_LAUNCH(ctx, st, "msm_combine", k_msm_combine<F>, dim3(cdiv(used_chunks, 256)), dim3(256), 0, slots, start,
-              end, used_chunks, step);
-  ZK_LAUNCH(ctx, st, "msm_combine", k_msm_finalize<F>, dim3(cdiv(used_chunks, 256)), dim3(256), 0, slots,
-            used_chunks, c, buckets);
+    ZK_LAUNCH(ctx, st, "msm_combine", k_msm_combine<F>, dim3(cdiv(nchunks, 256)), dim3(256), 0, slots, start, end,
+              nchunks, L0, step);
+  ZK_LAUNCH(ctx, st, "msm_combine", k_msm_finalize<F>, dim3(cdiv(nchunks, 256)), dim3(256), 0, slots, nchunks,
+            buckets);
 
   // bucket reduction: level 1 (T threads x G buckets per group), level 2 per window
-  constexpr int T1 = sizeof(F) == sizeof(fq) ? 256 : 128;
-  const uint32_t B1 = 1u << (c - 1);
-  int t1 = (int)std::min<uint32_t>(T1, B1 / MSM_G);
-  const uint32_t K = B1 / (t1 * MSM_G);
+  constexpr int TMAX = sizeof(F) == sizeof(fq) ? 256 : 128;
+  constexpr int KMAX = 256;
+  // measured: T = TMAX; G = 8 for 2^15 buckets per window, else 4
+  int T1 = TMAX, log2g = B >= 32768 ? 3 : 2;
+  // shrink the group for small windows: T1 * G <= B
+  while (log2g > 0 && (T1 << log2g) > (int)B) log2g--;
+  while (T1 > 1 && (T1 << log2g) > (int)B) T1 >>= 1;
+  uint32_t K = B / ((uint32_t)T1 << log2g);
+  while (K > KMAX) {  // too many groups for level 2: widen the groups
+    log2g++;
+    K >>= 1;
+  }
+  if (T1 < 1 || T1 > TMAX || (T1 & (T1 - 1)) || K < 1 || (size_t)K * ((size_t)T1 << log2g) != B)
+    return ctx->fail(ZK_ERR_INVALID, "msm: unsupported reduction shape");
   ZK_TRY(ctx->ensure(ws.seg, (size_t)K * W * sizeof(xyzz<F>)));
   ZK_TRY(ctx->ensure(ws.grp, (size_t)K * W * sizeof(xyzz<F>)));
   ZK_TRY(ctx->ensure(ws.win, (size_t)W * sizeof(xyzz<F>)));
   xyzz<F>* Pk = (xyzz<F>*)ws.seg.p;
   xyzz<F>* RUNk = (xyzz<F>*)ws.grp.p;
   xyzz<F>* win = (xyzz<F>*)ws.win.p;
-  switch (t1) {
-#define ZK_R1(TT)                                                                                              \
-  case TT:                                                                                                     \
-    ZK_LAUNCH(ctx, st, "msm_reduce", (k_msm_reduce1<F, TT>), dim3(K * W), dim3(TT), 0, buckets, start, end, c, K, \
-              Pk, RUNk);                                                                                       \
-    break;
-    ZK_R1(256)
-    ZK_R1(128)
-    ZK_R1(64)
-    ZK_R1(32)
-    ZK_R1(16)
-#undef ZK_R1
-    default:
-      return ctx->fail(ZK_ERR_INVALID, "msm: unsupported reduction shape");
-  }
-  int log2tg = 0;
-  while ((1 << log2tg) < t1 * MSM_G) log2tg++;
-  if (K <= 32)
-    ZK_LAUNCH(ctx, st, "msm_reduce", (k_msm_reduce2<F, 32>), dim3(W), dim3(32), 0, Pk, RUNk, K, log2tg, win);
-  else if (K <= 128)
-    ZK_LAUNCH(ctx, st, "msm_reduce", (k_msm_reduce2<F, 128>), dim3(W), dim3(128), 0, Pk, RUNk, K, log2tg, win);
-  else
-    return ctx->fail(ZK_ERR_INVALID, "msm: too many reduction groups");
+  ZK_LAUNCH(ctx, st, "msm_reduce", (k_msm_reduce1<F, TMAX>), dim3(K * W), dim3(T1), 0, buckets, start, end, B, K,
+            log2g, Pk, RUNk);
+  int log2tg = log2g;
+  while ((1 << (log2tg - log2g)) < T1) log2tg++;
+  uint32_t k2 = 1;
+  while (k2 < K) k2 <<= 1;
+  ZK_LAUNCH(ctx, st, "msm_reduce2", (k_msm_reduce2<F, KMAX>), dim3(W), dim3(k2), 0, Pk, RUNk, K, log2tg, win);
   std::vector<xyzz<F>> parts((size_t)W);
   ZK_HIP(ctx, hipMemcpyAsync(parts.data(), win, parts.size() * sizeof(xyzz<F>), hipMemcpyDeviceToHost, st));
   ZK_HIP(ctx, hipStreamSynchronize(st));
-  host_finish<F>(parts, W, 1, c, out);
+  host_finish<F>(parts, W, 1, out);
   return ZK_OK;
 }
 
@@ -653,7 +819,7 @@ static int msm_run(zk_context* ctx, MsmWorkspace*& wsp, const void* d_points, co
   memset(out, 0, OUTW * 8);
   if (n == 0) return ZK_OK;
   if (!d_points || !d_scalars) return ctx->fail(ZK_ERR_INVALID, "msm: null buffer");
-  if (n > (1u << 28)) return ctx->fail(ZK_ERR_SIZE, "msm: n above 2^28");
+  if (n > MSM_MAX_N) return ctx->fail(ZK_ERR_SIZE, "msm: n above 2^26");
   if (!wsp) wsp = new MsmWorkspace();
   MsmWorkspace& ws = *wsp;
   ZK_TRY(ctx->ensure(ws.recs, n * Rec<F>::WORDS * 4));
@@ -740,6 +906,13 @@ int zk_msm_g1(zk_context* ctx, const void* d_points, const void* d_scalars, size
 int zk_msm_g2(zk_context* ctx, const void* d_points, const void* d_scalars, size_t n, void* h_result, void* stream) {
   if (!ctx || !h_result) return ZK_ERR_INVALID;
   return zk::msm_g2_run(ctx, d_points, d_scalars, n, (uint64_t*)h_result, ctx->s(stream));
+}
+
+int zk_msm_config(size_t n, int g2, int* window_bits, int* windows) {
+  if (!window_bits || !windows) return ZK_ERR_INVALID;
+  *window_bits = zk::choose_c(n, g2 != 0);
+  *windows = (zk::MSM_BITS + *window_bits - 1) / *window_bits;
+  return ZK_OK;
 }
 
 // Reference host structs: G1Affine = {Fp x, y; bool infinity} (72 bytes),

@@ -116,10 +116,6 @@ int recs_from_std(zk_context* ctx, bool g2, void* d_recs, const void* d_std, con
 size_t rec_bytes(bool g2);
 void msm_workspace_free(MsmWorkspace* ws);
 
-// ---- radix sort of (u32 key, u32 value) pairs on key bits [0, end_bit) (sort.hip)
-int sort_pairs_u32(zk_context* ctx, DevBuf& tmp, const uint32_t* kin, uint32_t* kout, const uint32_t* vin,
-                   uint32_t* vout, size_t n, unsigned end_bit, hipStream_t st);
-
 // ---- fixed base (pointgen.hip)
 int g1_generator_mul(zk_context* ctx, const void* d_scalars, size_t n, void* d_out, hipStream_t st);
 int g2_generator_mul(zk_context* ctx, const void* d_scalars, size_t n, void* d_out, hipStream_t st);

@@ -49,6 +49,8 @@ def lib():
         L.zk_coset_ntt.argtypes = [vp, vp, vp, ctypes.c_int, ctypes.c_uint64, ctypes.c_int, ctypes.c_int, vp]
         L.zk_msm_g1.argtypes = [vp, vp, vp, ctypes.c_size_t, vp, vp]
         L.zk_msm_g2.argtypes = [vp, vp, vp, ctypes.c_size_t, vp, vp]
+        L.zk_msm_config.argtypes = [ctypes.c_size_t, ctypes.c_int, ctypes.POINTER(ctypes.c_int),
+                                    ctypes.POINTER(ctypes.c_int)]
         L.zk_msm_g1_host.argtypes = [vp, vp, vp, ctypes.c_int, vp]
         L.zk_msm_g2_host.argtypes = [vp, vp, vp, ctypes.c_int, vp]
         L.zk_g1_generator_mul.argtypes = [vp, vp, ctypes.c_size_t, vp, vp]
@@ -211,6 +213,15 @@ class Context:
         out = np.zeros(16, dtype=np.uint64)
         self._check(lib().zk_msm_g2(self.h, vp(d_points.ptr), vp(d_scalars.ptr), n, _np_ptr(out), None), "zk_msm_g2")
         return out
+
+    @staticmethod
+    def msm_config(n, g2=False):
+        """(window bits, windows) the MSM uses for n points."""
+        c, w = ctypes.c_int(), ctypes.c_int()
+        st = lib().zk_msm_config(n, int(g2), ctypes.byref(c), ctypes.byref(w))
+        if st:
+            raise ZkError(f"zk_msm_config failed ({lib().zk_status_string(st).decode()})")
+        return c.value, w.value
 
     def g1_generator_mul(self, d_scalars, n, d_out):
         self._check(lib().zk_g1_generator_mul(self.h, vp(d_scalars.ptr), n, vp(d_out.ptr), None), "g1_generator_mul")

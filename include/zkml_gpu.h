@@ -96,11 +96,17 @@ int zk_coset_ntt(zk_context* ctx, void* d_out, const void* d_in, int log_n, uint
  * result = sum_i scalars[i] * points[i].  Device-resident inputs (points in
  * zk_g1_affine / zk_g2_affine layout, scalars zk_fr), result written to host
  * memory as an affine point in the same layout (the reference returns a
- * Jacobian point whose callers convert it to affine).  n == 0 gives infinity. */
+ * Jacobian point whose callers convert it to affine).  n == 0 gives infinity;
+ * n above 2^26 returns ZK_ERR_SIZE. */
 int zk_msm_g1(zk_context* ctx, const void* d_points, const void* d_scalars, size_t n, void* h_result,
               void* stream);
 int zk_msm_g2(zk_context* ctx, const void* d_points, const void* d_scalars, size_t n, void* h_result,
               void* stream);
+
+/* Window configuration the MSM uses for n points (replaces
+ * bn254::MSMConfig::for_size, src/msm/msm.cuh:40-64): window bits c (the
+ * widest window) and the number of signed-digit windows.  CPU only. */
+int zk_msm_config(size_t n, int g2, int* window_bits, int* windows);
 
 /* Host-pointer drop-ins with the reference's exact signature semantics:
  * h_points are reference G1Affine / G2Affine structs (72 / 136 bytes),

@@ -1,0 +1,199 @@
+"""CPU unit tests of the kernels' own field and curve arithmetic.
+
+cuda-zkml_amd/csrc/field.hpp and curve.hpp are header-only and compile for the
+host as well; tests/native/field_host_check.cpp exposes them through a small C
+shim.  Expectations come from Python big integers (tests/zkpy.py), so a wrong
+limb, carry or range assumption fails here before any kernel runs:
+
+  fmul / fsqr / fmul2     a*b*2^-261 (+ c*e*2^-261) mod q, result < 2q, limbs < 2^29,
+                          at the edges of the documented input ranges
+  fsub_lazy / fneg_lazy   exact a - b + 2q and 2q - a
+  fadd / fsub / fmul_sub  congruence and the [0, 2q) output range
+  XYZZ madd/add/dbl/mdbl  G1 and G2 against affine formulas, with coordinates
+                          given in non-canonical [q, 2q) representatives and
+                          random Z, plus the doubling / inverse / infinity cases
+"""
+import ctypes
+import os
+import random
+import subprocess
+
+import pytest
+
+from zkpy import G1, G2, P as Q, R as ORDER, g1, g2, f2_inv, f2_mul
+
+ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+CSRC = os.path.join(ROOT, "cuda-zkml_amd", "csrc")
+SRC = os.path.join(ROOT, "tests", "native", "field_host_check.cpp")
+RP = 1 << 261          # internal Montgomery radix
+RP_INV = pow(RP, -1, Q)
+U32x9 = ctypes.c_uint32 * 9
+
+
+@pytest.fixture(scope="module")
+def fh(tmp_path_factory):
+    so = tmp_path_factory.mktemp("fh") / "field_host_check.so"
+    subprocess.run(["g++", "-O2", "-std=c++17", "-shared", "-fPIC", "-I", CSRC, SRC, "-o", str(so)], check=True)
+    lib = ctypes.CDLL(str(so))
+    lib.fh_op.restype = ctypes.c_int
+    lib.fh_xyzz.restype = ctypes.c_int
+    return lib
+
+
+def to_l(x):
+    assert 0 <= x < 1 << 261
+    return [(x >> (29 * i)) & ((1 << 29) - 1) for i in range(9)]
+
+
+def from_l(ws):
+    return sum(int(w) << (29 * i) for i, w in enumerate(ws))
+
+
+def op(fh, code, a, b=0, c=0, d=0):
+    out = U32x9()
+    assert fh.fh_op(code, U32x9(*to_l(a)), U32x9(*to_l(b)), U32x9(*to_l(c)), U32x9(*to_l(d)), out) == 0
+    ws = list(out)
+    assert all(w < 1 << 29 for w in ws), "limb not normalized"
+    return from_l(ws)
+
+
+def samples(rng, hi, k=40):
+    """Values in [0, hi): the edges plus random ones."""
+    return [0, 1, hi - 1, hi - 2, Q - 1, Q, Q + 1][: 7 if hi > Q + 1 else 4] + [rng.randrange(hi) for _ in range(k)]
+
+
+def test_fmul_fsqr_ranges(fh):
+    rng = random.Random(1)
+    for a in samples(rng, 8 * Q):
+        for b in samples(rng, 8 * Q, 6):
+            r = op(fh, 0, a, b)
+            assert r < 2 * Q and r % Q == a * b * RP_INV % Q
+    for a in samples(rng, 8 * Q):
+        r = op(fh, 1, a)
+        assert r < 2 * Q and r % Q == a * a * RP_INV % Q
+
+
+def test_fmul2_ranges(fh):
+    rng = random.Random(2)
+    vals = samples(rng, 4 * Q, 12)
+    for a in vals:
+        for b in vals[:6]:
+            c, e = rng.choice(vals), rng.choice(vals)
+            r = op(fh, 2, a, b, c, e)
+            assert r < 2 * Q and r % Q == (a * b + c * e) * RP_INV % Q
+    m = 4 * Q - 1  # every operand at its maximum
+    r = op(fh, 2, m, m, m, m)
+    assert r < 2 * Q and r % Q == 2 * m * m * RP_INV % Q
+
+
+def test_lazy_sub_neg_exact(fh):
+    rng = random.Random(3)
+    for a in samples(rng, 2 * Q):
+        for b in samples(rng, 2 * Q, 4):
+            assert op(fh, 3, a, b) == a + 2 * Q - b
+    for a in samples(rng, 2 * Q) + [2 * Q]:
+        assert op(fh, 4, a) == 2 * Q - a
+
+
+def test_add_sub_mulsub(fh):
+    rng = random.Random(4)
+    for a in samples(rng, 2 * Q):
+        for b in samples(rng, 2 * Q, 4):
+            s = op(fh, 5, a, b)
+            d = op(fh, 6, a, b)
+            assert s < 2 * Q and s % Q == (a + b) % Q
+            assert d < 2 * Q and d % Q == (a - b) % Q
+    for _ in range(200):
+        a, c, d = (rng.randrange(2 * Q) for _ in range(3))
+        b = rng.randrange(4 * Q)  # the lazy factor
+        r = op(fh, 7, a, b, c, d)
+        assert r < 2 * Q and r % Q == (a * b - c * d) * RP_INV % Q
+
+
+# ----------------------------------------------------------------- XYZZ
+def rep(rng, v):
+    """Internal representative of v (standard form): v*2^261 mod q, with q
+    added at random so that [q, 2q) inputs are exercised."""
+    x = v * RP % Q
+    return x + Q if rng.random() < 0.5 else x
+
+
+def enc1(rng, pt, z):
+    if pt is None:
+        return [0] * 36
+    x, y = pt
+    zz, zzz = z * z % Q, z * z * z % Q
+    out = []
+    for v in (x * zz % Q, y * zzz % Q, zz, zzz):
+        out += to_l(rep(rng, v))
+    return out
+
+
+def dec1(ws):
+    X, Y, ZZ, ZZZ = (from_l(ws[9 * i: 9 * i + 9]) for i in range(4))
+    for v in (X, Y, ZZ, ZZZ):
+        assert v < 2 * Q
+    if ZZ % Q == 0:
+        return None
+    return (X * pow(ZZ, Q - 2, Q) % Q, Y * pow(ZZZ, Q - 2, Q) % Q)
+
+
+def enc2(rng, pt, z):
+    if pt is None:
+        return [0] * 72
+    x, y = pt
+    zz = f2_mul(z, z)
+    zzz = f2_mul(zz, z)
+    out = []
+    for v in (f2_mul(x, zz), f2_mul(y, zzz), zz, zzz):
+        out += to_l(rep(rng, v[0])) + to_l(rep(rng, v[1]))
+    return out
+
+
+def dec2(ws):
+    parts = [(from_l(ws[18 * i: 18 * i + 9]), from_l(ws[18 * i + 9: 18 * i + 18])) for i in range(4)]
+    for v in parts:
+        assert v[0] < 2 * Q and v[1] < 2 * Q
+    X, Y, ZZ, ZZZ = ((a % Q, b % Q) for a, b in parts)
+    if ZZ == (0, 0):
+        return None
+    return (f2_mul(X, f2_inv(ZZ)), f2_mul(Y, f2_inv(ZZZ)))
+
+
+def xyzz_call(fh, g2flag, code, p, q):
+    nw = 72 if g2flag else 36
+    arr = ctypes.c_uint32 * nw
+    out = arr()
+    assert fh.fh_xyzz(g2flag, code, arr(*p), arr(*(q + [0] * (nw - len(q)))), out) == 0
+    return list(out)
+
+
+@pytest.mark.parametrize("g2flag", [0, 1])
+def test_xyzz_formulas(fh, g2flag):
+    rng = random.Random(5 + g2flag)
+    grp, gen = (g2, G2) if g2flag else (g1, G1)
+    enc, dec = (enc2, dec2) if g2flag else (enc1, dec1)
+
+    def rz():
+        return (rng.randrange(1, Q), rng.randrange(Q)) if g2flag else rng.randrange(1, Q)
+
+    def affine_words(pt):  # Z = 1, the record form madd/mdbl read
+        return enc(rng, pt, (1, 0) if g2flag else 1)[: 36 if g2flag else 18]
+
+    pts = [grp.pmul(gen, rng.randrange(1, ORDER)) for _ in range(6)]
+    for i in range(len(pts) - 1):
+        a, b = pts[i], pts[i + 1]
+        # madd, add, dbl, mdbl on generic inputs
+        assert dec(xyzz_call(fh, g2flag, 0, enc(rng, a, rz()), affine_words(b))) == grp.padd(a, b)
+        assert dec(xyzz_call(fh, g2flag, 1, enc(rng, a, rz()), enc(rng, b, rz()))) == grp.padd(a, b)
+        assert dec(xyzz_call(fh, g2flag, 2, enc(rng, a, rz()), [])) == grp.padd(a, a)
+        assert dec(xyzz_call(fh, g2flag, 3, [0] * (72 if g2flag else 36), affine_words(a))) == grp.padd(a, a)
+    a = pts[0]
+    # special cases: P + P (doubling branch), P + (-P), infinity operands
+    assert dec(xyzz_call(fh, g2flag, 0, enc(rng, a, rz()), affine_words(a))) == grp.padd(a, a)
+    assert dec(xyzz_call(fh, g2flag, 1, enc(rng, a, rz()), enc(rng, a, rz()))) == grp.padd(a, a)
+    assert dec(xyzz_call(fh, g2flag, 0, enc(rng, a, rz()), affine_words(grp.pneg(a)))) is None
+    assert dec(xyzz_call(fh, g2flag, 1, enc(rng, a, rz()), enc(rng, grp.pneg(a), rz()))) is None
+    assert dec(xyzz_call(fh, g2flag, 0, enc(rng, None, rz()), affine_words(a))) == a
+    assert dec(xyzz_call(fh, g2flag, 1, enc(rng, None, rz()), enc(rng, a, rz()))) == a
+    assert dec(xyzz_call(fh, g2flag, 1, enc(rng, a, rz()), enc(rng, None, rz()))) == a
