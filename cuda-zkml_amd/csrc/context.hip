@@ -21,22 +21,25 @@ int zk_context::ensure(DevBuf& b, size_t bytes) {
   return ZK_OK;
 }
 
-void zk_context::tic(const char* name, hipStream_t st) {
-  if (!profiling) return;
-  PendingTiming t;
+zk::TimingToken zk_context::tic(const char* name, hipStream_t st) {
+  zk::TimingToken t;
+  if (!profiling) return t;
   t.name = name;
   (void)hipEventCreate(&t.a);
   (void)hipEventCreate(&t.b);
   (void)hipEventRecord(t.a, st);
-  pending.push_back(t);
+  return t;
 }
 
-void zk_context::toc(hipStream_t st) {
-  if (!profiling || pending.empty()) return;
-  (void)hipEventRecord(pending.back().b, st);
+void zk_context::toc(zk::TimingToken& t, hipStream_t st) {
+  if (!t.name) return;
+  (void)hipEventRecord(t.b, st);
+  std::lock_guard<std::mutex> lk(mu);
+  pending.push_back(zk::PendingTiming{t.name, t.a, t.b});
 }
 
 void zk_context::collect() {
+  std::lock_guard<std::mutex> lk(mu);
   for (auto& t : pending) {
     (void)hipEventSynchronize(t.b);
     float ms = 0;
@@ -77,6 +80,10 @@ void zk_destroy(zk_context* ctx) {
   ntt_plans_free(ctx);
   if (ctx->msm_ws) msm_workspace_free(ctx->msm_ws);
   if (ctx->msm_ws_g2) msm_workspace_free(ctx->msm_ws_g2);
+  for (int j = 0; j < ZK_JOBS; j++) {
+    if (ctx->job_ws[j]) msm_workspace_free(ctx->job_ws[j]);
+    if (ctx->job_stream[j]) (void)hipStreamDestroy(ctx->job_stream[j]);
+  }
   for (DevBuf* b : {&ctx->scratch_a, &ctx->scratch_b, &ctx->scratch_c})
     if (b->p) (void)hipFree(b->p);
   if (ctx->g1_table) (void)hipFree(ctx->g1_table);

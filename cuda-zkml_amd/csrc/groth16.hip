@@ -9,6 +9,7 @@
 
 #include <algorithm>
 #include <random>
+#include <thread>
 #include <vector>
 
 #include "curve.hpp"
@@ -535,12 +536,15 @@ int zk_pk_info(const zk_pk* pk, int* n, int* m, int* npub) {
 int zk_prove(zk_context* ctx, const zk_pk* pk, const zk_r1cs* c, const void* h_witness, size_t m, int num_public,
              uint64_t blind_seed, int check_witness, uint8_t proof_out[256], double* timings) {
   if (!ctx || !pk || !c || !proof_out || (m && !h_witness)) return ZK_ERR_INVALID;
-  hipEvent_t ev[8];
+  // events: 0 start, 1 witness resident, 2 quotient done, 3 end,
+  // 4 + 2j / 5 + 2j start / end of MSM job j
+  constexpr int NEV = 4 + 2 * ZK_JOBS;
+  hipEvent_t ev[NEV];
   for (auto& e : ev) ZK_HIP(ctx, hipEventCreate(&e));
   struct EvGuard {
     hipEvent_t* e;
     ~EvGuard() {
-      for (int i = 0; i < 8; i++) (void)hipEventDestroy(e[i]);
+      for (int i = 0; i < NEV; i++) (void)hipEventDestroy(e[i]);
     }
   } guard{ev};
   hipStream_t st = ctx->stream;
@@ -552,19 +556,16 @@ int zk_prove(zk_context* ctx, const zk_pk* pk, const zk_r1cs* c, const void* h_w
   const size_t n = c->n;
   ZK_TRY(ctx->ensure(ctx->scratch_b, n * 32 * 3));
   ZK_TRY(ctx->ensure(ctx->scratch_c, n * 32 + m * 32 + 64));
+  for (int j = 0; j < ZK_JOBS; j++) {
+    if (!ctx->job_stream[j]) ZK_HIP(ctx, hipStreamCreateWithFlags(&ctx->job_stream[j], hipStreamNonBlocking));
+    if (!ctx->job_ws[j]) ctx->job_ws[j] = msm_workspace_new();
+  }
   uint8_t* base = (uint8_t*)ctx->scratch_c.p;
   void* d_h = base;
   void* d_w = base + n * 32;
   uint32_t* d_bad = (uint32_t*)(base + n * 32 + m * 32);
   ZK_HIP(ctx, hipEventRecord(ev[0], st));
   ZK_HIP(ctx, hipMemcpyAsync(d_w, h_witness, m * 32, hipMemcpyHostToDevice, st));
-  ZK_TRY(quotient_run(ctx, c, d_w, d_h, ctx->scratch_b.p, st, check_witness != 0, d_bad));
-  if (check_witness) {
-    uint32_t bad = 0;
-    ZK_HIP(ctx, hipMemcpyAsync(&bad, d_bad, 4, hipMemcpyDeviceToHost, st));
-    ZK_HIP(ctx, hipStreamSynchronize(st));
-    if (bad) return ctx->fail(ZK_ERR_WITNESS, "witness does not satisfy the R1CS");
-  }
   ZK_HIP(ctx, hipEventRecord(ev[1], st));
   // blinding factors (groth16.cu:708-718)
   std::mt19937_64 rng(blind_seed);
@@ -572,23 +573,68 @@ int zk_prove(zk_context* ctx, const zk_pk* pk, const zk_r1cs* c, const void* h_w
   Fr s = random_nonzero(rng);
   const uint8_t* w8 = (const uint8_t*)d_w;
   uint64_t a_msm[8], b2_msm[16], l_msm[8], h_msm[8], b1_msm[8];
+  memset(l_msm, 0, sizeof(l_msm));
   const size_t na = std::min(m, pk->nA);
-  ZK_TRY(msm_g1_recs(ctx, pk->A, d_w, na, a_msm, st));
-  ZK_HIP(ctx, hipEventRecord(ev[2], st));
   const size_t nb2 = std::min(m, pk->nB2);
-  ZK_TRY(msm_g2_recs(ctx, pk->B2, d_w, nb2, b2_msm, st));
-  ZK_HIP(ctx, hipEventRecord(ev[3], st));
   const long npriv_l = std::min<long>((long)pk->nL, (long)m - 1 - pk->npub);
-  if (npriv_l > 0) ZK_TRY(msm_g1_recs(ctx, pk->L, w8 + 32 * (1 + pk->npub), (size_t)npriv_l, l_msm, st));
-  else memset(l_msm, 0, 64);
-  ZK_HIP(ctx, hipEventRecord(ev[4], st));
   const size_t nh = std::min(n, pk->nH);
-  ZK_TRY(msm_g1_recs(ctx, pk->H, d_h, nh, h_msm, st));
-  ZK_HIP(ctx, hipEventRecord(ev[5], st));
   const size_t nb1 = std::min(m, pk->nB1);
-  ZK_TRY(msm_g1_recs(ctx, pk->B1, d_w, nb1, b1_msm, st));
-  ZK_HIP(ctx, hipEventRecord(ev[6], st));
-  ZK_HIP(ctx, hipEventSynchronize(ev[6]));
+  // The five MSMs are independent (groth16.cu:776-827): each runs on its own
+  // stream with its own workspace from its own host thread, so that their
+  // latency-bound phases overlap.  A, B2, L and B1 need only the witness; H
+  // waits for the quotient computed meanwhile on the context stream.
+  struct Job {
+    bool g2;
+    const void* recs;
+    const void* scalars;
+    size_t n;
+    uint64_t* out;
+    int rc;
+  } jobs[ZK_JOBS] = {{false, pk->A, d_w, na, a_msm, ZK_OK},
+                     {true, pk->B2, d_w, nb2, b2_msm, ZK_OK},
+                     {false, pk->L, w8 + 32 * (1 + pk->npub), npriv_l > 0 ? (size_t)npriv_l : 0, l_msm, ZK_OK},
+                     {false, pk->H, d_h, nh, h_msm, ZK_OK},
+                     {false, pk->B1, d_w, nb1, b1_msm, ZK_OK}};
+  constexpr int JOB_H = 3;
+  auto run_job = [&](int j) {
+    Job& jb = jobs[j];
+    hipStream_t js = ctx->job_stream[j];
+    if (hipEventRecord(ev[4 + 2 * j], js) != hipSuccess) {
+      jb.rc = ctx->fail(ZK_ERR_HIP, "prove: event record");
+      return;
+    }
+    jb.rc = jb.n ? msm_recs_ws(ctx, ctx->job_ws[j], jb.g2, jb.recs, jb.scalars, jb.n, jb.out, js) : ZK_OK;
+    if (hipEventRecord(ev[5 + 2 * j], js) != hipSuccess && jb.rc == ZK_OK)
+      jb.rc = ctx->fail(ZK_ERR_HIP, "prove: event record");
+  };
+  for (int j = 0; j < ZK_JOBS; j++)
+    if (j != JOB_H) ZK_HIP(ctx, hipStreamWaitEvent(ctx->job_stream[j], ev[1], 0));
+  std::vector<std::thread> workers;
+  for (int j = 0; j < ZK_JOBS; j++) {
+    if (j == JOB_H) continue;
+    try {
+      workers.emplace_back(run_job, j);
+    } catch (...) {
+      run_job(j);  // no thread available: run it here
+    }
+  }
+  int qrc = quotient_run(ctx, c, d_w, d_h, ctx->scratch_b.p, st, check_witness != 0, d_bad);
+  uint32_t bad = 0;
+  if (qrc == ZK_OK && check_witness) {
+    if (hipMemcpyAsync(&bad, d_bad, 4, hipMemcpyDeviceToHost, st) != hipSuccess)
+      qrc = ctx->fail(ZK_ERR_HIP, "prove: witness check read-back");
+  }
+  if (qrc == ZK_OK && hipEventRecord(ev[2], st) != hipSuccess) qrc = ctx->fail(ZK_ERR_HIP, "prove: event record");
+  if (qrc == ZK_OK && hipStreamWaitEvent(ctx->job_stream[JOB_H], ev[2], 0) != hipSuccess)
+    qrc = ctx->fail(ZK_ERR_HIP, "prove: stream wait");
+  if (qrc == ZK_OK) run_job(JOB_H);
+  for (auto& t : workers) t.join();
+  ZK_TRY(qrc);
+  if (check_witness) {
+    ZK_HIP(ctx, hipStreamSynchronize(st));
+    if (bad) return ctx->fail(ZK_ERR_WITNESS, "witness does not satisfy the R1CS");
+  }
+  for (const Job& jb : jobs) ZK_TRY(jb.rc);
   // host assembly (groth16.cu:769-840): C = L + H + s A + r (beta1 + B1)
   G1 A = g1_from_words(pk->alpha1).add(na > 0 ? g1_from_words(a_msm) : G1::inf());
   A = A.add(g1_from_words(pk->delta1).mul(r));
@@ -619,21 +665,26 @@ int zk_prove(zk_context* ctx, const zk_pk* pk, const zk_r1cs* c, const void* h_w
   put(Bw + 12);
   put(Cw);
   put(Cw + 4);
-  ZK_HIP(ctx, hipEventRecord(ev[7], st));
-  ZK_HIP(ctx, hipEventSynchronize(ev[7]));
+  ZK_HIP(ctx, hipEventRecord(ev[3], st));
+  ZK_HIP(ctx, hipEventSynchronize(ev[3]));
   if (timings) {
-    float t[8] = {0};
-    for (int i = 1; i < 8; i++) (void)hipEventElapsedTime(&t[i], ev[i - 1], ev[i]);
-    float total = 0;
-    (void)hipEventElapsedTime(&total, ev[0], ev[7]);
-    timings[0] = total;  // total
-    timings[1] = t[1];   // quotient (incl. witness upload / check)
-    timings[2] = t[2];   // A  (G1 MSM, m)
-    timings[3] = t[3];   // B  (G2 MSM, m)
-    timings[4] = t[4];   // L  (G1 MSM, m - npub - 1)
-    timings[5] = t[5];   // H  (G1 MSM, n)
-    timings[6] = t[6];   // B1 (G1 MSM, m)
-    timings[7] = t[7];   // host assembly
+    float t = 0;
+    (void)hipEventElapsedTime(&t, ev[0], ev[3]);
+    timings[0] = t;  // total
+    (void)hipEventElapsedTime(&t, ev[0], ev[2]);
+    timings[1] = t;  // witness upload + quotient (+ check)
+    // each MSM from its start to its result on the host (they overlap)
+    for (int j = 0; j < ZK_JOBS; j++) {
+      (void)hipEventElapsedTime(&t, ev[4 + 2 * j], ev[5 + 2 * j]);
+      timings[2 + j] = t;  // A, B (G2), L, H, B1
+    }
+    float last = 0;
+    for (int j = 0; j < ZK_JOBS; j++) {
+      (void)hipEventElapsedTime(&t, ev[0], ev[5 + 2 * j]);
+      last = std::max(last, t);
+    }
+    (void)hipEventElapsedTime(&t, ev[0], ev[3]);
+    timings[7] = t - last;  // host assembly after the last MSM
   }
   return ZK_OK;
 }

@@ -838,6 +838,15 @@ int msm_g2_run(zk_context* ctx, const void* d_points, const void* d_scalars, siz
   return msm_run<fq2>(ctx, ctx->msm_ws_g2, d_points, d_scalars, n, out, st);
 }
 
+MsmWorkspace* msm_workspace_new() { return new MsmWorkspace(); }
+
+int msm_recs_ws(zk_context* ctx, MsmWorkspace* ws, bool g2, const void* d_recs, const void* d_scalars, size_t n,
+                uint64_t* out, hipStream_t st) {
+  if (!ws) return ctx->fail(ZK_ERR_INVALID, "msm: no workspace");
+  if (g2) return msm_run_recs<fq2>(ctx, *ws, (const uint4*)d_recs, d_scalars, n, out, st);
+  return msm_run_recs<fq>(ctx, *ws, (const uint4*)d_recs, d_scalars, n, out, st);
+}
+
 int msm_g1_recs(zk_context* ctx, const void* d_recs, const void* d_scalars, size_t n, uint64_t out[8],
                 hipStream_t st) {
   if (!ctx->msm_ws) ctx->msm_ws = new MsmWorkspace();

@@ -47,6 +47,15 @@ struct PendingTiming {
   hipEvent_t a, b;
 };
 
+// One kernel's timing bracket (events recorded on the launch stream).
+struct TimingToken {
+  const char* name = nullptr;
+  hipEvent_t a = nullptr, b = nullptr;
+};
+
+// Concurrent MSM jobs of one proof: a stream and a workspace each.
+constexpr int ZK_JOBS = 5;
+
 }  // namespace zk
 
 struct zk_context {
@@ -62,21 +71,27 @@ struct zk_context {
   // fixed-base tables for the generators (device), built on first use
   void* g1_table = nullptr;
   void* g2_table = nullptr;
+  // streams and workspaces of the concurrent MSMs inside zk_prove
+  hipStream_t job_stream[zk::ZK_JOBS] = {};
+  zk::MsmWorkspace* job_ws[zk::ZK_JOBS] = {};
   // profiling
   bool profiling = false;
   std::map<std::string, zk::KernelStat> stats;
   std::vector<zk::PendingTiming> pending;
   std::string stat_names;
+  // guards last_error and pending: zk_prove runs MSMs from several threads
+  std::mutex mu;
 
   int fail(int code, const char* what, const char* detail = "") {
+    std::lock_guard<std::mutex> lk(mu);
     last_error = std::string(what) + (detail && *detail ? std::string(": ") + detail : std::string());
     return code;
   }
   hipStream_t s(void* st) { return st ? (hipStream_t)st : stream; }
   int ensure(zk::DevBuf& b, size_t bytes);
   // Kernel timing brackets; no-ops unless profiling is enabled.
-  void tic(const char* name, hipStream_t st);
-  void toc(hipStream_t st);
+  zk::TimingToken tic(const char* name, hipStream_t st);
+  void toc(zk::TimingToken& t, hipStream_t st);
   void collect();
 };
 
@@ -85,11 +100,11 @@ namespace zk {
 // Launch helper with error capture.
 #define ZK_LAUNCH(ctx, st, name, kernel, grid, block, shmem, ...)                            \
   do {                                                                                     \
-    (ctx)->tic(name, st);                                                                  \
+    zk::TimingToken _tk = (ctx)->tic(name, st);                                            \
     hipLaunchKernelGGL(kernel, grid, block, shmem, st, __VA_ARGS__);                       \
     hipError_t _e = hipGetLastError();                                                     \
     if (_e != hipSuccess) return (ctx)->fail(ZK_ERR_HIP, name, hipGetErrorString(_e));    \
-    (ctx)->toc(st);                                                                        \
+    (ctx)->toc(_tk, st);                                                                   \
   } while (0)
 
 inline uint32_t cdiv(size_t a, size_t b) { return (uint32_t)((a + b - 1) / b); }
@@ -114,7 +129,11 @@ int msm_g2_recs(zk_context* ctx, const void* d_recs, const void* d_scalars, size
 int recs_from_std(zk_context* ctx, bool g2, void* d_recs, const void* d_std, const void* d_flags, size_t n,
                   hipStream_t st);
 size_t rec_bytes(bool g2);
+MsmWorkspace* msm_workspace_new();
 void msm_workspace_free(MsmWorkspace* ws);
+// MSM over records with an explicit workspace (one per concurrent caller)
+int msm_recs_ws(zk_context* ctx, MsmWorkspace* ws, bool g2, const void* d_recs, const void* d_scalars, size_t n,
+                uint64_t* out_affine, hipStream_t st);
 
 // ---- fixed base (pointgen.hip)
 int g1_generator_mul(zk_context* ctx, const void* d_scalars, size_t n, void* d_out, hipStream_t st);
