@@ -23,12 +23,15 @@ ZK_HD fq2 fadd(const fq2& a, const fq2& b) { return fq2{fadd(a.c0, b.c0), fadd(a
 ZK_HD fq2 fsub(const fq2& a, const fq2& b) { return fq2{fsub(a.c0, b.c0), fsub(a.c1, b.c1)}; }
 ZK_HD fq2 fdbl(const fq2& a) { return fq2{fdbl(a.c0), fdbl(a.c1)}; }
 ZK_HD fq2 fneg(const fq2& a) { return fq2{fneg(a.c0), fneg(a.c1)}; }
-// Karatsuba, 3 base multiplies (reference src/field/fp2.cuh:73-78).
+// (a0 + a1 u)(b0 + b1 u) = (a0 b0 - a1 b1) + (a0 b1 + a1 b0) u, each
+// coordinate one fmul_sum (4 limb products, 2 reductions; the reference uses
+// Karatsuba, src/field/fp2.cuh:73-78: 3 multiplies, each with its own
+// reduction).  -a1 enters as 2q - a1, so a must be reduced (< 2q); b may be a
+// lazy difference (< 4q).
 ZK_HD fq2 fmul(const fq2& a, const fq2& b) {
-  fq ac = fmul(a.c0, b.c0);
-  fq bd = fmul(a.c1, b.c1);
-  fq s = fmul(fadd_lazy(a.c0, a.c1), fadd_lazy(b.c0, b.c1));
-  return fq2{fsub(ac, bd), fsub(fsub(s, ac), bd)};
+  const fq x0[2] = {a.c0, fneg_lazy(a.c1)}, y0[2] = {b.c0, b.c1};
+  const fq x1[2] = {a.c0, a.c1}, y1[2] = {b.c1, b.c0};
+  return fq2{fmul_sum<FqP, 2>(x0, y0), fmul_sum<FqP, 2>(x1, y1)};
 }
 // (a + bu)^2 = (a+b)(a-b) + 2ab u
 ZK_HD fq2 fsqr(const fq2& a) {
@@ -42,11 +45,17 @@ ZK_HD void fset_zero(fq2& a) { a = fq2{fe_zero<FqP>(), fe_zero<FqP>()}; }
 ZK_HD void fset_one(fq& a) { a = fe_one<FqP>(); }
 ZK_HD void fset_one(fq2& a) { a = fq2{fe_one<FqP>(), fe_zero<FqP>()}; }
 
-// a*b - c*d.  Over Fq one Montgomery reduction serves both products (fmul2
-// with 2m - d); over Fq2 the Karatsuba products are formed separately.
-// b may be a lazy difference (fsub_m), the other inputs are reduced.
+// a*b - c*d with one Montgomery reduction per coordinate (fmul_sum, the
+// subtracted products entering as (2m - x) * y).  b may be a lazy difference
+// (fsub_m), the other inputs are reduced.
 ZK_HD fq fmul_sub(const fq& a, const fq& b, const fq& c, const fq& d) { return fmul2(a, b, c, fneg_lazy(d)); }
-ZK_HD fq2 fmul_sub(const fq2& a, const fq2& b, const fq2& c, const fq2& d) { return fsub(fmul(a, b), fmul(c, d)); }
+ZK_HD fq2 fmul_sub(const fq2& a, const fq2& b, const fq2& c, const fq2& d) {
+  // real: a0 b0 - a1 b1 - c0 d0 + c1 d1, imaginary: a0 b1 + a1 b0 - c0 d1 - c1 d0
+  const fq na1 = fneg_lazy(a.c1), nc0 = fneg_lazy(c.c0), nc1 = fneg_lazy(c.c1);
+  const fq x0[4] = {a.c0, na1, nc0, c.c1}, y0[4] = {b.c0, b.c1, d.c0, d.c1};
+  const fq x1[4] = {a.c0, a.c1, nc0, nc1}, y1[4] = {b.c1, b.c0, d.c1, d.c0};
+  return fq2{fmul_sum<FqP, 4>(x0, y0), fmul_sum<FqP, 4>(x1, y1)};
+}
 // a - b left in (0, 4m): only for the second factor of fmul_sub.
 ZK_HD fq fsub_m(const fq& a, const fq& b) { return fsub_lazy(a, b); }
 ZK_HD fq2 fsub_m(const fq2& a, const fq2& b) { return fq2{fsub_lazy(a.c0, b.c0), fsub_lazy(a.c1, b.c1)}; }

@@ -131,12 +131,14 @@ ZK_HD fe<P> fmul(const fe<P>& a, const fe<P>& b) {
   return r;
 }
 
-// (a*b + c*e) * 2^-261 mod m with one Montgomery reduction for both
-// products.  Inputs: normalized limbs (< 2^29), values < 4m; then every
-// column holds at most 27 products below 2^58 plus a carry below 2^35, which
-// stays below 2^64, and the result is below 32m^2 / 2^261 + m < 2m.
-template <class P>
-ZK_HD fe<P> fmul2(const fe<P>& a, const fe<P>& b, const fe<P>& c, const fe<P>& e) {
+// sum_t a[t]*b[t] * 2^-261 mod m, N <= 4, with one Montgomery reduction for
+// all products.  Inputs: normalized limbs (< 2^29); a[t] < 2m and b[t] < 4m
+// (or both < 4m when N <= 2).  Every column then holds at most 9N + 9 terms
+// below 2^58 plus a carry below 2^35, which stays below 2^64, and the result
+// is below 32m^2 / 2^261 + m < 2m.
+template <class P, int N>
+ZK_HD fe<P> fmul_sum(const fe<P> (&a)[N], const fe<P> (&b)[N]) {
+  static_assert(N >= 1 && N <= 4, "column accumulator bound");
   uint32_t q[NL];
   fe<P> r;
   uint64_t acc = 0;
@@ -146,8 +148,8 @@ ZK_HD fe<P> fmul2(const fe<P>& a, const fe<P>& b, const fe<P>& c, const fe<P>& e
     for (int i = 0; i < NL; i++) {
       const int j = k - i;
       if (j >= 0 && j < NL) {
-        acc += (uint64_t)a.l[i] * b.l[j];
-        acc += (uint64_t)c.l[i] * e.l[j];
+#pragma unroll
+        for (int t = 0; t < N; t++) acc += (uint64_t)a[t].l[i] * b[t].l[j];
       }
     }
 #pragma unroll
@@ -165,6 +167,13 @@ ZK_HD fe<P> fmul2(const fe<P>& a, const fe<P>& b, const fe<P>& c, const fe<P>& e
   }
   r.l[NL - 1] = (uint32_t)acc;
   return r;
+}
+
+// (a*b + c*e) * 2^-261 mod m: fmul_sum of two products (values < 4m).
+template <class P>
+ZK_HD fe<P> fmul2(const fe<P>& a, const fe<P>& b, const fe<P>& c, const fe<P>& e) {
+  const fe<P> x[2] = {a, c}, y[2] = {b, e};
+  return fmul_sum<P, 2>(x, y);
 }
 
 // Squaring: cross products are summed once and doubled per column.

@@ -8,6 +8,8 @@
 #include <string.h>
 
 #include <algorithm>
+#include <condition_variable>
+#include <mutex>
 #include <random>
 #include <thread>
 #include <vector>
@@ -537,8 +539,8 @@ int zk_prove(zk_context* ctx, const zk_pk* pk, const zk_r1cs* c, const void* h_w
              uint64_t blind_seed, int check_witness, uint8_t proof_out[256], double* timings) {
   if (!ctx || !pk || !c || !proof_out || (m && !h_witness)) return ZK_ERR_INVALID;
   // events: 0 start, 1 witness resident, 2 quotient done, 3 end,
-  // 4 + 2j / 5 + 2j start / end of MSM job j
-  constexpr int NEV = 4 + 2 * ZK_JOBS;
+  // 4 + 2j / 5 + 2j start / end of MSM job j, last: G2 accumulation enqueued
+  constexpr int NEV = 5 + 2 * ZK_JOBS;
   hipEvent_t ev[NEV];
   for (auto& e : ev) ZK_HIP(ctx, hipEventCreate(&e));
   struct EvGuard {
@@ -595,23 +597,54 @@ int zk_prove(zk_context* ctx, const zk_pk* pk, const zk_r1cs* c, const void* h_w
                      {false, pk->L, w8 + 32 * (1 + pk->npub), npriv_l > 0 ? (size_t)npriv_l : 0, l_msm, ZK_OK},
                      {false, pk->H, d_h, nh, h_msm, ZK_OK},
                      {false, pk->B1, d_w, nb1, b1_msm, ZK_OK}};
-  constexpr int JOB_H = 3;
+  constexpr int JOB_B2 = 1, JOB_H = 3;
+  // The G2 MSM is the longest: its accumulation runs first on its own and the
+  // G1 MSMs start once it is enqueued (their streams wait for it), so that they
+  // fill the GPU during the G2 MSM's latency-bound combine and reduction.
+  struct Gate {
+    std::mutex m;
+    std::condition_variable cv;
+    bool open = false, recorded = false;
+    void release(bool rec) {
+      {
+        std::lock_guard<std::mutex> lk(m);
+        if (open) return;
+        open = true;
+        recorded = rec;
+      }
+      cv.notify_all();
+    }
+  } gate;
+  MsmHook hook;
+  hook.ev = ev[NEV - 1];
+  hook.fn = [](void* a) { ((Gate*)a)->release(true); };
+  hook.arg = &gate;
   auto run_job = [&](int j) {
     Job& jb = jobs[j];
     hipStream_t js = ctx->job_stream[j];
+    if (j != JOB_B2) {
+      std::unique_lock<std::mutex> lk(gate.m);
+      gate.cv.wait(lk, [&] { return gate.open; });
+      if (gate.recorded && hipStreamWaitEvent(js, hook.ev, 0) != hipSuccess) {
+        jb.rc = ctx->fail(ZK_ERR_HIP, "prove: stream wait");
+        return;
+      }
+    }
     if (hipEventRecord(ev[4 + 2 * j], js) != hipSuccess) {
       jb.rc = ctx->fail(ZK_ERR_HIP, "prove: event record");
-      return;
+    } else {
+      jb.rc = jb.n ? msm_recs_ws(ctx, ctx->job_ws[j], jb.g2, jb.recs, jb.scalars, jb.n, jb.out, js,
+                                 j == JOB_B2 ? &hook : nullptr)
+                   : ZK_OK;
+      if (hipEventRecord(ev[5 + 2 * j], js) != hipSuccess && jb.rc == ZK_OK)
+        jb.rc = ctx->fail(ZK_ERR_HIP, "prove: event record");
     }
-    jb.rc = jb.n ? msm_recs_ws(ctx, ctx->job_ws[j], jb.g2, jb.recs, jb.scalars, jb.n, jb.out, js) : ZK_OK;
-    if (hipEventRecord(ev[5 + 2 * j], js) != hipSuccess && jb.rc == ZK_OK)
-      jb.rc = ctx->fail(ZK_ERR_HIP, "prove: event record");
+    if (j == JOB_B2) gate.release(false);  // no-op when the hook already ran
   };
   for (int j = 0; j < ZK_JOBS; j++)
     if (j != JOB_H) ZK_HIP(ctx, hipStreamWaitEvent(ctx->job_stream[j], ev[1], 0));
   std::vector<std::thread> workers;
-  for (int j = 0; j < ZK_JOBS; j++) {
-    if (j == JOB_H) continue;
+  for (int j : {JOB_B2, 0, 2, 4}) {  // the G2 job first: the others wait for it
     try {
       workers.emplace_back(run_job, j);
     } catch (...) {

@@ -689,7 +689,7 @@ static void host_finish(const std::vector<xyzz<F>>& parts, int W, int per_w, uin
 // the workspace's own conversion buffer or a proving key's resident queries.
 template <class F>
 static int msm_run_recs(zk_context* ctx, MsmWorkspace& ws, const uint4* recs, const void* d_scalars, size_t n,
-                        uint64_t* out, hipStream_t st) {
+                        uint64_t* out, hipStream_t st, const MsmHook* hook = nullptr) {
   constexpr int OUTW = sizeof(F) == sizeof(fq) ? 8 : 16;
   memset(out, 0, OUTW * 8);
   if (n == 0) return ZK_OK;
@@ -765,6 +765,10 @@ static int msm_run_recs(zk_context* ctx, MsmWorkspace& ws, const uint4* recs, co
   ChunkSlots<F> slots{(uint32_t*)ws.hkey.p, (uint32_t*)ws.tkey.p, (xyzz<F>*)ws.hpt.p, (xyzz<F>*)ws.tpt.p};
   ZK_LAUNCH(ctx, st, "msm_accumulate", k_msm_accumulate<F>, dim3(cdiv(nchunks, 256)), dim3(256), 0, sorted, recs,
             start, end, wstat, nchunks, cpw, n_pad, L0, buckets, slots);
+  if (hook) {
+    ZK_HIP(ctx, hipEventRecord(hook->ev, st));
+    hook->fn(hook->arg);
+  }
   // the largest bucket decides the depth of the chunk-combine tree; its
   // read-back overlaps the accumulation
   ZK_HIP(ctx, hipEventSynchronize(ws.stat_ready));
@@ -841,10 +845,10 @@ int msm_g2_run(zk_context* ctx, const void* d_points, const void* d_scalars, siz
 MsmWorkspace* msm_workspace_new() { return new MsmWorkspace(); }
 
 int msm_recs_ws(zk_context* ctx, MsmWorkspace* ws, bool g2, const void* d_recs, const void* d_scalars, size_t n,
-                uint64_t* out, hipStream_t st) {
+                uint64_t* out, hipStream_t st, const MsmHook* hook) {
   if (!ws) return ctx->fail(ZK_ERR_INVALID, "msm: no workspace");
-  if (g2) return msm_run_recs<fq2>(ctx, *ws, (const uint4*)d_recs, d_scalars, n, out, st);
-  return msm_run_recs<fq>(ctx, *ws, (const uint4*)d_recs, d_scalars, n, out, st);
+  if (g2) return msm_run_recs<fq2>(ctx, *ws, (const uint4*)d_recs, d_scalars, n, out, st, hook);
+  return msm_run_recs<fq>(ctx, *ws, (const uint4*)d_recs, d_scalars, n, out, st, hook);
 }
 
 int msm_g1_recs(zk_context* ctx, const void* d_recs, const void* d_scalars, size_t n, uint64_t out[8],

@@ -131,9 +131,16 @@ int recs_from_std(zk_context* ctx, bool g2, void* d_recs, const void* d_std, con
 size_t rec_bytes(bool g2);
 MsmWorkspace* msm_workspace_new();
 void msm_workspace_free(MsmWorkspace* ws);
+// Callback after the accumulation kernel is enqueued: `ev` is recorded on the
+// MSM's stream right after it, then `fn` runs on the calling thread.
+struct MsmHook {
+  hipEvent_t ev = nullptr;
+  void (*fn)(void*) = nullptr;
+  void* arg = nullptr;
+};
 // MSM over records with an explicit workspace (one per concurrent caller)
 int msm_recs_ws(zk_context* ctx, MsmWorkspace* ws, bool g2, const void* d_recs, const void* d_scalars, size_t n,
-                uint64_t* out_affine, hipStream_t st);
+                uint64_t* out_affine, hipStream_t st, const MsmHook* after_accumulate = nullptr);
 
 // ---- fixed base (pointgen.hip)
 int g1_generator_mul(zk_context* ctx, const void* d_scalars, size_t n, void* d_out, hipStream_t st);

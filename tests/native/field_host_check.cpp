@@ -34,6 +34,11 @@ int fh_op(int op, const uint32_t* a, const uint32_t* b, const uint32_t* c, const
     case 5: r = fadd(A, B); break;
     case 6: r = fsub(A, B); break;
     case 7: r = fmul_sub(A, B, C, D); break;
+    case 8: {  // four products: a*b + c*d + a*d + c*b
+      const fq x[4] = {A, C, A, C}, y[4] = {B, D, D, B};
+      r = fmul_sum<FqP, 4>(x, y);
+      break;
+    }
     default: return -1;
   }
   st(out, r);

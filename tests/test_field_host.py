@@ -5,7 +5,7 @@ host as well; tests/native/field_host_check.cpp exposes them through a small C
 shim.  Expectations come from Python big integers (tests/zkpy.py), so a wrong
 limb, carry or range assumption fails here before any kernel runs:
 
-  fmul / fsqr / fmul2     a*b*2^-261 (+ c*e*2^-261) mod q, result < 2q, limbs < 2^29,
+  fmul / fsqr / fmul_sum  a*b*2^-261 (sums of 2 and 4 products) mod q, result < 2q, limbs < 2^29,
                           at the edges of the documented input ranges
   fsub_lazy / fneg_lazy   exact a - b + 2q and 2q - a
   fadd / fsub / fmul_sub  congruence and the [0, 2q) output range
@@ -84,6 +84,15 @@ def test_fmul2_ranges(fh):
     m = 4 * Q - 1  # every operand at its maximum
     r = op(fh, 2, m, m, m, m)
     assert r < 2 * Q and r % Q == 2 * m * m * RP_INV % Q
+    # four products (a, c < 2q; b, d < 4q), including all at their maxima
+    for _ in range(200):
+        a, c = rng.randrange(2 * Q), rng.randrange(2 * Q)
+        b, d = rng.randrange(4 * Q), rng.randrange(4 * Q)
+        r = op(fh, 8, a, b, c, d)
+        assert r < 2 * Q and r % Q == (a * b + c * d + a * d + c * b) * RP_INV % Q
+    a, b = 2 * Q - 1, 4 * Q - 1
+    r = op(fh, 8, a, b, a, b)
+    assert r < 2 * Q and r % Q == 4 * a * b * RP_INV % Q
 
 
 def test_lazy_sub_neg_exact(fh):
