@@ -46,6 +46,9 @@ constexpr int MSM_CMAX = 16;       // widest window: 2^15 LDS counters (128 KB)
 constexpr int SORT_T = 1024;       // threads of the histogram / scatter blocks
 constexpr int SORT_U = 8;          // loads in flight per thread in the sort passes
 constexpr int SCAN_T = 128;        // buckets per column-scan block (<= the smallest B)
+constexpr int MSM_NCB = 256;       // coarse bins per window of the two-pass placement
+constexpr int MSM_BPC_MAX = 128;   // buckets per coarse bin at B = 2^15
+constexpr int PLACE_T = 256;       // threads of a placement block
 constexpr size_t MSM_MAX_N = (size_t)1 << 26;  // keeps W * n_pad below 2^32
 // Bits covered by the windows.  After the optional negation s <= (r-1)/2 <
 // 2^253, and signed digits need one more bit for the final carry.
@@ -378,6 +381,90 @@ __global__ __launch_bounds__(SORT_T) void k_msm_scatter(const uint32_t* __restri
   }
 }
 
+// Two-pass placement for wide windows (B >= 2^13 buckets): one-pass random
+// 8-byte writes across the whole window region leave every cache line
+// partially written by many blocks.
+//
+// Pass 1 (block per window x slice): entries go to NCB coarse bins of BPC =
+// B / NCB consecutive buckets; a bin's region is exactly its buckets' span,
+// and each block writes its share of every bin as one contiguous run.  The
+// block's run of bin cb starts at start(first bucket of cb) + sum over the
+// bin's buckets of their slice prefixes.  Blocks of slice 0 store start/end.
+__global__ __launch_bounds__(SORT_T) void k_msm_scatter_coarse(const uint32_t* __restrict__ dig, size_t n,
+                                                               uint32_t slice, uint32_t S, uint32_t B, uint32_t BPC,
+                                                               uint32_t n_pad, const uint32_t* __restrict__ H,
+                                                               const uint32_t* __restrict__ boff,
+                                                               const uint32_t* __restrict__ lex,
+                                                               const uint32_t* __restrict__ tot,
+                                                               uint32_t* __restrict__ start,
+                                                               uint32_t* __restrict__ end, uint2* __restrict__ tmp) {
+  __shared__ uint32_t cur[MSM_NCB];
+  const uint32_t s = blockIdx.x, w = blockIdx.y, t = threadIdx.x;
+  const uint32_t* hp = H + ((size_t)w * S + s) * B;
+  if (t < MSM_NCB) {
+    const uint32_t k0 = w * B + t * BPC;
+    cur[t] = w * n_pad + boff[k0 / SCAN_T] + lex[k0];
+  }
+  __syncthreads();
+  for (uint32_t i = t; i < B; i += SORT_T) {
+    const uint32_t k = w * B + i;
+    atomicAdd(&cur[i / BPC], hp[i]);
+    if (s == 0) {
+      const uint32_t st = w * n_pad + boff[k / SCAN_T] + lex[k];
+      start[k] = st;
+      end[k] = st + tot[k];
+    }
+  }
+  __syncthreads();
+  const size_t lo = (size_t)s * slice, hi = min(n, lo + slice);
+  const uint32_t* d = dig + (size_t)w * n;
+  const uint32_t kb = w * B - 1;
+  for (size_t p0 = lo + t; p0 < hi; p0 += (size_t)SORT_T * SORT_U) {
+    uint32_t v[SORT_U];
+#pragma unroll
+    for (int u = 0; u < SORT_U; u++) {
+      const size_t p = p0 + (size_t)u * SORT_T;
+      v[u] = p < hi ? d[p] : 0u;
+    }
+#pragma unroll
+    for (int u = 0; u < SORT_U; u++) {
+      const uint32_t m = v[u] & 0x7fffffffu;
+      if (m) {
+        const uint32_t pos = atomicAdd(&cur[(m - 1) / BPC], 1u);
+        tmp[pos] = make_uint2(kb + m, (uint32_t)(p0 + (size_t)u * SORT_T) | (v[u] & 0x80000000u));
+      }
+    }
+  }
+}
+
+// Pass 2 (block per window x coarse bin): LDS cursors for the bin's BPC
+// buckets; every write stays inside the bin's region.
+__global__ __launch_bounds__(PLACE_T) void k_msm_place(const uint2* __restrict__ tmp, uint32_t B, uint32_t BPC,
+                                                       const uint32_t* __restrict__ start,
+                                                       const uint32_t* __restrict__ end, uint2* __restrict__ out) {
+  __shared__ uint32_t cur[MSM_BPC_MAX];
+  const uint32_t cb = blockIdx.x, w = blockIdx.y, t = threadIdx.x;
+  const uint32_t k0 = w * B + cb * BPC;
+  for (uint32_t j = t; j < BPC; j += PLACE_T) cur[j] = start[k0 + j];
+  const uint32_t lo = start[k0], hi = end[k0 + BPC - 1];
+  __syncthreads();
+  for (uint32_t p0 = lo + t; p0 < hi; p0 += PLACE_T * SORT_U) {
+    uint2 e[SORT_U];
+#pragma unroll
+    for (int u = 0; u < SORT_U; u++) {
+      const uint32_t p = p0 + u * PLACE_T;
+      e[u] = p < hi ? tmp[p] : make_uint2(KEY_INVALID, 0u);
+    }
+#pragma unroll
+    for (int u = 0; u < SORT_U; u++) {
+      if (e[u].x != KEY_INVALID) {
+        const uint32_t pos = atomicAdd(&cur[e[u].x - k0], 1u);
+        out[pos] = e[u];
+      }
+    }
+  }
+}
+
 // ------------------------------------------------------------------ accumulate
 template <class F>
 struct ChunkSlots {
@@ -581,15 +668,15 @@ __global__ __launch_bounds__(KMAX) void k_msm_reduce2(const xyzz<F>* __restrict_
 
 // ------------------------------------------------------------------ workspace
 struct MsmWorkspace {
-  DevBuf recs, dig, hist, tot, lex, bsum, bmax, boff, sorted, start, end, wstat, buckets, hkey, tkey, hpt, tpt, seg,
-      grp, win;
+  DevBuf recs, dig, hist, tot, lex, bsum, bmax, boff, tmp, sorted, start, end, wstat, buckets, hkey, tkey, hpt, tpt,
+      seg, grp, win;
   uint32_t* h_stat = nullptr;  // pinned, 2 words per window
   hipEvent_t stat_ready = nullptr;
 };
 
 void msm_workspace_free(MsmWorkspace* ws) {
   if (!ws) return;
-  for (DevBuf* b : {&ws->recs, &ws->dig, &ws->hist, &ws->tot, &ws->lex, &ws->bsum, &ws->bmax, &ws->boff,
+  for (DevBuf* b : {&ws->recs, &ws->dig, &ws->hist, &ws->tot, &ws->lex, &ws->bsum, &ws->bmax, &ws->boff, &ws->tmp,
                     &ws->sorted, &ws->start, &ws->end, &ws->wstat, &ws->buckets, &ws->hkey, &ws->tkey, &ws->hpt,
                     &ws->tpt, &ws->seg, &ws->grp, &ws->win})
     if (b->p) (void)hipFree(b->p);
@@ -758,8 +845,13 @@ static int msm_run_recs(zk_context* ctx, MsmWorkspace& ws, const uint4* recs, co
     ZK_LAUNCH(ctx, st, "msm_scatter", k_msm_scatter<4096>, dim3(S, W), dim3(SORT_T), 0, dig, n, slice, S, B, n_pad,
               hist, boff, lex, tot, start, end, sorted);
   } else {
-    ZK_LAUNCH(ctx, st, "msm_scatter", k_msm_scatter<32768>, dim3(S, W), dim3(SORT_T), 0, dig, n, slice, S, B, n_pad,
-              hist, boff, lex, tot, start, end, sorted);
+    const uint32_t BPC = B / MSM_NCB;  // 32..128
+    ZK_TRY(ctx->ensure(ws.tmp, (size_t)W * n_pad * 8));
+    uint2* tmp = (uint2*)ws.tmp.p;
+    ZK_LAUNCH(ctx, st, "msm_scatter", k_msm_scatter_coarse, dim3(S, W), dim3(SORT_T), 0, dig, n, slice, S, B, BPC,
+              n_pad, hist, boff, lex, tot, start, end, tmp);
+    ZK_LAUNCH(ctx, st, "msm_place", k_msm_place, dim3(MSM_NCB, W), dim3(PLACE_T), 0, tmp, B, BPC, start, end,
+              sorted);
   }
 
   ChunkSlots<F> slots{(uint32_t*)ws.hkey.p, (uint32_t*)ws.tkey.p, (xyzz<F>*)ws.hpt.p, (xyzz<F>*)ws.tpt.p};
