@@ -55,48 +55,35 @@ constexpr size_t MSM_MAX_N = (size_t)1 << 26;  // keeps W * n_pad below 2^32
 constexpr int MSM_BITS = 254;
 
 // ------------------------------------------------------------------ point records
-// G1 record: x[9], y[9], inf, pad  (80 bytes);  G2 record: x0,x1,y0,y1 [9 each],
-// inf, pad[3] (160 bytes).  Coordinates in internal form, canonical.
+// One record per point, exactly one 64-byte (G1) / 128-byte (G2) line so that
+// a random gather in the accumulation touches a single line: every
+// coordinate is the canonical internal-form value (x * 2^261 mod q) packed as
+// 8 little-endian 32-bit words; x = y = 0 encodes the point at infinity (no
+// finite point of y^2 = x^3 + 3 has x = y = 0).  G1: x, y; G2: x.c0, x.c1,
+// y.c0, y.c1.
 template <class F>
 struct Rec;
 template <>
 struct Rec<fq> {
-  static constexpr int WORDS = 20;
-  static constexpr int EXT_WORDS = 16;  // 64 external bytes
+  static constexpr int WORDS = 16;
 };
 template <>
 struct Rec<fq2> {
-  static constexpr int WORDS = 40;
-  static constexpr int EXT_WORDS = 32;  // 128 external bytes
+  static constexpr int WORDS = 32;
 };
 
-__device__ __forceinline__ fq load_fq9(const uint32_t* p) {
-  fq r;
-#pragma unroll
-  for (int i = 0; i < NL; i++) r.l[i] = p[i];
-  return r;
+__device__ __forceinline__ void unpack_coord(const uint32_t* p, fq& a) { a = repack_in<FqP>(p); }
+__device__ __forceinline__ void unpack_coord(const uint32_t* p, fq2& a) {
+  a.c0 = repack_in<FqP>(p);
+  a.c1 = repack_in<FqP>(p + 8);
 }
-__device__ __forceinline__ void store_fq9(uint32_t* p, const fq& a) {
-#pragma unroll
-  for (int i = 0; i < NL; i++) p[i] = a.l[i];
-}
-
-__device__ __forceinline__ void load_coord(const uint32_t* p, fq& a) { a = load_fq9(p); }
-__device__ __forceinline__ void load_coord(const uint32_t* p, fq2& a) {
-  a.c0 = load_fq9(p);
-  a.c1 = load_fq9(p + NL);
-}
-__device__ __forceinline__ void store_coord(uint32_t* p, const fq& a) { store_fq9(p, a); }
-__device__ __forceinline__ void store_coord(uint32_t* p, const fq2& a) {
-  store_fq9(p, a.c0);
-  store_fq9(p + NL, a.c1);
-}
-template <class F>
-__device__ __forceinline__ constexpr int coord_words() {
-  return sizeof(F) / 4;
+__device__ __forceinline__ void pack_coord(uint32_t* p, const fq& a) { repack_out(a, p); }
+__device__ __forceinline__ void pack_coord(uint32_t* p, const fq2& a) {
+  repack_out(a.c0, p);
+  repack_out(a.c1, p + 8);
 }
 
-// Record load through 16-byte vector loads (records are 16-byte aligned).
+// Record load through 16-byte vector loads; returns true for infinity.
 template <class F>
 __device__ __forceinline__ bool load_rec(const uint4* __restrict__ recs, uint32_t idx, F& x, F& y) {
   constexpr int W = Rec<F>::WORDS;
@@ -110,9 +97,27 @@ __device__ __forceinline__ bool load_rec(const uint4* __restrict__ recs, uint32_
     w[4 * i + 2] = v.z;
     w[4 * i + 3] = v.w;
   }
-  load_coord(w, x);
-  load_coord(w + coord_words<F>(), y);
-  return w[2 * coord_words<F>()] != 0;  // infinity flag
+  uint32_t any = 0;
+#pragma unroll
+  for (int i = 0; i < W; i++) any |= w[i];
+  unpack_coord(w, x);
+  unpack_coord(w + W / 2, y);
+  return any == 0;
+}
+
+template <class F>
+__device__ __forceinline__ void store_rec(uint4* __restrict__ recs, size_t idx, const F& x, const F& y, bool inf) {
+  constexpr int W = Rec<F>::WORDS;
+  uint32_t w[W];
+  pack_coord(w, x);
+  pack_coord(w + W / 2, y);
+  if (inf) {
+#pragma unroll
+    for (int k = 0; k < W; k++) w[k] = 0;
+  }
+  uint4* p = recs + idx * (W / 4);
+#pragma unroll
+  for (int k = 0; k < W / 4; k++) p[k] = make_uint4(w[4 * k], w[4 * k + 1], w[4 * k + 2], w[4 * k + 3]);
 }
 
 __device__ __forceinline__ void ext_to_coord(const uint32_t* e, fq& a) { a = from_mont256<FqP>(e); }
@@ -126,14 +131,14 @@ __device__ __forceinline__ void std_to_coord(const uint32_t* e, fq2& a) {
   a.c0 = from_std<FqP>(e);
   a.c1 = from_std<FqP>(e + 8);
 }
-__device__ __forceinline__ fq fcanon_coord(const fq& a) { return fcanon(a); }
-__device__ __forceinline__ fq2 fcanon_coord(const fq2& a) { return fq2{fcanon(a.c0), fcanon(a.c1)}; }
 
+// External points (zk_g1_affine / zk_g2_affine: Montgomery R = 2^256, x = y =
+// 0 for infinity) -> records.
 template <class F>
 __global__ void k_msm_convert(uint4* __restrict__ recs, const uint32_t* __restrict__ ext, size_t n) {
   size_t i = blockIdx.x * (size_t)blockDim.x + threadIdx.x;
   if (i >= n) return;
-  constexpr int EW = Rec<F>::EXT_WORDS, W = Rec<F>::WORDS, CW = coord_words<F>();
+  constexpr int EW = Rec<F>::WORDS;  // the external point has the same word count
   uint32_t e[EW];
   uint32_t any = 0;
 #pragma unroll
@@ -144,15 +149,7 @@ __global__ void k_msm_convert(uint4* __restrict__ recs, const uint32_t* __restri
   F x, y;
   ext_to_coord(e, x);
   ext_to_coord(e + EW / 2, y);
-  uint32_t w[W];
-  store_coord(w, x);
-  store_coord(w + CW, y);
-  w[2 * CW] = any == 0 ? 1u : 0u;
-#pragma unroll
-  for (int k = 2 * CW + 1; k < W; k++) w[k] = 0;
-  uint4* p = recs + i * (W / 4);
-#pragma unroll
-  for (int k = 0; k < W / 4; k++) p[k] = make_uint4(w[4 * k], w[4 * k + 1], w[4 * k + 2], w[4 * k + 3]);
+  store_rec(recs, i, x, y, any == 0);
 }
 
 // ------------------------------------------------------------------ digits
@@ -963,25 +960,14 @@ __global__ void k_recs_from_std(uint4* __restrict__ recs, const uint32_t* __rest
                                 const uint8_t* __restrict__ flags, size_t n) {
   size_t i = blockIdx.x * (size_t)blockDim.x + threadIdx.x;
   if (i >= n) return;
-  constexpr int EW = Rec<F>::EXT_WORDS, W = Rec<F>::WORDS, CW = coord_words<F>();
+  constexpr int EW = Rec<F>::WORDS;
   uint32_t e[EW];
 #pragma unroll
   for (int k = 0; k < EW; k++) e[k] = std_words[i * EW + k];
-  const bool inf = flags[i] != 0;
-  uint32_t w[W];
-#pragma unroll
-  for (int k = 0; k < W; k++) w[k] = 0;
-  if (!inf) {
-    F x, y;
-    std_to_coord(e, x);
-    std_to_coord(e + EW / 2, y);
-    store_coord(w, fcanon_coord(x));
-    store_coord(w + CW, fcanon_coord(y));
-  }
-  w[2 * CW] = inf ? 1u : 0u;
-  uint4* p = recs + i * (W / 4);
-#pragma unroll
-  for (int k = 0; k < W / 4; k++) p[k] = make_uint4(w[4 * k], w[4 * k + 1], w[4 * k + 2], w[4 * k + 3]);
+  F x, y;
+  std_to_coord(e, x);
+  std_to_coord(e + EW / 2, y);
+  store_rec(recs, i, x, y, flags[i] != 0);
 }
 
 int recs_from_std(zk_context* ctx, bool g2, void* d_recs, const void* d_std, const void* d_flags, size_t n,
