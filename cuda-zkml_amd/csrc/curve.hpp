@@ -33,12 +33,18 @@ ZK_HD fq2 fmul(const fq2& a, const fq2& b) {
   const fq x1[2] = {a.c0, a.c1}, y1[2] = {b.c1, b.c0};
   return fq2{fmul_sum<FqP, 2>(x0, y0), fmul_sum<FqP, 2>(x1, y1)};
 }
-// (a + bu)^2 = (a+b)(a-b) + 2ab u
+// (a + bu)^2 = (a+b)(a-b) + 2ab u; a may be a lazy value (< 4q).
 ZK_HD fq2 fsqr(const fq2& a) {
   fq ab = fmul(a.c0, a.c1);
-  return fq2{fmul(fadd_lazy(a.c0, a.c1), fsub(a.c0, a.c1)), fdbl(ab)};
+  return fq2{fmul(fadd_lazy(a.c0, a.c1), fsub_lazy4(a.c0, a.c1)), fdbl(ab)};
 }
 ZK_HD bool fis_zero(const fq2& a) { return fis_zero(a.c0) && fis_zero(a.c1); }
+ZK_HD bool fis_zero4(const fq& a) { return fis_zero4<FqP>(a); }
+ZK_HD bool fis_zero4(const fq2& a) { return fis_zero4<FqP>(a.c0) && fis_zero4<FqP>(a.c1); }
+ZK_HD fq fsub3(const fq& a, const fq& b, const fq& c) { return fsub3<FqP>(a, b, c); }
+ZK_HD fq2 fsub3(const fq2& a, const fq2& b, const fq2& c) {
+  return fq2{fsub3<FqP>(a.c0, b.c0, c.c0), fsub3<FqP>(a.c1, b.c1, c.c1)};
+}
 
 ZK_HD void fset_zero(fq& a) { a = fe_zero<FqP>(); }
 ZK_HD void fset_zero(fq2& a) { a = fq2{fe_zero<FqP>(), fe_zero<FqP>()}; }
@@ -46,17 +52,18 @@ ZK_HD void fset_one(fq& a) { a = fe_one<FqP>(); }
 ZK_HD void fset_one(fq2& a) { a = fq2{fe_one<FqP>(), fe_zero<FqP>()}; }
 
 // a*b - c*d with one Montgomery reduction per coordinate (fmul_sum, the
-// subtracted products entering as (2m - x) * y).  b may be a lazy difference
-// (fsub_m), the other inputs are reduced.
+// subtracted products entering as (km - x) * y).  a and b may be lazy values
+// (< 4m: fsub_m, fsub_r); c and d are reduced (< 2m).
 ZK_HD fq fmul_sub(const fq& a, const fq& b, const fq& c, const fq& d) { return fmul2(a, b, c, fneg_lazy(d)); }
 ZK_HD fq2 fmul_sub(const fq2& a, const fq2& b, const fq2& c, const fq2& d) {
   // real: a0 b0 - a1 b1 - c0 d0 + c1 d1, imaginary: a0 b1 + a1 b0 - c0 d1 - c1 d0
-  const fq na1 = fneg_lazy(a.c1), nc0 = fneg_lazy(c.c0), nc1 = fneg_lazy(c.c1);
+  const fq na1 = fneg_lazy4(a.c1), nc0 = fneg_lazy(c.c0), nc1 = fneg_lazy(c.c1);
   const fq x0[4] = {a.c0, na1, nc0, c.c1}, y0[4] = {b.c0, b.c1, d.c0, d.c1};
   const fq x1[4] = {a.c0, a.c1, nc0, nc1}, y1[4] = {b.c1, b.c0, d.c1, d.c0};
   return fq2{fmul_sum<FqP, 4>(x0, y0), fmul_sum<FqP, 4>(x1, y1)};
 }
-// a - b left in (0, 4m): only for the second factor of fmul_sub.
+// a - b left in (0, 4m) for reduced a, b: only as an fmul_sub factor or an
+// fsqr input.
 ZK_HD fq fsub_m(const fq& a, const fq& b) { return fsub_lazy(a, b); }
 ZK_HD fq2 fsub_m(const fq2& a, const fq2& b) { return fq2{fsub_lazy(a.c0, b.c0), fsub_lazy(a.c1, b.c1)}; }
 
@@ -96,7 +103,9 @@ ZK_HD void xyzz_mdbl(xyzz<F>& p, const F& x, const F& y) {
   F s = fmul(x, v);
   F x2 = fsqr(x);
   F m = fadd(fdbl(x2), x2);
-  F x3 = fsub(fsub(fsqr(m), s), s);
+  F zero;
+  fset_zero(zero);
+  F x3 = fsub3(fsqr(m), zero, s);
   F y3 = fmul_sub(m, fsub_m(s, x3), w, y);
   p.x = x3;
   p.y = y3;
@@ -114,7 +123,9 @@ ZK_HD void xyzz_dbl(xyzz<F>& p) {
   F s = fmul(p.x, v);
   F x2 = fsqr(p.x);
   F m = fadd(fdbl(x2), x2);
-  F x3 = fsub(fsub(fsqr(m), s), s);
+  F zero;
+  fset_zero(zero);
+  F x3 = fsub3(fsqr(m), zero, s);
   F y3 = fmul_sub(m, fsub_m(s, x3), w, p.y);
   p.x = x3;
   p.y = y3;
@@ -123,30 +134,41 @@ ZK_HD void xyzz_dbl(xyzz<F>& p) {
 }
 
 // p += (x2, y2) affine, finite (madd-2008-s)
+// p += (x2, y2) for a finite p; returns true when the sum is the point at
+// infinity (then p is set to it).
+template <class F>
+ZK_HD bool xyzz_madd_fin(xyzz<F>& p, const F& x2, const F& y2) {
+  F u2 = fmul(x2, p.zz);
+  F s2 = fmul(y2, p.zzz);
+  F P = fsub(u2, p.x);
+  F R = fsub_m(s2, p.y);  // lazy, (0, 4m)
+  if (fis_zero(P)) {
+    if (fis_zero4(R)) {
+      xyzz_mdbl(p, x2, y2);
+      return false;
+    }
+    xyzz_set_inf(p);
+    return true;
+  }
+  F pp = fsqr(P);
+  F ppp = fmul(P, pp);
+  F q = fmul(p.x, pp);
+  F x3 = fsub3(fsqr(R), ppp, q);
+  F y3 = fmul_sub(R, fsub_m(q, x3), p.y, ppp);
+  p.x = x3;
+  p.y = y3;
+  p.zz = fmul(p.zz, pp);
+  p.zzz = fmul(p.zzz, ppp);
+  return false;
+}
+
 template <class F>
 ZK_HD void xyzz_madd(xyzz<F>& p, const F& x2, const F& y2) {
   if (xyzz_is_inf(p)) {
     xyzz_set_affine(p, x2, y2);
     return;
   }
-  F u2 = fmul(x2, p.zz);
-  F s2 = fmul(y2, p.zzz);
-  F P = fsub(u2, p.x);
-  F R = fsub(s2, p.y);
-  if (fis_zero(P)) {
-    if (fis_zero(R)) xyzz_mdbl(p, x2, y2);
-    else xyzz_set_inf(p);
-    return;
-  }
-  F pp = fsqr(P);
-  F ppp = fmul(P, pp);
-  F q = fmul(p.x, pp);
-  F x3 = fsub(fsub(fsqr(R), ppp), fdbl(q));
-  F y3 = fmul_sub(R, fsub_m(q, x3), p.y, ppp);
-  p.x = x3;
-  p.y = y3;
-  p.zz = fmul(p.zz, pp);
-  p.zzz = fmul(p.zzz, ppp);
+  (void)xyzz_madd_fin(p, x2, y2);
 }
 
 // p += q (add-2008-s)
@@ -162,16 +184,16 @@ ZK_HD void xyzz_add(xyzz<F>& p, const xyzz<F>& q) {
   F s1 = fmul(p.y, q.zzz);
   F s2 = fmul(q.y, p.zzz);
   F P = fsub(u2, u1);
-  F R = fsub(s2, s1);
+  F R = fsub_m(s2, s1);  // lazy, (0, 4m)
   if (fis_zero(P)) {
-    if (fis_zero(R)) xyzz_dbl(p);
+    if (fis_zero4(R)) xyzz_dbl(p);
     else xyzz_set_inf(p);
     return;
   }
   F pp = fsqr(P);
   F ppp = fmul(P, pp);
   F qq = fmul(u1, pp);
-  F x3 = fsub(fsub(fsqr(R), ppp), fdbl(qq));
+  F x3 = fsub3(fsqr(R), ppp, qq);
   F y3 = fmul_sub(R, fsub_m(qq, x3), s1, ppp);
   p.x = x3;
   p.y = y3;

@@ -41,6 +41,12 @@ struct FqP {
                                       0x02db40c0u, 0x00a6e141u, 0x0e5c2634u, 0x0030644eu};
   static constexpr uint32_t MOD2[9] = {0x10f9fa8eu, 0x0208c16du, 0x18e5469eu, 0x05aa45a1u, 0x0b0bb2f0u,
                                        0x05b68181u, 0x014dc282u, 0x1cb84c68u, 0x0060c89cu};
+  static constexpr uint32_t MOD3[9] = {0x0976f7d5u, 0x030d2224u, 0x1557e9edu, 0x087f6872u, 0x00918c68u,
+                                       0x0891c242u, 0x01f4a3c3u, 0x0b14729cu, 0x00912cebu};
+  static constexpr uint32_t MOD4[9] = {0x01f3f51cu, 0x041182dbu, 0x11ca8d3cu, 0x0b548b43u, 0x161765e0u,
+                                       0x0b6d0302u, 0x029b8504u, 0x197098d0u, 0x00c19139u};
+  static constexpr uint32_t MOD6[9] = {0x12edefaau, 0x061a4448u, 0x0aafd3dau, 0x10fed0e5u, 0x012318d0u,
+                                       0x11238484u, 0x03e94786u, 0x1628e538u, 0x012259d6u};
   static constexpr uint32_t INV = 0x04866389u;  // -q^-1 mod 2^29
   static constexpr uint32_t ONE[9] = {0x157ccc21u, 0x141c2758u, 0x185230d3u, 0x014c0419u, 0x0aa36fb9u,
                                       0x1d4240ceu, 0x11d54c07u, 0x052ac7a8u, 0x000dc836u};  // 2^261 mod q
@@ -59,6 +65,12 @@ struct FrP {
                                       0x02db40c0u, 0x00a6e141u, 0x0e5c2634u, 0x0030644eu};
   static constexpr uint32_t MOD2[9] = {0x00000002u, 0x1e1f593fu, 0x1cb848a1u, 0x0fa121e6u, 0x0b0ba506u,
                                        0x05b68181u, 0x014dc282u, 0x1cb84c68u, 0x0060c89cu};
+  static constexpr uint32_t MOD3[9] = {0x10000003u, 0x1d2f05deu, 0x0b146cf2u, 0x1771b2dau, 0x00917789u,
+                                       0x0891c242u, 0x01f4a3c3u, 0x0b14729cu, 0x00912cebu};
+  static constexpr uint32_t MOD4[9] = {0x00000004u, 0x1c3eb27eu, 0x19709143u, 0x1f4243cdu, 0x16174a0cu,
+                                       0x0b6d0302u, 0x029b8504u, 0x197098d0u, 0x00c19139u};
+  static constexpr uint32_t MOD6[9] = {0x00000006u, 0x1a5e0bbdu, 0x1628d9e5u, 0x0ee365b4u, 0x0122ef13u,
+                                       0x11238484u, 0x03e94786u, 0x1628e538u, 0x012259d6u};
   static constexpr uint32_t INV = 0x0fffffffu;  // -r^-1 mod 2^29
   static constexpr uint32_t ONE[9] = {0x0fffff57u, 0x1ea70ab4u, 0x052c068bu, 0x17504f49u, 0x0aa8075bu,
                                       0x1d4240ceu, 0x11d54c07u, 0x052ac7a8u, 0x000dc836u};  // 2^261 mod r
@@ -132,10 +144,9 @@ ZK_HD fe<P> fmul(const fe<P>& a, const fe<P>& b) {
 }
 
 // sum_t a[t]*b[t] * 2^-261 mod m, N <= 4, with one Montgomery reduction for
-// all products.  Inputs: normalized limbs (< 2^29); a[t] < 2m and b[t] < 4m
-// (or both < 4m when N <= 2).  Every column then holds at most 9N + 9 terms
-// below 2^58 plus a carry below 2^35, which stays below 2^64, and the result
-// is below 32m^2 / 2^261 + m < 2m.
+// all products.  Inputs: normalized limbs (< 2^29), values <= 4m.  Every
+// column then holds at most 9N + 9 terms below 2^58 plus a carry below 2^35,
+// which stays below 2^64, and the result is below 64m^2 / 2^261 + m < 1.4m.
 template <class P, int N>
 ZK_HD fe<P> fmul_sum(const fe<P> (&a)[N], const fe<P> (&b)[N]) {
   static_assert(N >= 1 && N <= 4, "column accumulator bound");
@@ -322,13 +333,91 @@ ZK_HD fe<P> fcanon(const fe<P>& a) {
   return r;
 }
 
+// a == 0 mod m for a in [0, 2m): a is 0 or m.
 template <class P>
 ZK_HD bool fis_zero(const fe<P>& a) {
-  fe<P> c = fcanon(a);
-  uint32_t o = 0;
+  uint32_t z = 0, e = 0;
 #pragma unroll
-  for (int i = 0; i < NL; i++) o |= c.l[i];
-  return o == 0;
+  for (int i = 0; i < NL; i++) {
+    z |= a.l[i];
+    e |= a.l[i] ^ P::MOD[i];
+  }
+  return z == 0 || e == 0;
+}
+
+// a == 0 mod m for a in [0, 4m): a is 0, m, 2m or 3m.
+template <class P>
+ZK_HD bool fis_zero4(const fe<P>& a) {
+  uint32_t z = 0, e1 = 0, e2 = 0, e3 = 0;
+#pragma unroll
+  for (int i = 0; i < NL; i++) {
+    z |= a.l[i];
+    e1 |= a.l[i] ^ P::MOD[i];
+    e2 |= a.l[i] ^ P::MOD2[i];
+    e3 |= a.l[i] ^ P::MOD3[i];
+  }
+  return z == 0 || e1 == 0 || e2 == 0 || e3 == 0;
+}
+
+// t - K if t >= K (K normalized limbs), else t.
+template <class P>
+ZK_HD fe<P> fcsub(const fe<P>& t, const uint32_t (&K)[NL]) {
+  fe<P> u;
+  int32_t br = 0;
+#pragma unroll
+  for (int i = 0; i < NL; i++) {
+    int32_t v = (int32_t)t.l[i] - (int32_t)K[i] + br;
+    br = v >> 29;
+    u.l[i] = (uint32_t)v & LMASK;
+  }
+  fe<P> r;
+#pragma unroll
+  for (int i = 0; i < NL; i++) r.l[i] = br ? t.l[i] : u.l[i];
+  return r;
+}
+
+// (a - b - 2c) mod m into [0, 2m) for a, b, c in [0, 2m): one pass forms
+// a + 6m - b - 2c in (0, 8m), then two conditional subtractions of 4m, 2m.
+template <class P>
+ZK_HD fe<P> fsub3(const fe<P>& a, const fe<P>& b, const fe<P>& c) {
+  fe<P> t;
+  int32_t cy = 0;
+#pragma unroll
+  for (int i = 0; i < NL; i++) {
+    int32_t v = (int32_t)a.l[i] + (int32_t)P::MOD6[i] - (int32_t)b.l[i] - 2 * (int32_t)c.l[i] + cy;
+    cy = v >> 29;
+    t.l[i] = (uint32_t)v & LMASK;
+  }
+  return fcsub(fcsub(t, P::MOD4), P::MOD2);
+}
+
+// a - b + 4m for a in [0, 4m), b in [0, 4m]: value in (0, 8m), normalized
+// limbs.  Valid only as an fmul / fsqr input.
+template <class P>
+ZK_HD fe<P> fsub_lazy4(const fe<P>& a, const fe<P>& b) {
+  fe<P> d;
+  int32_t c = 0;
+#pragma unroll
+  for (int i = 0; i < NL; i++) {
+    int32_t v = (int32_t)a.l[i] + (int32_t)P::MOD4[i] - (int32_t)b.l[i] + c;
+    c = v >> 29;
+    d.l[i] = (uint32_t)v & LMASK;
+  }
+  return d;
+}
+
+// 4m - a for a in [0, 4m]: value in [0, 4m], normalized limbs.
+template <class P>
+ZK_HD fe<P> fneg_lazy4(const fe<P>& a) {
+  fe<P> d;
+  int32_t c = 0;
+#pragma unroll
+  for (int i = 0; i < NL; i++) {
+    int32_t v = (int32_t)P::MOD4[i] - (int32_t)a.l[i] + c;
+    c = v >> 29;
+    d.l[i] = (uint32_t)v & LMASK;
+  }
+  return d;
 }
 
 template <class P>

@@ -491,6 +491,7 @@ __global__ __launch_bounds__(256) void k_msm_accumulate(const uint2* __restrict_
     const uint32_t hi = min(lo + L0, total);
     xyzz<F> acc;
     xyzz_set_inf(acc);
+    bool empty = true;  // acc is the point at infinity
     uint32_t cur = sorted[lo].x;
     for (uint32_t p = lo; p < hi; p++) {
       const uint2 e = sorted[p];
@@ -505,12 +506,18 @@ __global__ __launch_bounds__(256) void k_msm_accumulate(const uint2* __restrict_
         }
         cur = key;
         xyzz_set_inf(acc);
+        empty = true;
       }
       const uint32_t v = e.y;
       F x, y;
       if (!load_rec(recs, v & 0x7fffffffu, x, y)) {
         if (v >> 31) y = fneg(y);
-        xyzz_madd(acc, x, y);
+        if (empty) {
+          xyzz_set_affine(acc, x, y);
+          empty = false;
+        } else {
+          empty = xyzz_madd_fin(acc, x, y);
+        }
       }
     }
     // last run of the chunk

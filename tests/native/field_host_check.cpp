@@ -34,6 +34,11 @@ int fh_op(int op, const uint32_t* a, const uint32_t* b, const uint32_t* c, const
     case 5: r = fadd(A, B); break;
     case 6: r = fsub(A, B); break;
     case 7: r = fmul_sub(A, B, C, D); break;
+    case 9: r = fsub3<FqP>(A, B, C); break;
+    case 10: r = fsub_lazy4<FqP>(A, B); break;
+    case 11: r = fneg_lazy4<FqP>(A); break;
+    case 12: r = fe_zero<FqP>(); r.l[0] = fis_zero<FqP>(A) ? 1u : 0u; break;
+    case 13: r = fe_zero<FqP>(); r.l[0] = fis_zero4<FqP>(A) ? 1u : 0u; break;
     case 8: {  // four products: a*b + c*d + a*d + c*b
       const fq x[4] = {A, C, A, C}, y[4] = {B, D, D, B};
       r = fmul_sum<FqP, 4>(x, y);

@@ -7,7 +7,8 @@ limb, carry or range assumption fails here before any kernel runs:
 
   fmul / fsqr / fmul_sum  a*b*2^-261 (sums of 2 and 4 products) mod q, result < 2q, limbs < 2^29,
                           at the edges of the documented input ranges
-  fsub_lazy / fneg_lazy   exact a - b + 2q and 2q - a
+  fsub_lazy / fneg_lazy   exact a - b + 2q and 2q - a (and the 4q forms)
+  fsub3, fis_zero(4)      a - b - 2c into [0, 2q); zero tests over [0, 2q) / [0, 4q)
   fadd / fsub / fmul_sub  congruence and the [0, 2q) output range
   XYZZ madd/add/dbl/mdbl  G1 and G2 against affine formulas, with coordinates
                           given in non-canonical [q, 2q) representatives and
@@ -104,6 +105,28 @@ def test_lazy_sub_neg_exact(fh):
         assert op(fh, 4, a) == 2 * Q - a
 
 
+def test_fused_sub_lazy4_zero_tests(fh):
+    rng = random.Random(7)
+    for a in samples(rng, 2 * Q, 20):
+        for b in samples(rng, 2 * Q, 3):
+            c = rng.randrange(2 * Q)
+            r = op(fh, 9, a, b, c)  # a - b - 2c into [0, 2q)
+            assert r < 2 * Q and r % Q == (a - b - 2 * c) % Q
+    for a, b, c in ((0, 2 * Q - 1, 2 * Q - 1), (2 * Q - 1, 0, 0), (Q, Q, Q)):
+        r = op(fh, 9, a, b, c)
+        assert r < 2 * Q and r % Q == (a - b - 2 * c) % Q
+    for a in samples(rng, 4 * Q, 10):
+        for b in samples(rng, 4 * Q, 3) + [4 * Q]:
+            assert op(fh, 10, a, b) == a + 4 * Q - b
+    for a in samples(rng, 4 * Q, 10) + [4 * Q]:
+        assert op(fh, 11, a) == 4 * Q - a
+    # zero tests: exactly the multiples of q inside the documented ranges
+    for a in [0, Q, 1, Q - 1, Q + 1, 2 * Q - 1] + [rng.randrange(2 * Q) for _ in range(50)]:
+        assert op(fh, 12, a) == (1 if a % Q == 0 else 0)
+    for a in [0, Q, 2 * Q, 3 * Q, 1, 2 * Q + 1, 3 * Q - 1, 4 * Q - 1] + [rng.randrange(4 * Q) for _ in range(50)]:
+        assert op(fh, 13, a) == (1 if a % Q == 0 else 0)
+
+
 def test_add_sub_mulsub(fh):
     rng = random.Random(4)
     for a in samples(rng, 2 * Q):
@@ -113,8 +136,8 @@ def test_add_sub_mulsub(fh):
             assert s < 2 * Q and s % Q == (a + b) % Q
             assert d < 2 * Q and d % Q == (a - b) % Q
     for _ in range(200):
-        a, c, d = (rng.randrange(2 * Q) for _ in range(3))
-        b = rng.randrange(4 * Q)  # the lazy factor
+        c, d = (rng.randrange(2 * Q) for _ in range(2))
+        a, b = rng.randrange(4 * Q), rng.randrange(4 * Q)  # the lazy factors
         r = op(fh, 7, a, b, c, d)
         assert r < 2 * Q and r % Q == (a * b - c * d) * RP_INV % Q
 
