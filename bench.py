@@ -110,6 +110,13 @@ def main():
     acc_ms = acc["ms_per_step"] / max(acc["launches_per_step"], 1)
     acc_mads = n * windows * 10 * MADS_PER_FIELD_MUL
     achieved = acc_mads / (acc_ms * 1e-3) / 1e12
+    # HBM bytes per launch of the same kernel, from the committed rocprofv3
+    # FETCH_SIZE / WRITE_SIZE runs (profiles/msm_2e20_pmc_traffic.md), scaled by
+    # the counters' reading for a plain copy of known size
+    traffic = None
+    tpath = os.path.join(ROOT, "profiles", "msm_2e20_pmc_traffic.json")
+    if args.log_n == 20 and os.path.exists(tpath):
+        traffic = json.load(open(tpath)).get("msm_accumulate_bytes_per_launch")
     # whole-MSM VALU fraction with BASELINE.md's algorithmic count
     f_mults = msm_algorithmic_mults(n, best_c(n))
     msm_frac = f_mults * MADS_PER_FIELD_MUL / (ms_step * 1e-3) / 1e12 / PEAK_MAD_TOPS
@@ -200,7 +207,7 @@ def main():
         "config": {"workload": f"G1 MSM, n = 2^{args.log_n}, BASELINE config 3 (uniform scalars)",
                    "window_bits": c, "windows": windows},
         "roofline": {"bound": "valu", "achieved": round(achieved, 3), "peak": round(PEAK_MAD_TOPS, 2),
-                     "unit": "T mad32/s", "frac": round(achieved / PEAK_MAD_TOPS, 4), "traffic": None,
+                     "unit": "T mad32/s", "frac": round(achieved / PEAK_MAD_TOPS, 4), "traffic": traffic,
                      "kernel": "msm_accumulate", "kernel_ms": round(acc_ms, 4)},
         "msm_valu_frac_whole": round(msm_frac, 4),
         "kernels_ms_per_step": {k_: round(v["ms_per_step"], 4) for k_, v in kernels.items()},
