@@ -65,6 +65,10 @@ def lib():
         L.zk_pk_info.argtypes = [vp] + [ctypes.POINTER(ctypes.c_int)] * 3
         L.zk_setup.argtypes = [vp, vp, ctypes.c_uint64, ctypes.c_char_p, ctypes.c_char_p]
         L.zk_prove.argtypes = [vp, vp, vp, vp, ctypes.c_size_t, ctypes.c_int, ctypes.c_uint64, ctypes.c_int, vp, vp]
+        L.zk_pairing.argtypes = [vp, vp, vp]
+        L.zk_verify.argtypes = [vp, ctypes.c_size_t, vp, vp, ctypes.c_int, ctypes.POINTER(ctypes.c_int)]
+        L.zk_verify_files.argtypes = [ctypes.c_char_p, ctypes.c_char_p, ctypes.c_char_p,
+                                      ctypes.POINTER(ctypes.c_int)]
         _lib = L
     return _lib
 
@@ -263,6 +267,39 @@ class Context:
 
     def quotient_h(self, r1cs, d_witness, m, d_h):
         self._check(lib().zk_quotient_h(self.h, r1cs.h, vp(d_witness.ptr), m, vp(d_h.ptr), None), "zk_quotient_h")
+
+
+def pairing(p_std, q_std):
+    """e(P, Q): P (8,) u64 standard form x, y; Q (16,) u64.  Returns (48,) u64,
+    the Fp12 value in standard form (12 Fq elements, reference order)."""
+    p = np.ascontiguousarray(p_std, dtype=np.uint64)
+    q = np.ascontiguousarray(q_std, dtype=np.uint64)
+    out = np.zeros(48, dtype=np.uint64)
+    st = lib().zk_pairing(_np_ptr(p), _np_ptr(q), _np_ptr(out))
+    if st:
+        raise ZkError(f"zk_pairing failed ({lib().zk_status_string(st).decode()})")
+    return out
+
+
+def verify(vk_bytes, proof_bytes, publics_std):
+    """Groth16 verification (host).  publics_std: (npub, 4) u64 standard form."""
+    pub = np.ascontiguousarray(publics_std, dtype=np.uint64).reshape(-1, 4)
+    vk = np.frombuffer(bytes(vk_bytes), dtype=np.uint8).copy()
+    pr = np.frombuffer(bytes(proof_bytes), dtype=np.uint8).copy()
+    ok = ctypes.c_int(0)
+    st = lib().zk_verify(_np_ptr(vk), vk.size, _np_ptr(pr), _np_ptr(pub) if pub.size else None, pub.shape[0],
+                         ctypes.byref(ok))
+    if st:
+        raise ZkError(f"zk_verify failed ({lib().zk_status_string(st).decode()})")
+    return bool(ok.value)
+
+
+def verify_files(vk_path, proof_path, publics_path):
+    ok = ctypes.c_int(0)
+    st = lib().zk_verify_files(vk_path.encode(), proof_path.encode(), publics_path.encode(), ctypes.byref(ok))
+    if st:
+        raise ZkError(f"zk_verify_files failed ({lib().zk_status_string(st).decode()})")
+    return bool(ok.value)
 
 
 class R1CS:

@@ -158,6 +158,28 @@ int zk_setup(zk_context* ctx, const zk_r1cs* r1cs, uint64_t toxic_seed, const ch
 int zk_prove(zk_context* ctx, const zk_pk* pk, const zk_r1cs* r1cs, const void* h_witness, size_t m,
              int num_public, uint64_t blind_seed, int check_witness, uint8_t proof_out[256], double* timings_ms);
 
+/* ---- pairing and verification (host code, no device needed) -------------
+ * zk_pairing replaces bn254::pairing (src/curve/pairing.cuh:198-282): the
+ * reduced optimal ate pairing e(P, Q).  P: 64 bytes x, y; Q: 128 bytes x.c0,
+ * x.c1, y.c0, y.c1; both standard form little endian, all-zero = infinity.
+ * out: the Fp12 value as 12 x 32 bytes standard form in the reference's order
+ * (c0.c0.c0, c0.c0.c1, c0.c1.c0, ..., c1.c2.c1).
+ * zk_verify replaces Groth16Verifier::verify (groth16.cu:967-1022): vk_bytes
+ * is a verification-key file image (verifier.cu:103-148), proof256 a proof
+ * file image, publics npub x 32-byte standard-form scalars.  *valid = 1 when
+ * e(-A, B) e(alpha, beta) e(vk_x, gamma) e(C, delta) == 1; a public-input
+ * count other than the key's rejects (valid = 0, status ZK_OK), as in the
+ * reference.  A and C must be on the curve and B on the twist and in the
+ * order-r subgroup (the reference does not check; it would reject such
+ * points only by chance).
+ * zk_verify_files replaces zkml-verify's loading (src/cli/verify.cu): the
+ * public-input file is .bin (i32 count + 32-byte scalars) or .json (decimal
+ * list). */
+int zk_pairing(const void* p_std, const void* q_std, void* out_std);
+int zk_verify(const void* vk_bytes, size_t vk_len, const void* proof256, const void* publics_std, int npub,
+              int* valid);
+int zk_verify_files(const char* vk_path, const char* proof_path, const char* publics_path, int* valid);
+
 #ifdef __cplusplus
 }
 #endif

@@ -100,6 +100,18 @@ void ref_msm_g2_small(const uint64_t* pts, const uint64_t* sc, size_t n, uint64_
   out_g2(acc.to_affine(), o);
 }
 
+// Reduced optimal ate pairing with the reference's code (src/curve/pairing.cuh:
+// 252-255).  p, q: Montgomery words as above; o: the Fp12 result as six Fp2
+// (c0.c0, c0.c1, c0.c2, c1.c0, c1.c1, c1.c2), each c0 then c1, Montgomery words.
+void ref_pairing(const uint64_t* p, const uint64_t* q, uint64_t* o) {
+  Fp12 f = pairing(in_g1(p), in_g2(q));
+  const Fp2* c[6] = {&f.c0.c0, &f.c0.c1, &f.c0.c2, &f.c1.c0, &f.c1.c1, &f.c1.c2};
+  for (int i = 0; i < 6; i++) {
+    memcpy(o + 8 * i, c[i]->c0.val, 32);
+    memcpy(o + 8 * i + 4, c[i]->c1.val, 32);
+  }
+}
+
 // Groth16 verification of artefact files with the reference's loaders and
 // pairing.  Returns 1 valid, 0 invalid, -1 on a load error.
 int ref_verify_files(const char* vk_path, const char* proof_path, const char* pub_path) {
