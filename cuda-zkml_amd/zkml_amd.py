@@ -65,6 +65,17 @@ def lib():
         L.zk_pk_info.argtypes = [vp] + [ctypes.POINTER(ctypes.c_int)] * 3
         L.zk_setup.argtypes = [vp, vp, ctypes.c_uint64, ctypes.c_char_p, ctypes.c_char_p]
         L.zk_prove.argtypes = [vp, vp, vp, vp, ctypes.c_size_t, ctypes.c_int, ctypes.c_uint64, ctypes.c_int, vp, vp]
+        ip = ctypes.POINTER(ctypes.c_int)
+        sp = ctypes.POINTER(ctypes.c_size_t)
+        L.zk_iden3_r1cs_info.argtypes = [ctypes.c_char_p, ip, ip, ip, ip, sp, sp, sp]
+        L.zk_iden3_r1cs_read.argtypes = [ctypes.c_char_p, vp, vp, vp]
+        L.zk_iden3_r1cs_write.argtypes = [ctypes.c_char_p, ctypes.c_int, ctypes.c_int, ctypes.c_int, ctypes.c_int,
+                                          vp, ctypes.c_size_t, vp, ctypes.c_size_t, vp, ctypes.c_size_t]
+        L.zk_wtns_info.argtypes = [ctypes.c_char_p, sp]
+        L.zk_wtns_read.argtypes = [ctypes.c_char_p, vp, ctypes.c_size_t]
+        L.zk_wtns_write.argtypes = [ctypes.c_char_p, vp, ctypes.c_size_t]
+        L.zk_synthetic_r1cs.argtypes = [ctypes.c_int, ctypes.c_int, ctypes.c_int, ctypes.c_uint64, vp, sp, vp, sp,
+                                        vp, sp, vp]
         L.zk_pairing.argtypes = [vp, vp, vp]
         L.zk_verify.argtypes = [vp, ctypes.c_size_t, vp, vp, ctypes.c_int, ctypes.POINTER(ctypes.c_int)]
         L.zk_verify_files.argtypes = [ctypes.c_char_p, ctypes.c_char_p, ctypes.c_char_p,
@@ -267,6 +278,62 @@ class Context:
 
     def quotient_h(self, r1cs, d_witness, m, d_h):
         self._check(lib().zk_quotient_h(self.h, r1cs.h, vp(d_witness.ptr), m, vp(d_h.ptr), None), "zk_quotient_h")
+
+
+def _status(st, what):
+    if st:
+        raise ZkError(f"{what} failed ({lib().zk_status_string(st).decode()})")
+
+
+def _opt_ptr(a):
+    return _np_ptr(a) if len(a) else None
+
+
+def iden3_r1cs_read(path):
+    """(num_constraints, num_variables, num_public, num_private, A, B, C) from an
+    iden3 .r1cs file; A, B, C as SPARSE_DTYPE arrays (Montgomery values)."""
+    nc, nv, npub, npriv = (ctypes.c_int() for _ in range(4))
+    na, nb, ncc = (ctypes.c_size_t() for _ in range(3))
+    _status(lib().zk_iden3_r1cs_info(path.encode(), ctypes.byref(nc), ctypes.byref(nv), ctypes.byref(npub),
+                                     ctypes.byref(npriv), ctypes.byref(na), ctypes.byref(nb), ctypes.byref(ncc)),
+            "zk_iden3_r1cs_info")
+    mats = [np.zeros(k.value, dtype=SPARSE_DTYPE) for k in (na, nb, ncc)]
+    _status(lib().zk_iden3_r1cs_read(path.encode(), *[_opt_ptr(m) for m in mats]), "zk_iden3_r1cs_read")
+    return (nc.value, nv.value, npub.value, npriv.value, *mats)
+
+
+def iden3_r1cs_write(path, num_constraints, num_variables, num_public, num_private, A, B, C):
+    mats = [np.ascontiguousarray(M if isinstance(M, np.ndarray) else sparse_entries(*M)) for M in (A, B, C)]
+    _status(lib().zk_iden3_r1cs_write(path.encode(), num_constraints, num_variables, num_public, num_private,
+                                      _opt_ptr(mats[0]), len(mats[0]), _opt_ptr(mats[1]), len(mats[1]),
+                                      _opt_ptr(mats[2]), len(mats[2])), "zk_iden3_r1cs_write")
+
+
+def wtns_read(path):
+    m = ctypes.c_size_t()
+    _status(lib().zk_wtns_info(path.encode(), ctypes.byref(m)), "zk_wtns_info")
+    w = np.zeros((m.value, 4), dtype=np.uint64)
+    _status(lib().zk_wtns_read(path.encode(), _np_ptr(w), m.value), "zk_wtns_read")
+    return w
+
+
+def wtns_write(path, w_mont):
+    w = np.ascontiguousarray(w_mont, dtype=np.uint64).reshape(-1, 4)
+    _status(lib().zk_wtns_write(path.encode(), _np_ptr(w), w.shape[0]), "zk_wtns_write")
+
+
+def synthetic_r1cs(num_constraints, num_public, num_inputs, seed):
+    """Config-5 style random R1CS: (A, B, C, witness) with the witness in
+    Montgomery words; num_variables = witness rows."""
+    A = np.zeros(3 * num_constraints, dtype=SPARSE_DTYPE)
+    B = np.zeros(3 * num_constraints, dtype=SPARSE_DTYPE)
+    C = np.zeros(num_constraints, dtype=SPARSE_DTYPE)
+    w = np.zeros((1 + num_public + num_inputs + num_constraints, 4), dtype=np.uint64)
+    na, nb, ncc = (ctypes.c_size_t() for _ in range(3))
+    _status(lib().zk_synthetic_r1cs(num_constraints, num_public, num_inputs, seed, _opt_ptr(A), ctypes.byref(na),
+                                    _opt_ptr(B), ctypes.byref(nb), _opt_ptr(C), ctypes.byref(ncc), _np_ptr(w)),
+            "zk_synthetic_r1cs")
+    return A[:na.value].copy(), B[:nb.value].copy(), C[:ncc.value].copy(), w
 
 
 def pairing(p_std, q_std):

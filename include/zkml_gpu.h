@@ -158,6 +158,33 @@ int zk_setup(zk_context* ctx, const zk_r1cs* r1cs, uint64_t toxic_seed, const ch
 int zk_prove(zk_context* ctx, const zk_pk* pk, const zk_r1cs* r1cs, const void* h_witness, size_t m,
              int num_public, uint64_t blind_seed, int check_witness, uint8_t proof_out[256], double* timings_ms);
 
+/* ---- R1CS / witness files and the synthetic R1CS (host code) ------------
+ * iden3 binary formats (circom / snarkjs): .r1cs version 1, .wtns version 2.
+ * zk_iden3_r1cs_write replaces export_r1cs_iden3 and zk_wtns_write replaces
+ * export_wtns_iden3 (src/prover/r1cs_export.cuh:41-92): same bytes for the
+ * same R1CS (public wires as nPubOut, nPubIn = 0, identity label map).
+ * Matrix values and witnesses are the reference's Montgomery Fr words; files
+ * hold standard form.  Reading: zk_iden3_r1cs_info gives the sizes (public =
+ * nPubOut + nPubIn), then zk_iden3_r1cs_read fills caller arrays of those
+ * sizes; zk_wtns_info / zk_wtns_read likewise.
+ * zk_synthetic_r1cs builds the large random R1CS of BASELINE config 5 from a
+ * seed: w[0] = 1, num_public + num_inputs uniform variables, then per row A and
+ * B with 1-3 terms over earlier variables (uniform coefficients) and C = one
+ * fresh variable set to (A.w)(B.w), so the witness satisfies every row.
+ * Capacities: A, B 3 * num_constraints entries, C num_constraints, w_mont
+ * 1 + num_public + num_inputs + num_constraints elements. */
+int zk_iden3_r1cs_info(const char* path, int* num_constraints, int* num_variables, int* num_public,
+                       int* num_private, size_t* nA, size_t* nB, size_t* nC);
+int zk_iden3_r1cs_read(const char* path, zk_sparse_entry* A, zk_sparse_entry* B, zk_sparse_entry* C);
+int zk_iden3_r1cs_write(const char* path, int num_constraints, int num_variables, int num_public, int num_private,
+                        const zk_sparse_entry* A, size_t nA, const zk_sparse_entry* B, size_t nB,
+                        const zk_sparse_entry* C, size_t nC);
+int zk_wtns_info(const char* path, size_t* m);
+int zk_wtns_read(const char* path, void* w_mont, size_t m);
+int zk_wtns_write(const char* path, const void* w_mont, size_t m);
+int zk_synthetic_r1cs(int num_constraints, int num_public, int num_inputs, uint64_t seed, zk_sparse_entry* A,
+                      size_t* nA, zk_sparse_entry* B, size_t* nB, zk_sparse_entry* C, size_t* nC, void* w_mont);
+
 /* ---- pairing and verification (host code, no device needed) -------------
  * zk_pairing replaces bn254::pairing (src/curve/pairing.cuh:198-282): the
  * reduced optimal ate pairing e(P, Q).  P: 64 bytes x, y; Q: 128 bytes x.c0,

@@ -14,6 +14,7 @@
 
 #include "curve/pairing.cuh"
 #include "prover/circuit.cuh"
+#include "prover/r1cs_export.cuh"
 #include "verifier/verifier.cuh"
 
 using namespace bn254;
@@ -145,6 +146,29 @@ int ref_verify_witness(int nc, int nv, const int32_t* rows, const int32_t* cols,
   std::vector<Fr> wv(nv);
   for (int i = 0; i < nv; i++) wv[i] = Fr(w[4 * i], w[4 * i + 1], w[4 * i + 2], w[4 * i + 3]);
   return c.verify_witness(wv) ? 1 : 0;
+}
+
+// iden3 exports with the reference's writers (src/prover/r1cs_export.cuh:41-92).
+int ref_export_r1cs(int nc, int nv, int npub, int npriv, const int32_t* rows, const int32_t* cols,
+                    const uint64_t* vals, const size_t* counts, const char* path) {
+  zkml::R1CS c;
+  c.num_constraints = nc;
+  c.num_variables = nv;
+  c.num_public_inputs = npub;
+  c.num_private_inputs = npriv;
+  size_t off = 0;
+  for (int which = 0; which < 3; which++) {
+    std::vector<zkml::SparseEntry>& v = which == 0 ? c.A : (which == 1 ? c.B : c.C);
+    for (size_t i = 0; i < counts[which]; i++, off++)
+      v.push_back({rows[off], cols[off], Fr(vals[4 * off], vals[4 * off + 1], vals[4 * off + 2], vals[4 * off + 3])});
+  }
+  return zkml::export_r1cs_iden3(c, path) ? 1 : 0;
+}
+
+int ref_export_wtns(const uint64_t* w, int m, const char* path) {
+  std::vector<Fr> wv(m);
+  for (int i = 0; i < m; i++) wv[i] = Fr(w[4 * i], w[4 * i + 1], w[4 * i + 2], w[4 * i + 3]);
+  return zkml::export_wtns_iden3(wv, path) ? 1 : 0;
 }
 
 }  // extern "C"

@@ -86,6 +86,9 @@ def ref():
         lib.ref_msm_g2_small.argtypes = [vp, vp, ctypes.c_size_t, vp]
         lib.ref_verify_files.argtypes = [ctypes.c_char_p] * 3
         lib.ref_verify_witness.argtypes = [ctypes.c_int, ctypes.c_int, vp, vp, vp, vp, vp]
+        lib.ref_export_r1cs.argtypes = [ctypes.c_int] * 4 + [vp, vp, vp, vp, ctypes.c_char_p]
+        lib.ref_export_wtns.argtypes = [vp, ctypes.c_int, ctypes.c_char_p]
+        lib.ref_pairing.argtypes = [vp, vp, vp]
         _ref = lib
     return _ref
 
