@@ -1,0 +1,72 @@
+"""GPU runs of the zkml-prove / zkml-verify command lines (cuda-zkml_amd/cli).
+
+Pins:
+  * a synthetic config-5 statement proved through zkml-prove (GPU setup +
+    prove, deterministic seeds) gives a proof that zkml-verify, the product's
+    zk_verify and the reference's own verifier (oracle/_ref) accept;
+  * the same statement exported with --export-r1cs/--export-wtns and proved
+    again from those iden3 files with --pk-load gives the same 256 bytes;
+  * the oracle's restatement of the reference prover gives the same 256 bytes
+    for the same R1CS, witness, key and seed;
+  * exit code 1 and no proof acceptance for a tampered witness.
+"""
+import os
+import subprocess
+
+import numpy as np
+import pytest
+
+import zkml_amd
+from bindings import OracleR1CS, ref, ref_available
+
+pytestmark = pytest.mark.gpu
+ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+PROVE = os.path.join(ROOT, "cuda-zkml_amd", "zkml-prove")
+VERIFY = os.path.join(ROOT, "cuda-zkml_amd", "zkml-verify")
+ENV = dict(os.environ, ZKML_DETERMINISTIC_PROVE="1")
+
+
+def run(args, **kw):
+    print("[cli]", " ".join(os.path.basename(a) if a.startswith("/") else a for a in args), flush=True)
+    return subprocess.run(args, capture_output=True, text=True, env=ENV, timeout=240, **kw)
+
+
+def test_cli_synthetic_then_files(tmp_path):
+    assert os.path.exists(PROVE) and os.path.exists(VERIFY), "run __graft_entry__.build() first"
+    t = lambda name: str(tmp_path / name)
+    r = run([PROVE, "--synthetic", "3000", "--synthetic-seed", "9", "--pk-save", t("pk.bin"), "--vk", t("vk.bin"),
+             "--output", t("p1.bin"), "--public-inputs", t("pub.bin"), "--export-r1cs", t("s.r1cs"),
+             "--export-wtns", t("s.wtns")])
+    assert r.returncode == 0, r.stdout + r.stderr
+    assert "Proving time:" in r.stdout and "VALID" in r.stdout
+    v = run([VERIFY, "--vk", t("vk.bin"), "--proof", t("p1.bin"), "--public-inputs", t("pub.bin")])
+    assert v.returncode == 0, v.stdout + v.stderr
+    if ref_available():
+        assert ref().ref_verify_files(t("vk.bin").encode(), t("p1.bin").encode(), t("pub.bin").encode()) == 1
+    # the same statement from the exported iden3 files and the saved key
+    r2 = run([PROVE, "--r1cs", t("s.r1cs"), "--wtns", t("s.wtns"), "--pk-load", t("pk.bin"), "--vk", t("vk.bin"),
+              "--output", t("p2.bin"), "--public-inputs", t("pub.json")])
+    assert r2.returncode == 0, r2.stdout + r2.stderr
+    p1 = open(t("p1.bin"), "rb").read()
+    assert open(t("p2.bin"), "rb").read() == p1
+    assert zkml_amd.verify_files(t("vk.bin"), t("p2.bin"), t("pub.json"))
+    # the oracle's prover gives the same bytes
+    nc, nv, npub, npriv, A, B, C = zkml_amd.iden3_r1cs_read(t("s.r1cs"))
+    w = zkml_amd.wtns_read(t("s.wtns"))
+    oc = OracleR1CS(nc, nv, npub, npriv, [(M["row"], M["col"], M["value"].reshape(-1, 4)) for M in (A, B, C)])
+    rc, proof_o, _ = oc.prove(t("pk.bin"), w, 0xCAFEBABE)
+    assert rc == 0 and proof_o == p1
+
+
+def test_cli_rejects_bad_witness(tmp_path):
+    t = lambda name: str(tmp_path / name)
+    A, B, C, w = zkml_amd.synthetic_r1cs(500, 2, 4, 3)
+    nv = w.shape[0]
+    zkml_amd.iden3_r1cs_write(t("s.r1cs"), 500, nv, 2, 4, A, B, C)
+    w_bad = w.copy()
+    w_bad[-1, 0] ^= 1
+    zkml_amd.wtns_write(t("bad.wtns"), w_bad)
+    r = run([PROVE, "--r1cs", t("s.r1cs"), "--wtns", t("bad.wtns"), "--pk-save", t("pk.bin"), "--vk", t("vk.bin"),
+             "--output", t("p.bin")])
+    assert r.returncode == 1
+    assert "witness" in (r.stdout + r.stderr).lower()
