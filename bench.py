@@ -3,10 +3,12 @@
 
 A step is one G1 MSM over 2^20 points (P_i = k_i G1 for
 seeded k_i, scalars uniform in [0, r)), with points and scalars resident in
-HBM.  `value` is that MSM's throughput in Mpoints/s.  The same run also times a
-full Groth16 prove on a 2^16-domain synthetic R1CS (config-5 shape) and the
-2^22 NTT of config 2, and the CPU oracle's restatement of the reference MSM on
-the host cores (cpu_baseline).  Prints one JSON line.
+HBM.  `value` is that MSM's throughput in Mpoints/s.  The same run also times
+full Groth16 proves on synthetic config-5 R1CS (the product's generator) with
+a 2^16 domain and at config 5's full 2^22 constraints (each proof checked by
+the product's verifier), the 2^22 NTT of config 2, and the CPU oracle's
+restatement of the reference MSM on the host cores (cpu_baseline).  Prints
+one JSON line.
 
     python bench.py [--gpus 1] [--steps K] [--warmup W]
 """
@@ -26,6 +28,7 @@ sys.path.insert(0, os.path.join(ROOT, "tests"))
 # gfx950, measured) = 256 CU x 64 lanes x 2.4 GHz; HBM3E 8 TB/s.
 PEAK_MAD_TOPS = 256 * 64 * 2.4e9 / 1e12
 PEAK_HBM_GBS = 8000.0
+R_ORDER = 0x30644E72E131A029B85045B68181585D2833E84879B9709143E1F593F0000001
 MADS_PER_FIELD_MUL = 136  # 8x32-bit CIOS: 2*8^2 + 8
 
 
@@ -148,30 +151,46 @@ def main():
     del da, do
 
     # ---------------- full prove at 2^16
-    prove = None
+    prove = prove22 = None
     if not args.no_prove:
-        from r1cs_gen import random_r1cs
         import tempfile
-        log("[bench] building a 2^16-domain synthetic R1CS and running GPU setup")
-        circ = random_r1cs((1 << 16) - 40, inputs=16, npub=4, seed=16, small_frac=0.7)
-        r = ctx.r1cs(circ.nc, circ.nv, circ.npub, *circ.mats())
-        w = circ.witness_words()
-        with tempfile.TemporaryDirectory() as td:
-            ctx.setup(r, 0xDEADBEEF42, os.path.join(td, "pk.bin"), os.path.join(td, "vk.bin"))
-            pk = ctx.load_pk(os.path.join(td, "pk.bin"))
-        for _ in range(2):
-            ctx.prove(pk, r, w, circ.npub, 0xCAFEBABE)
-        times = []
-        parts = None
-        for _ in range(5):
-            t0 = time.perf_counter()
-            _, t = ctx.prove(pk, r, w, circ.npub, 0xCAFEBABE)
-            times.append((time.perf_counter() - t0) * 1e3)
-            parts = t
-        prove = {"constraints": circ.nc, "variables": circ.nv, "domain": 1 << r.log_n,
-                 "ms": round(float(np.median(times)), 3),
-                 "breakdown_ms": {k_: round(v, 3) for k_, v in parts.items()}}
-        log(f"[bench] prove 2^16: {prove['ms']:.3f} ms")
+
+        def prove_case(nc, seed, reps, label):
+            """Synthetic config-5 statement (product generator), GPU setup, then
+            `reps` proves with the witness handed over from host memory."""
+            log(f"[bench] {label}: generating a {nc}-constraint synthetic R1CS and running GPU setup")
+            A, B, C, w = zkml_amd.synthetic_r1cs(nc, 4, 16, seed)
+            nv = w.shape[0]
+            r = ctx.r1cs(nc, nv, 4, A, B, C)
+            del A, B, C
+            with tempfile.TemporaryDirectory() as td:
+                t0 = time.perf_counter()
+                ctx.setup(r, 0xDEADBEEF42, os.path.join(td, "pk.bin"), os.path.join(td, "vk.bin"))
+                t_setup = time.perf_counter() - t0
+                pk = ctx.load_pk(os.path.join(td, "pk.bin"))
+                vk_bytes = open(os.path.join(td, "vk.bin"), "rb").read()
+            ctx.prove(pk, r, w, 4, 0xCAFEBABE)  # warm-up (workspaces, plans)
+            times, parts, proof = [], None, None
+            for _ in range(reps):
+                t0 = time.perf_counter()
+                proof, t = ctx.prove(pk, r, w, 4, 0xCAFEBABE)
+                times.append((time.perf_counter() - t0) * 1e3)
+                parts = t
+            pub = np.zeros((4, 4), dtype=np.uint64)
+            for i in range(4):  # w[1..4] to standard form for the verifier
+                x = sum(int(w[1 + i][k]) << (64 * k) for k in range(4)) * pow(1 << 256, -1, R_ORDER) % R_ORDER
+                pub[i] = [(x >> (64 * k)) & (2**64 - 1) for k in range(4)]
+            ok = zkml_amd.verify(vk_bytes, proof, pub)
+            out = {"constraints": nc, "variables": nv, "domain": 1 << r.log_n,
+                   "ms": round(float(np.median(times)), 3), "setup_s": round(t_setup, 2), "proof_verifies": ok,
+                   "breakdown_ms": {k_: round(v, 3) for k_, v in parts.items()}}
+            log(f"[bench] {label}: {out['ms']:.3f} ms (median of {reps}), setup {t_setup:.1f} s, verifies: {ok}")
+            pk.close()
+            r.close()
+            return out
+
+        prove = prove_case((1 << 16) - 64, 16, 5, "prove 2^16")
+        prove22 = prove_case(1 << 22, 22, 3, "prove 2^22 (config 5)")
 
     # ---------------- CPU baseline (oracle restatement of the reference MSM)
     cpu = None
@@ -212,6 +231,7 @@ def main():
         "msm_valu_frac_whole": round(msm_frac, 4),
         "kernels_ms_per_step": {k_: round(v["ms_per_step"], 4) for k_, v in kernels.items()},
         "prove_2_16": prove,
+        "prove_2_22_config5": prove22,
         "ntt_2_22": ntt,
         "cpu_baseline": cpu,
     }
