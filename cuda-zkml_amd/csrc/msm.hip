@@ -49,6 +49,7 @@ constexpr int SCAN_T = 128;        // buckets per column-scan block (<= the smal
 constexpr int MSM_NCB = 256;       // coarse bins per window of the two-pass placement
 constexpr int MSM_BPC_MAX = 128;   // buckets per coarse bin at B = 2^15
 constexpr int PLACE_T = 256;       // threads of a placement block
+constexpr uint32_t MSM_SERIAL_SPAN = 8;  // longest serial chunk-partial chain of the one-launch combine
 constexpr size_t MSM_MAX_N = (size_t)1 << 26;  // keeps W * n_pad below 2^32
 // Bits covered by the windows.  After the optional negation s <= (r-1)/2 <
 // 2^253, and signed digits need one more bit for the final carry.
@@ -556,6 +557,25 @@ __global__ __launch_bounds__(256) void k_msm_combine(ChunkSlots<F> slots, const 
   }
 }
 
+// All levels at once when no bucket spans more than MSM_SERIAL_SPAN + 1
+// chunks: the chunk where a spanning run starts adds the head partials of the
+// following chunks it covers, in order (one launch instead of ceil(log2(span))
+// tree levels plus the final store; each level costs a launch and an EC-add
+// latency).
+template <class F>
+__global__ __launch_bounds__(256) void k_msm_combine_serial(ChunkSlots<F> slots, const uint32_t* __restrict__ end,
+                                                            uint32_t nchunks, uint32_t L0,
+                                                            xyzz<F>* __restrict__ buckets) {
+  const uint32_t ch = blockIdx.x * blockDim.x + threadIdx.x;
+  if (ch >= nchunks) return;
+  const uint32_t tk = slots.tkey[ch];
+  if (tk == KEY_INVALID) return;
+  const uint32_t c1 = (end[tk] - 1) / L0;
+  xyzz<F> acc = slots.tpt[ch];
+  for (uint32_t j = ch + 1; j <= c1; j++) xyzz_add(acc, slots.hpt[j]);
+  buckets[tk] = acc;
+}
+
 template <class F>
 __global__ __launch_bounds__(256) void k_msm_finalize(ChunkSlots<F> slots, uint32_t nchunks,
                                                       xyzz<F>* __restrict__ buckets) {
@@ -871,11 +891,16 @@ static int msm_run_recs(zk_context* ctx, MsmWorkspace& ws, const uint4* recs, co
   uint32_t maxrun = 1;
   for (int w = 0; w < W; w++) maxrun = std::max(maxrun, ws.h_stat[2 * w + 1]);
   const uint32_t max_span = (maxrun + L0 - 2) / L0 + 1;  // chunks spanned by the largest bucket
-  for (uint32_t step = 1; step < max_span; step <<= 1)
-    ZK_LAUNCH(ctx, st, "msm_combine", k_msm_combine<F>, dim3(cdiv(nchunks, 256)), dim3(256), 0, slots, start, end,
-              nchunks, L0, step);
-  ZK_LAUNCH(ctx, st, "msm_combine", k_msm_finalize<F>, dim3(cdiv(nchunks, 256)), dim3(256), 0, slots, nchunks,
-            buckets);
+  if (max_span <= MSM_SERIAL_SPAN + 1) {
+    ZK_LAUNCH(ctx, st, "msm_combine", k_msm_combine_serial<F>, dim3(cdiv(nchunks, 256)), dim3(256), 0, slots, end,
+              nchunks, L0, buckets);
+  } else {
+    for (uint32_t step = 1; step < max_span; step <<= 1)
+      ZK_LAUNCH(ctx, st, "msm_combine", k_msm_combine<F>, dim3(cdiv(nchunks, 256)), dim3(256), 0, slots, start,
+                end, nchunks, L0, step);
+    ZK_LAUNCH(ctx, st, "msm_combine", k_msm_finalize<F>, dim3(cdiv(nchunks, 256)), dim3(256), 0, slots, nchunks,
+              buckets);
+  }
 
   // bucket reduction: level 1 (T threads x G buckets per group), level 2 per window
   constexpr int TMAX = sizeof(F) == sizeof(fq) ? 256 : 128;
