@@ -4,11 +4,15 @@
 A step is one G1 MSM over 2^20 points (P_i = k_i G1 for
 seeded k_i, scalars uniform in [0, r)), with points and scalars resident in
 HBM.  `value` is that MSM's throughput in Mpoints/s.  The same run also times
-full Groth16 proves on synthetic config-5 R1CS (the product's generator) with
-a 2^16 domain and at config 5's full 2^22 constraints (each proof checked by
-the product's verifier), the 2^22 NTT of config 2, and the CPU oracle's
-restatement of the reference MSM on the host cores (cpu_baseline).  Prints
-one JSON line.
+full Groth16 proves, each checked by the product's verifier:
+  prove_2_16            config 4's statement (62.7 k constraints, domain 2^16),
+                        built by the reference's own statement builder and
+                        committed under tests/golden/statements
+  prove_config1         config 1's quantized MLP statement (domain 2^13)
+  prove_2_16_synthetic  a uniform-witness config-5-shaped R1CS, domain 2^16
+  prove_2_22_config5    config 5 at its full 2^22 constraints
+the 2^22 NTT of config 2, and the CPU oracle's restatement of the reference
+MSM on the host cores (cpu_baseline).  Prints one JSON line.
 
     python bench.py [--gpus 1] [--steps K] [--warmup W]
 """
@@ -151,37 +155,37 @@ def main():
     del da, do
 
     # ---------------- full prove at 2^16
-    prove = prove22 = None
+    prove = prove_syn = prove22 = prove_c1 = None
     if not args.no_prove:
         import tempfile
+        from statements import load as load_statement
 
-        def prove_case(nc, seed, reps, label):
-            """Synthetic config-5 statement (product generator), GPU setup, then
-            `reps` proves with the witness handed over from host memory."""
-            log(f"[bench] {label}: generating a {nc}-constraint synthetic R1CS and running GPU setup")
-            A, B, C, w = zkml_amd.synthetic_r1cs(nc, 4, 16, seed)
-            nv = w.shape[0]
-            r = ctx.r1cs(nc, nv, 4, A, B, C)
-            del A, B, C
+        def prove_case(stmt, reps, label):
+            """GPU setup, then `reps` proves of a statement (nc, nv, npub, A, B, C,
+            w) with the witness handed over from host memory; the proof is
+            checked with the product's verifier."""
+            nc, nv, npub, A, B, C, w = stmt
+            log(f"[bench] {label}: {nc} constraints, GPU setup")
+            r = ctx.r1cs(nc, nv, npub, A, B, C)
             with tempfile.TemporaryDirectory() as td:
                 t0 = time.perf_counter()
                 ctx.setup(r, 0xDEADBEEF42, os.path.join(td, "pk.bin"), os.path.join(td, "vk.bin"))
                 t_setup = time.perf_counter() - t0
                 pk = ctx.load_pk(os.path.join(td, "pk.bin"))
                 vk_bytes = open(os.path.join(td, "vk.bin"), "rb").read()
-            ctx.prove(pk, r, w, 4, 0xCAFEBABE)  # warm-up (workspaces, plans)
+            ctx.prove(pk, r, w, npub, 0xCAFEBABE)  # warm-up (workspaces, plans)
             times, parts, proof = [], None, None
             for _ in range(reps):
                 t0 = time.perf_counter()
-                proof, t = ctx.prove(pk, r, w, 4, 0xCAFEBABE)
+                proof, t = ctx.prove(pk, r, w, npub, 0xCAFEBABE)
                 times.append((time.perf_counter() - t0) * 1e3)
                 parts = t
-            pub = np.zeros((4, 4), dtype=np.uint64)
-            for i in range(4):  # w[1..4] to standard form for the verifier
+            pub = np.zeros((npub, 4), dtype=np.uint64)
+            for i in range(npub):  # w[1..npub] to standard form for the verifier
                 x = sum(int(w[1 + i][k]) << (64 * k) for k in range(4)) * pow(1 << 256, -1, R_ORDER) % R_ORDER
                 pub[i] = [(x >> (64 * k)) & (2**64 - 1) for k in range(4)]
             ok = zkml_amd.verify(vk_bytes, proof, pub)
-            out = {"constraints": nc, "variables": nv, "domain": 1 << r.log_n,
+            out = {"constraints": nc, "variables": nv, "public": npub, "domain": 1 << r.log_n,
                    "ms": round(float(np.median(times)), 3), "setup_s": round(t_setup, 2), "proof_verifies": ok,
                    "breakdown_ms": {k_: round(v, 3) for k_, v in parts.items()}}
             log(f"[bench] {label}: {out['ms']:.3f} ms (median of {reps}), setup {t_setup:.1f} s, verifies: {ok}")
@@ -189,8 +193,18 @@ def main():
             r.close()
             return out
 
-        prove = prove_case((1 << 16) - 64, 16, 5, "prove 2^16")
-        prove22 = prove_case(1 << 22, 22, 3, "prove 2^22 (config 5)")
+        def synthetic(nc, seed):
+            A, B, C, w = zkml_amd.synthetic_r1cs(nc, 4, 16, seed)
+            return nc, w.shape[0], 4, A, B, C, w
+
+        def fixture(name):
+            nc, nv, npub, _npriv, A, B, C, w = load_statement(name)
+            return nc, nv, npub, A, B, C, w
+
+        prove = prove_case(fixture("config4"), 7, "prove config 4 (2^16)")
+        prove_c1 = prove_case(fixture("config1"), 7, "prove config 1 (2^13)")
+        prove_syn = prove_case(synthetic((1 << 16) - 64, 16), 5, "prove 2^16 synthetic")
+        prove22 = prove_case(synthetic(1 << 22, 22), 3, "prove 2^22 (config 5)")
 
     # ---------------- CPU baseline (oracle restatement of the reference MSM)
     cpu = None
@@ -231,6 +245,8 @@ def main():
         "msm_valu_frac_whole": round(msm_frac, 4),
         "kernels_ms_per_step": {k_: round(v["ms_per_step"], 4) for k_, v in kernels.items()},
         "prove_2_16": prove,
+        "prove_2_16_synthetic": prove_syn,
+        "prove_config1": prove_c1,
         "prove_2_22_config5": prove22,
         "ntt_2_22": ntt,
         "cpu_baseline": cpu,

@@ -10,11 +10,14 @@
 //     g2.cuh -- G2 through its affine-inversion formulas).
 #include <cstdint>
 #include <cstring>
+#include <random>
+#include <string>
 #include <vector>
 
 #include "curve/pairing.cuh"
 #include "prover/circuit.cuh"
 #include "prover/r1cs_export.cuh"
+#include "prover/statement_v2.cuh"
 #include "verifier/verifier.cuh"
 
 using namespace bn254;
@@ -146,6 +149,90 @@ int ref_verify_witness(int nc, int nv, const int32_t* rows, const int32_t* cols,
   std::vector<Fr> wv(nv);
   for (int i = 0; i < nv; i++) wv[i] = Fr(w[4 * i], w[4 * i + 1], w[4 * i + 2], w[4 * i + 3]);
   return c.verify_witness(wv) ? 1 : 0;
+}
+
+// ------------------------------------------------------------------ statements
+// BASELINE config 4's 62.7 k-constraint statement: the reference's tiny CNN
+// (tests/host/test_statement_v2.cpp:28-43) as statement variant B (:129-137):
+// private model (Poseidon commitment), private inputs, private outputs and
+// in-circuit routing, batch of two.  Writes iden3 .r1cs/.wtns with the
+// reference's exporters; info = {constraints, variables, public}.
+static zkml::NNModel tiny_cnn_model() {
+  using namespace zkml;
+  NNModel m;
+  Conv2DParams c;
+  c.in_c = 1; c.in_h = 6; c.in_w = 6; c.out_c = 2; c.kh = 3; c.kw = 3; c.stride = 1; c.pad = 1;
+  m.layers.push_back(NNModel::make_conv2d_layer(c));
+  m.layers.push_back(NNModel::make_relu_exact_layer(c.out_size(), 24, 2));
+  m.layers.push_back(NNModel::make_linear_layer(c.out_size(), 4));
+  m.layers.push_back(NNModel::make_softmax_layer(4));
+  auto& conv = m.layers[0];
+  for (size_t i = 0; i < conv.weights.size(); i++) conv.weights[i] = i64_to_fp((int64_t)((i * 5) % 7) - 3);
+  conv.bias[0] = i64_to_fp(4);
+  conv.bias[1] = i64_to_fp(-2);
+  auto& lin = m.layers[2];
+  for (size_t i = 0; i < lin.weights.size(); i++) lin.weights[i] = i64_to_fp((int64_t)((i * 3) % 9) - 4);
+  for (size_t i = 0; i < lin.bias.size(); i++) lin.bias[i] = i64_to_fp((int64_t)i - 1);
+  return m;
+}
+
+static int emit_statement(const zkml::StatementV2& st, const char* r1cs_path, const char* wtns_path, int* info) {
+  if (!st.r1cs.verify_witness(st.witness.values)) return -2;
+  if (!zkml::export_r1cs_iden3(st.r1cs, r1cs_path) || !zkml::export_wtns_iden3(st.witness.values, wtns_path))
+    return -3;
+  info[0] = st.r1cs.num_constraints;
+  info[1] = st.r1cs.num_variables;
+  info[2] = st.layout.num_public;
+  return 0;
+}
+
+int ref_statement_tiny_cnn_b(const char* r1cs_path, const char* wtns_path, int* info) {
+  using namespace zkml;
+  NNModel m = tiny_cnn_model();
+  std::vector<std::vector<Fp>> batch(2, std::vector<Fp>(36));
+  for (int i = 0; i < 36; i++) {
+    batch[0][(size_t)i] = i64_to_fp((i * 7) % 13 - 4);
+    batch[1][(size_t)i] = i64_to_fp((i * 11) % 17 - 8);
+  }
+  StatementV2Options bo;
+  bo.model_tag = Fr::from_uint(0xC0FFEE);
+  bo.private_input = true;
+  bo.input_blinding = {Fr::from_uint(0x5EED1), Fr::from_uint(0x5EED2)};
+  bo.private_model = true;
+  bo.private_outputs = true;
+  bo.route = true;
+  bo.route_threshold = 5;
+  StatementV2 sb;
+  std::string err;
+  if (!build_statement_v2(m, batch, bo, sb, err)) return -1;
+  return emit_statement(sb, r1cs_path, wtns_path, info);
+}
+
+// seeded quantized MLP n_in -> hidden -> n_out with int8
+// weights U[-127, 127], int32 biases, uint8 inputs U[0, 16] and RELU_EXACT
+// (bits, shift) between the layers; public model, inputs and outputs
+// (statement v2 defaults), `batch` samples.
+int ref_statement_mlp(uint64_t seed, int batch, int n_in, int hidden, int n_out, int bits, int shift,
+                      const char* r1cs_path, const char* wtns_path, int* info) {
+  using namespace zkml;
+  std::mt19937_64 rng(seed);
+  NNModel m;
+  m.layers.push_back(NNModel::make_linear_layer(n_in, hidden));
+  m.layers.push_back(NNModel::make_relu_exact_layer(hidden, bits, shift));
+  m.layers.push_back(NNModel::make_linear_layer(hidden, n_out));
+  m.layers.push_back(NNModel::make_softmax_layer(n_out));
+  for (size_t li : {(size_t)0, (size_t)2}) {
+    for (auto& w : m.layers[li].weights) w = i64_to_fp((int64_t)(rng() % 255) - 127);
+    for (auto& b : m.layers[li].bias) b = i64_to_fp((int64_t)(int32_t)(uint32_t)rng());
+  }
+  std::vector<std::vector<Fp>> xs((size_t)batch, std::vector<Fp>((size_t)n_in));
+  for (auto& x : xs)
+    for (auto& v : x) v = i64_to_fp((int64_t)(rng() % 17));
+  StatementV2Options opt;
+  StatementV2 st;
+  std::string err;
+  if (!build_statement_v2(m, xs, opt, st, err)) return -1;
+  return emit_statement(st, r1cs_path, wtns_path, info);
 }
 
 // iden3 exports with the reference's writers (src/prover/r1cs_export.cuh:41-92).

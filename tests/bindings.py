@@ -89,6 +89,8 @@ def ref():
         lib.ref_export_r1cs.argtypes = [ctypes.c_int] * 4 + [vp, vp, vp, vp, ctypes.c_char_p]
         lib.ref_export_wtns.argtypes = [vp, ctypes.c_int, ctypes.c_char_p]
         lib.ref_pairing.argtypes = [vp, vp, vp]
+        lib.ref_statement_tiny_cnn_b.argtypes = [ctypes.c_char_p, ctypes.c_char_p, vp]
+        lib.ref_statement_mlp.argtypes = [ctypes.c_uint64] + [ctypes.c_int] * 6 + [ctypes.c_char_p, ctypes.c_char_p, vp]
         _ref = lib
     return _ref
 
