@@ -20,6 +20,26 @@ class ZkError(RuntimeError):
     pass
 
 
+class ZkLayer(ctypes.Structure):
+    """zk_layer of include/zkml_gpu.h (reference NNModel::Layer)."""
+    _fields_ = [("type", ctypes.c_int32), ("in_size", ctypes.c_int32), ("out_size", ctypes.c_int32),
+                ("conv_in_c", ctypes.c_int32), ("conv_in_h", ctypes.c_int32), ("conv_in_w", ctypes.c_int32),
+                ("conv_out_c", ctypes.c_int32), ("conv_kh", ctypes.c_int32), ("conv_kw", ctypes.c_int32),
+                ("conv_stride", ctypes.c_int32), ("conv_pad", ctypes.c_int32),
+                ("relu_bits", ctypes.c_int32), ("relu_shift", ctypes.c_int32),
+                ("relu_c", ctypes.c_int64 * 4), ("relu_scale", ctypes.c_int64),
+                ("weights", ctypes.c_void_p), ("bias", ctypes.c_void_p)]
+
+
+class ZkStatementOptions(ctypes.Structure):
+    """zk_statement_options of include/zkml_gpu.h (reference StatementV2Options)."""
+    _fields_ = [("model_tag", ctypes.c_uint64 * 4), ("has_context", ctypes.c_int32),
+                ("context", ctypes.c_uint64 * 4), ("private_input", ctypes.c_int32),
+                ("input_blinding", ctypes.c_void_p), ("private_model", ctypes.c_int32),
+                ("private_outputs", ctypes.c_int32), ("route", ctypes.c_int32),
+                ("route_threshold", ctypes.c_int64), ("compare_bits", ctypes.c_int32)]
+
+
 def lib():
     global _lib
     if _lib is None:
@@ -80,6 +100,23 @@ def lib():
         L.zk_verify.argtypes = [vp, ctypes.c_size_t, vp, vp, ctypes.c_int, ctypes.POINTER(ctypes.c_int)]
         L.zk_verify_files.argtypes = [ctypes.c_char_p, ctypes.c_char_p, ctypes.c_char_p,
                                       ctypes.POINTER(ctypes.c_int)]
+        L.zk_poseidon_permute.argtypes = [vp]
+        L.zk_poseidon_hash2.argtypes = [vp, vp, vp]
+        L.zk_poseidon_commit.argtypes = [vp, ctypes.c_size_t, ctypes.c_uint64, vp]
+        L.zk_poseidon_constants.argtypes = [vp, vp]
+        L.zk_statement_v2_build.argtypes = [ctypes.POINTER(ZkLayer), ctypes.c_int, vp, ctypes.c_int, ctypes.c_int,
+                                            ctypes.POINTER(ZkStatementOptions), ctypes.POINTER(vp),
+                                            ctypes.c_char_p, ctypes.c_size_t]
+        L.zk_statement_destroy.argtypes = [vp]
+        L.zk_statement_destroy.restype = None
+        L.zk_statement_info.argtypes = [vp, ip, ip, ip, ip, sp, sp, sp]
+        L.zk_statement_layout.argtypes = [vp, vp]
+        L.zk_statement_r1cs.argtypes = [vp, vp, vp, vp]
+        L.zk_statement_witness.argtypes = [vp, vp]
+        L.zk_statement_scores.argtypes = [vp, vp]
+        L.zk_statement_check.argtypes = [vp]
+        L.zk_statement_write.argtypes = [vp, ctypes.c_char_p, ctypes.c_char_p]
+        L.zk_statement_meta_json.argtypes = [vp, ctypes.c_uint64, ctypes.c_char_p, ctypes.c_size_t, sp]
         _lib = L
     return _lib
 
@@ -367,6 +404,205 @@ def verify_files(vk_path, proof_path, publics_path):
     if st:
         raise ZkError(f"zk_verify_files failed ({lib().zk_status_string(st).decode()})")
     return bool(ok.value)
+
+
+R_INT = 21888242871839275222246405745257275088548364400416034343698204186575808495617
+
+
+def std_words(x):
+    """Python int -> 4 little-endian u64 words of x mod r (standard form)."""
+    x %= R_INT
+    return np.array([(x >> (64 * k)) & ((1 << 64) - 1) for k in range(4)], dtype=np.uint64)
+
+
+def words_int(w):
+    w = np.asarray(w, dtype=np.uint64).reshape(-1)
+    return sum(int(w[k]) << (64 * k) for k in range(4))
+
+
+# ---- Poseidon (host) -----------------------------------------------------------
+DOMAIN_MODEL = 0x4D4F44454C
+DOMAIN_INPUT = 0x494E505554
+
+
+def poseidon_permute(state):
+    """Poseidon t = 3 permutation of three field elements (Python ints)."""
+    s = np.concatenate([std_words(x) for x in state])
+    _status(lib().zk_poseidon_permute(_np_ptr(s)), "zk_poseidon_permute")
+    return [words_int(s[4 * i:4 * i + 4]) for i in range(3)]
+
+
+def poseidon_hash2(a, b):
+    """circomlib Poseidon([a, b])."""
+    out = np.zeros(4, dtype=np.uint64)
+    _status(lib().zk_poseidon_hash2(_np_ptr(std_words(a)), _np_ptr(std_words(b)), _np_ptr(out)),
+            "zk_poseidon_hash2")
+    return words_int(out)
+
+
+def poseidon_commit(values, domain):
+    """Rate-2 sponge commitment of the statement (capacity (len << 64) | domain)."""
+    v = np.concatenate([std_words(x) for x in values]) if len(values) else np.zeros(0, dtype=np.uint64)
+    out = np.zeros(4, dtype=np.uint64)
+    _status(lib().zk_poseidon_commit(_opt_ptr(v), len(values), domain, _np_ptr(out)), "zk_poseidon_commit")
+    return words_int(out)
+
+
+def poseidon_constants():
+    """(round constants: 195 ints, MDS: 3 x 3 ints)."""
+    rc = np.zeros(195 * 4, dtype=np.uint64)
+    mds = np.zeros(9 * 4, dtype=np.uint64)
+    _status(lib().zk_poseidon_constants(_np_ptr(rc), _np_ptr(mds)), "zk_poseidon_constants")
+    rci = [words_int(rc[4 * i:4 * i + 4]) for i in range(195)]
+    m = [words_int(mds[4 * i:4 * i + 4]) for i in range(9)]
+    return rci, [m[0:3], m[3:6], m[6:9]]
+
+
+# ---- statement producer (host) ---------------------------------------------------
+LINEAR, RELU_APPROX, SOFTMAX_APPROX, SELF_ATTENTION, RELU_EXACT, CONV2D = range(6)
+LAYOUT_KEYS = ("batch", "n_in", "n_out", "outputs_start", "model_tag_index", "context_index",
+               "model_commitment_index", "inputs_start", "input_slot_size", "route_start", "num_public")
+
+
+def layer_linear(in_size, out_size, weights, bias):
+    return {"type": LINEAR, "in_size": in_size, "out_size": out_size,
+            "weights": np.asarray(weights, dtype=np.int64).reshape(-1),
+            "bias": np.asarray(bias, dtype=np.int64).reshape(-1)}
+
+
+def layer_conv2d(in_c, in_h, in_w, out_c, kh, kw, stride, pad, weights, bias):
+    return {"type": CONV2D, "conv": (in_c, in_h, in_w, out_c, kh, kw, stride, pad),
+            "weights": np.asarray(weights, dtype=np.int64).reshape(-1),
+            "bias": np.asarray(bias, dtype=np.int64).reshape(-1)}
+
+
+def layer_relu_exact(size, bits, shift):
+    return {"type": RELU_EXACT, "in_size": size, "out_size": size, "bits": bits, "shift": shift}
+
+
+def layer_relu_approx(size, c=(64, 64, 1, 0), scale=1):
+    """Defaults are NNModel::make_relu_layer's coefficients."""
+    return {"type": RELU_APPROX, "in_size": size, "out_size": size, "c": tuple(c), "scale": scale}
+
+
+def layer_softmax(size):
+    return {"type": SOFTMAX_APPROX, "in_size": size, "out_size": size}
+
+
+class Statement:
+    """R1CS + witness of zk_statement_v2_build (reference build_statement_v2)."""
+
+    def __init__(self, h):
+        self.h = h
+        nc, nv, npub, npriv = (ctypes.c_int() for _ in range(4))
+        na, nb, ncc = (ctypes.c_size_t() for _ in range(3))
+        _status(lib().zk_statement_info(h, ctypes.byref(nc), ctypes.byref(nv), ctypes.byref(npub),
+                                        ctypes.byref(npriv), ctypes.byref(na), ctypes.byref(nb), ctypes.byref(ncc)),
+                "zk_statement_info")
+        self.nc, self.nv, self.npub, self.npriv = nc.value, nv.value, npub.value, npriv.value
+        self.A, self.B, self.C = (np.zeros(k.value, dtype=SPARSE_DTYPE) for k in (na, nb, ncc))
+        _status(lib().zk_statement_r1cs(h, _opt_ptr(self.A), _opt_ptr(self.B), _opt_ptr(self.C)),
+                "zk_statement_r1cs")
+        self.w = np.zeros((self.nv, 4), dtype=np.uint64)
+        _status(lib().zk_statement_witness(h, _np_ptr(self.w)), "zk_statement_witness")
+        lay = np.zeros(len(LAYOUT_KEYS), dtype=np.int32)
+        _status(lib().zk_statement_layout(h, _np_ptr(lay)), "zk_statement_layout")
+        self.layout = dict(zip(LAYOUT_KEYS, (int(x) for x in lay)))
+        sc = np.zeros(self.layout["batch"] * self.layout["n_out"], dtype=np.int64)
+        _status(lib().zk_statement_scores(h, _np_ptr(sc)), "zk_statement_scores")
+        self.scores = sc.reshape(self.layout["batch"], self.layout["n_out"])
+
+    def check(self):
+        """True when the witness satisfies every row (host check)."""
+        st = lib().zk_statement_check(self.h)
+        if st not in (0, 6):
+            _status(st, "zk_statement_check")
+        return st == 0
+
+    def write(self, r1cs_path=None, wtns_path=None):
+        _status(lib().zk_statement_write(self.h, r1cs_path.encode() if r1cs_path else None,
+                                         wtns_path.encode() if wtns_path else None), "zk_statement_write")
+
+    def meta_json(self, model_tag64=0):
+        n = ctypes.c_size_t()
+        _status(lib().zk_statement_meta_json(self.h, model_tag64, None, 0, ctypes.byref(n)),
+                "zk_statement_meta_json")
+        buf = ctypes.create_string_buffer(n.value + 1)
+        _status(lib().zk_statement_meta_json(self.h, model_tag64, buf, n.value + 1, ctypes.byref(n)),
+                "zk_statement_meta_json")
+        return buf.value.decode()
+
+    def publics_std(self):
+        """Public inputs w[1..npub] as (npub, 4) standard-form words."""
+        out = np.zeros((self.npub, 4), dtype=np.uint64)
+        for i in range(self.npub):
+            out[i] = std_words(words_int(self.w[1 + i]) * pow(1 << 256, -1, R_INT))
+        return out
+
+    def close(self):
+        if self.h:
+            lib().zk_statement_destroy(self.h)
+            self.h = None
+
+    def __del__(self):
+        try:
+            self.close()
+        except Exception:
+            pass
+
+
+def statement_v2(layers, inputs, model_tag=0, context=None, private_input=False, input_blinding=None,
+                 private_model=False, private_outputs=False, route_threshold=None, compare_bits=48):
+    """Build the statement for `inputs` (batch x n_in signed ints) through the
+    product's builder.  route_threshold not None enables in-circuit routing."""
+    x = np.asarray(inputs, dtype=np.int64)
+    x = np.ascontiguousarray(x.reshape(len(inputs), -1) if x.size else x.reshape(len(inputs), 0))
+    keep = [x]
+    arr = (ZkLayer * max(1, len(layers)))()
+    for i, d in enumerate(layers):
+        L = arr[i]
+        L.type = d["type"]
+        L.in_size = d.get("in_size", 0)
+        L.out_size = d.get("out_size", 0)
+        if "conv" in d:
+            (L.conv_in_c, L.conv_in_h, L.conv_in_w, L.conv_out_c, L.conv_kh, L.conv_kw, L.conv_stride,
+             L.conv_pad) = d["conv"]
+        L.relu_bits, L.relu_shift = d.get("bits", 0), d.get("shift", 0)
+        for k, c in enumerate(d.get("c", (0, 0, 0, 0))):
+            L.relu_c[k] = c
+        L.relu_scale = d.get("scale", 0)
+        for f in ("weights", "bias"):
+            if f in d:
+                a = np.ascontiguousarray(d[f], dtype=np.int64)
+                keep.append(a)
+                setattr(L, f, a.ctypes.data if a.size else None)
+    o = ZkStatementOptions()
+    for k, wd in enumerate(std_words(model_tag)):
+        o.model_tag[k] = int(wd)
+    if context is not None:
+        o.has_context = 1
+        for k, wd in enumerate(std_words(context)):
+            o.context[k] = int(wd)
+    if private_input:
+        o.private_input = 1
+        if input_blinding is not None:
+            bl = np.concatenate([std_words(v) for v in input_blinding])
+            keep.append(bl)
+            o.input_blinding = bl.ctypes.data
+    o.private_model = int(bool(private_model))
+    o.private_outputs = int(bool(private_outputs))
+    if route_threshold is not None:
+        o.route = 1
+        o.route_threshold = int(route_threshold)
+    o.compare_bits = compare_bits
+    h = vp()
+    err = ctypes.create_string_buffer(256)
+    st = lib().zk_statement_v2_build(arr, len(layers), _np_ptr(x) if x.size else None, x.shape[0],
+                                     x.shape[1] if x.ndim == 2 else 0, ctypes.byref(o), ctypes.byref(h), err, 256)
+    if st:
+        raise ZkError(f"zk_statement_v2_build failed: {err.value.decode()}")
+    del keep
+    return Statement(h)
 
 
 class R1CS:

@@ -207,6 +207,111 @@ int zk_verify(const void* vk_bytes, size_t vk_len, const void* proof256, const v
               int* valid);
 int zk_verify_files(const char* vk_path, const char* proof_path, const char* publics_path, int* valid);
 
+/* ---- Poseidon (host code) -------------------------------------------------
+ * BN254 Fr, t = 3, x^5, R_F = 8, R_P = 57: the circomlib instance of the
+ * reference (src/prover/gadgets.cuh:323-427, poseidon_constants.cuh).  Values
+ * cross as 4 x u64 standard form (inputs >= r are reduced mod r).
+ * zk_poseidon_permute replaces poseidon_permute_native (state: 3 elements, in
+ * place); zk_poseidon_hash2 replaces poseidon_hash2_native (= circomlib
+ * Poseidon([a, b])); zk_poseidon_commit replaces poseidon_commit_native (rate-2
+ * sponge, capacity (n << 64) | domain, output state[1]; domains "MODEL" =
+ * 0x4d4f44454c and "INPUT" = 0x494e505554).  zk_poseidon_constants writes the
+ * 195 round constants and the 3 x 3 MDS matrix (row major), either may be
+ * NULL. */
+int zk_poseidon_permute(uint64_t state[12]);
+int zk_poseidon_hash2(const uint64_t a[4], const uint64_t b[4], uint64_t out[4]);
+int zk_poseidon_commit(const uint64_t* values, size_t n, uint64_t domain, uint64_t out[4]);
+int zk_poseidon_constants(uint64_t* round_constants, uint64_t* mds);
+
+/* ---- statement producer (host code) ---------------------------------------
+ * zk_statement_v2_build replaces build_statement_v2
+ * (src/prover/statement_v2.cuh:82-253) with the TracedBuilder gadgets
+ * (gadgets.cuh:128-457): one R1CS + witness for `batch` samples of a quantized
+ * model, term for term the reference's (same variables, rows and term order).
+ * Layers mirror NNModel::Layer (src/nn/inference.cuh:95-147); type values are
+ * the reference's LayerType (src/nn/layers.cuh:36-43).  Model values and
+ * inputs are signed integers (v -> v mod r; |v| >= 2^62 -> 0, as the
+ * reference's Fp -> int64 conversion).  LINEAR: weights out_size x in_size row
+ * major, bias out_size.  CONV2D: CHW, weights [out_c][in_c][kh][kw], bias
+ * out_c; in_size / out_size are derived from the conv fields.  RELU_EXACT:
+ * relu_bits in [1, 252], relu_shift in [0, 62].  RELU_APPROX: y = scale (c0 +
+ * c1 x + c2 x^2 + c3 x^3).  SOFTMAX_APPROX only as the last layer (outside the
+ * statement); SELF_ATTENTION is rejected.  inputs: batch x n_in.
+ * Options mirror StatementV2Options (statement_v2.cuh:31-42); an all-zero
+ * struct (or NULL) is the reference's default, compare_bits 0 meaning 48.
+ * Field values are 4 x u64 standard form; input_blinding holds batch of them.
+ * Errors: ZK_ERR_INVALID with the reference's message in err (err_cap bytes).
+ * Results: zk_statement_info (sizes), zk_statement_r1cs (COO, Montgomery
+ * values, caller arrays of nA / nB / nC entries), zk_statement_witness
+ * (num_variables Montgomery Fr), zk_statement_layout (public-input layout,
+ * ZK_LAYOUT_* indices; -1 for absent groups), zk_statement_scores (batch x
+ * n_out final scores), zk_statement_check (R1CS::verify_witness,
+ * src/prover/circuit.cuh:92-124: ZK_OK or ZK_ERR_WITNESS),
+ * zk_statement_write (iden3 .r1cs / .wtns; either path may be NULL) and
+ * zk_statement_meta_json (statement_v2_meta_json, statement_v2.cuh:255-287;
+ * *len = length without the terminator, ZK_ERR_SIZE if cap is too small). */
+enum zk_layer_type {
+  ZK_LAYER_LINEAR = 0,
+  ZK_LAYER_RELU_APPROX = 1,
+  ZK_LAYER_SOFTMAX_APPROX = 2,
+  ZK_LAYER_SELF_ATTENTION = 3,
+  ZK_LAYER_RELU_EXACT = 4,
+  ZK_LAYER_CONV2D = 5
+};
+
+typedef struct zk_layer {
+  int32_t type;
+  int32_t in_size, out_size;
+  int32_t conv_in_c, conv_in_h, conv_in_w, conv_out_c, conv_kh, conv_kw, conv_stride, conv_pad;
+  int32_t relu_bits, relu_shift;
+  int64_t relu_c[4];
+  int64_t relu_scale;
+  const int64_t* weights;
+  const int64_t* bias;
+} zk_layer;
+
+typedef struct zk_statement_options {
+  uint64_t model_tag[4];
+  int32_t has_context;
+  uint64_t context[4];
+  int32_t private_input;
+  const uint64_t* input_blinding;
+  int32_t private_model;
+  int32_t private_outputs;
+  int32_t route;
+  int64_t route_threshold;
+  int32_t compare_bits;
+} zk_statement_options;
+
+enum zk_statement_layout_index {
+  ZK_LAYOUT_BATCH = 0,
+  ZK_LAYOUT_N_IN,
+  ZK_LAYOUT_N_OUT,
+  ZK_LAYOUT_OUTPUTS_START,
+  ZK_LAYOUT_MODEL_TAG,
+  ZK_LAYOUT_CONTEXT,
+  ZK_LAYOUT_MODEL_COMMITMENT,
+  ZK_LAYOUT_INPUTS_START,
+  ZK_LAYOUT_INPUT_SLOT,
+  ZK_LAYOUT_ROUTE_START,
+  ZK_LAYOUT_NUM_PUBLIC,
+  ZK_STATEMENT_LAYOUT_WORDS
+};
+
+typedef struct zk_statement zk_statement;
+int zk_statement_v2_build(const zk_layer* layers, int num_layers, const int64_t* inputs, int batch, int n_in,
+                          const zk_statement_options* options, zk_statement** out, char* err, size_t err_cap);
+void zk_statement_destroy(zk_statement* st);
+int zk_statement_info(const zk_statement* st, int* num_constraints, int* num_variables, int* num_public,
+                      int* num_private, size_t* nA, size_t* nB, size_t* nC);
+int zk_statement_layout(const zk_statement* st, int32_t layout[ZK_STATEMENT_LAYOUT_WORDS]);
+int zk_statement_r1cs(const zk_statement* st, zk_sparse_entry* A, zk_sparse_entry* B, zk_sparse_entry* C);
+int zk_statement_witness(const zk_statement* st, void* w_mont);
+int zk_statement_scores(const zk_statement* st, int64_t* scores);
+int zk_statement_check(const zk_statement* st);
+int zk_statement_write(const zk_statement* st, const char* r1cs_path, const char* wtns_path);
+int zk_statement_meta_json(const zk_statement* st, uint64_t model_tag64, char* buf, size_t cap, size_t* len);
+
 #ifdef __cplusplus
 }
 #endif

@@ -235,6 +235,98 @@ int ref_statement_mlp(uint64_t seed, int batch, int n_in, int hidden, int n_out,
   return emit_statement(st, r1cs_path, wtns_path, info);
 }
 
+// The reference's Poseidon table (src/prover/poseidon_constants.cuh), standard
+// form: 195 round constants, then the 3 x 3 MDS matrix row major.
+void ref_poseidon_constants(uint64_t* rc, uint64_t* mds) {
+  using namespace zkml::poseidon_bn254;
+  for (int i = 0; i < (RF + RP) * T; i++) memcpy(rc + 4 * i, ROUND_CONSTANTS[i], 32);
+  for (int i = 0; i < 3; i++)
+    for (int j = 0; j < 3; j++) memcpy(mds + 4 * (3 * i + j), MDS[i][j], 32);
+}
+
+// Any statement v2 through the reference builder, for parity sweeps.
+// layer_ints: n_layers x 13 {type, in_size, out_size, conv in_c, in_h, in_w,
+// out_c, kh, kw, stride, pad, relu bits, relu shift}; relu_params: n_layers x 5
+// {c0, c1, c2, c3, scale} (RELU_APPROX); weights / biases: per layer (LINEAR,
+// CONV2D).  opt_words: model_tag[4], context[4] standard form; opt_flags:
+// {has_context, private_input, private_model, private_outputs, route,
+// compare_bits}; blinding: batch x 4 standard form.  Writes the iden3 files
+// and the metadata JSON (or the error message) into text; info = {constraints,
+// variables, public, witness satisfies}.  Returns 0, or -1 when the builder
+// rejects the statement.
+int ref_statement_generic(int n_layers, const int32_t* layer_ints, const int64_t* relu_params,
+                          const int64_t* const* weights, const int64_t* const* biases, const int64_t* inputs,
+                          int batch, int n_in, const uint64_t* opt_words, const int32_t* opt_flags,
+                          int64_t route_threshold, const uint64_t* blinding, uint64_t tag64, const char* r1cs_path,
+                          const char* wtns_path, int* info, char* text, size_t text_cap) {
+  using namespace zkml;
+  NNModel m;
+  for (int i = 0; i < n_layers; i++) {
+    const int32_t* L = layer_ints + 13 * i;
+    const int64_t* rp = relu_params + 5 * i;
+    NNModel::Layer layer;
+    switch ((LayerType)L[0]) {
+      case LayerType::LINEAR: layer = NNModel::make_linear_layer(L[1], L[2]); break;
+      case LayerType::CONV2D: {
+        Conv2DParams c;
+        c.in_c = L[3]; c.in_h = L[4]; c.in_w = L[5]; c.out_c = L[6];
+        c.kh = L[7]; c.kw = L[8]; c.stride = L[9]; c.pad = L[10];
+        layer = NNModel::make_conv2d_layer(c);
+        break;
+      }
+      case LayerType::RELU_EXACT: layer = NNModel::make_relu_exact_layer(L[1], L[11], L[12]); break;
+      case LayerType::RELU_APPROX:
+        layer = NNModel::make_relu_layer(L[1]);
+        layer.relu_params.c0 = i64_to_fp(rp[0]);
+        layer.relu_params.c1 = i64_to_fp(rp[1]);
+        layer.relu_params.c2 = i64_to_fp(rp[2]);
+        layer.relu_params.c3 = i64_to_fp(rp[3]);
+        layer.relu_params.scale = i64_to_fp(rp[4]);
+        break;
+      case LayerType::SOFTMAX_APPROX: layer = NNModel::make_softmax_layer(L[1]); break;
+      default: layer.type = (LayerType)L[0]; layer.in_size = L[1]; layer.out_size = L[2]; break;
+    }
+    for (size_t k = 0; k < layer.weights.size(); k++) layer.weights[k] = i64_to_fp(weights[i][k]);
+    for (size_t k = 0; k < layer.bias.size(); k++) layer.bias[k] = i64_to_fp(biases[i][k]);
+    m.layers.push_back(layer);
+  }
+  std::vector<std::vector<Fp>> xs((size_t)batch, std::vector<Fp>((size_t)n_in));
+  for (int b = 0; b < batch; b++)
+    for (int i = 0; i < n_in; i++) xs[(size_t)b][(size_t)i] = i64_to_fp(inputs[(size_t)b * n_in + i]);
+  StatementV2Options o;
+  o.model_tag = fr_from_limbs(opt_words);
+  o.has_context = opt_flags[0] != 0;
+  o.context = fr_from_limbs(opt_words + 4);
+  o.private_input = opt_flags[1] != 0;
+  if (o.private_input && blinding)
+    for (int b = 0; b < batch; b++) o.input_blinding.push_back(fr_from_limbs(blinding + 4 * b));
+  o.private_model = opt_flags[2] != 0;
+  o.private_outputs = opt_flags[3] != 0;
+  o.route = opt_flags[4] != 0;
+  o.route_threshold = route_threshold;
+  o.compare_bits = opt_flags[5];
+  StatementV2 st;
+  std::string err;
+  auto put_text = [&](const std::string& s) {
+    if (text && text_cap) {
+      size_t k = s.size() < text_cap - 1 ? s.size() : text_cap - 1;
+      memcpy(text, s.data(), k);
+      text[k] = 0;
+    }
+  };
+  if (!build_statement_v2(m, xs, o, st, err)) {
+    put_text(err);
+    return -1;
+  }
+  info[0] = st.r1cs.num_constraints;
+  info[1] = st.r1cs.num_variables;
+  info[2] = st.layout.num_public;
+  info[3] = st.r1cs.verify_witness(st.witness.values) ? 1 : 0;
+  if (!export_r1cs_iden3(st.r1cs, r1cs_path) || !export_wtns_iden3(st.witness.values, wtns_path)) return -3;
+  put_text(statement_v2_meta_json(st, o, tag64));
+  return 0;
+}
+
 // iden3 exports with the reference's writers (src/prover/r1cs_export.cuh:41-92).
 int ref_export_r1cs(int nc, int nv, int npub, int npriv, const int32_t* rows, const int32_t* cols,
                     const uint64_t* vals, const size_t* counts, const char* path) {

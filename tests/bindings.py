@@ -91,6 +91,11 @@ def ref():
         lib.ref_pairing.argtypes = [vp, vp, vp]
         lib.ref_statement_tiny_cnn_b.argtypes = [ctypes.c_char_p, ctypes.c_char_p, vp]
         lib.ref_statement_mlp.argtypes = [ctypes.c_uint64] + [ctypes.c_int] * 6 + [ctypes.c_char_p, ctypes.c_char_p, vp]
+        lib.ref_poseidon_constants.argtypes = [vp, vp]
+        lib.ref_poseidon_constants.restype = None
+        lib.ref_statement_generic.argtypes = [ctypes.c_int, vp, vp, vp, vp, vp, ctypes.c_int, ctypes.c_int, vp, vp,
+                                              ctypes.c_int64, vp, ctypes.c_uint64, ctypes.c_char_p, ctypes.c_char_p,
+                                              vp, ctypes.c_char_p, ctypes.c_size_t]
         _ref = lib
     return _ref
 

@@ -70,3 +70,37 @@ def test_cli_rejects_bad_witness(tmp_path):
              "--output", t("p.bin")])
     assert r.returncode == 1
     assert "witness" in (r.stdout + r.stderr).lower()
+
+
+def test_cli_statement_v2_end_to_end(tmp_path):
+    """zkml-prove --statement-v2 on the config-4-shaped CNN with a context and
+    routing: proof verifies (zkml-verify, reference verifier), the public
+    inputs carry the scores / tag / context, the metadata JSON equals the
+    reference front end's, and a changed context is rejected."""
+    import json
+    from cli_models import digits_cnn, ref_cli_available, ref_statement, write_model, write_sample
+    t = lambda name: str(tmp_path / name)
+    layers, params = digits_cnn()
+    arch, model = write_model(str(tmp_path), layers, params)
+    x = write_sample(t("x.npy"), np.random.default_rng(7).integers(0, 17, 64))
+    r = run([PROVE, "--statement-v2", "--integer-model", "--integer-input", "--model", model, "--arch", arch,
+             "--input", x, "--context", "0x1234abcd", "--route-threshold", "3", "--output", t("proof.bin"),
+             "--vk", t("vk.bin"), "--public-inputs", t("public.json"), "--statement-meta", t("meta.json")])
+    assert r.returncode == 0, r.stdout + r.stderr
+    assert "Proving time:" in r.stdout and "Statement mode: PCANI v2" in r.stdout
+    v = run([VERIFY, "--vk", t("vk.bin"), "--proof", t("proof.bin"), "--public-inputs", t("public.json")])
+    assert v.returncode == 0, v.stdout + v.stderr
+    meta = json.load(open(t("meta.json")))
+    pub = json.load(open(t("public.json")))
+    assert len(pub) == meta["num_public"]
+    assert pub[meta["context_public_index"]] == 0x1234abcd
+    assert pub[meta["model_tag_public_index"]] == int(meta["model_tag64"], 16)
+    if ref_cli_available():
+        rc, info, tag, ref_meta = ref_statement(arch, model, [x], t("ref.r1cs"), t("ref.wtns"), context="0x1234abcd",
+                                                route_threshold=3)
+        assert rc == 0 and open(t("meta.json")).read() == ref_meta
+    bad = list(pub)
+    bad[meta["context_public_index"]] += 1
+    json.dump(bad, open(t("bad.json"), "w"))
+    v2 = run([VERIFY, "--vk", t("vk.bin"), "--proof", t("proof.bin"), "--public-inputs", t("bad.json")])
+    assert v2.returncode == 1
