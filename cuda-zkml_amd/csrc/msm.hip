@@ -50,7 +50,6 @@ constexpr int MSM_NCB = 256;       // coarse bins per window of the two-pass pla
 constexpr int MSM_BPC_MAX = 128;   // buckets per coarse bin at B = 2^15
 constexpr int PLACE_T = 256;       // threads of a placement block
 constexpr uint32_t MSM_SERIAL_SPAN = 8;  // longest serial chunk-partial chain of the one-launch combine
-constexpr size_t MSM_MAX_N = (size_t)1 << 26;  // keeps W * n_pad below 2^32
 // Bits covered by the windows.  After the optional negation s <= (r-1)/2 <
 // 2^253, and signed digits need one more bit for the final carry.
 constexpr int MSM_BITS = 254;

@@ -117,6 +117,7 @@ int quotient_pointwise(zk_context* ctx, void* d_h, const void* d_a, const void* 
                        const uint64_t zinv_mont[4], hipStream_t st);
 
 // ---- MSM (msm.hip); results are canonical affine in the zk_g*_affine layout
+constexpr size_t MSM_MAX_N = (size_t)1 << 26;  // largest MSM; keeps W * n_pad below 2^32
 int msm_g1_run(zk_context* ctx, const void* d_points, const void* d_scalars, size_t n, uint64_t out_affine[8],
                hipStream_t st);
 int msm_g2_run(zk_context* ctx, const void* d_points, const void* d_scalars, size_t n, uint64_t out_affine[16],

@@ -100,6 +100,8 @@ def lib():
         L.zk_verify.argtypes = [vp, ctypes.c_size_t, vp, vp, ctypes.c_int, ctypes.POINTER(ctypes.c_int)]
         L.zk_verify_files.argtypes = [ctypes.c_char_p, ctypes.c_char_p, ctypes.c_char_p,
                                       ctypes.POINTER(ctypes.c_int)]
+        L.zk_kzg_commit.argtypes = [vp, vp, vp, ctypes.c_size_t, vp, vp]
+        L.zk_kzg_open.argtypes = [vp, vp, vp, ctypes.c_size_t, vp, vp, vp, vp]
         L.zk_poseidon_permute.argtypes = [vp]
         L.zk_poseidon_hash2.argtypes = [vp, vp, vp]
         L.zk_poseidon_commit.argtypes = [vp, ctypes.c_size_t, ctypes.c_uint64, vp]
@@ -265,6 +267,22 @@ class Context:
         out = np.zeros(16, dtype=np.uint64)
         self._check(lib().zk_msm_g2(self.h, vp(d_points.ptr), vp(d_scalars.ptr), n, _np_ptr(out), None), "zk_msm_g2")
         return out
+
+    def kzg_commit(self, d_srs, d_coeffs, degree):
+        """sum f_i [tau^i]_1 as (8,) u64 affine (Montgomery words)."""
+        out = np.zeros(8, dtype=np.uint64)
+        self._check(lib().zk_kzg_commit(self.h, vp(d_srs.ptr), vp(d_coeffs.ptr), degree, _np_ptr(out), None),
+                    "zk_kzg_commit")
+        return out
+
+    def kzg_open(self, d_srs, d_coeffs, degree, z_mont):
+        """(opening proof (8,) u64 affine, f(z) (4,) u64 Montgomery)."""
+        out = np.zeros(8, dtype=np.uint64)
+        fz = np.zeros(4, dtype=np.uint64)
+        z = np.ascontiguousarray(z_mont, dtype=np.uint64).reshape(4)
+        self._check(lib().zk_kzg_open(self.h, vp(d_srs.ptr), vp(d_coeffs.ptr), degree, _np_ptr(z), _np_ptr(out),
+                                      _np_ptr(fz), None), "zk_kzg_open")
+        return out, fz
 
     @staticmethod
     def msm_config(n, g2=False):

@@ -108,6 +108,20 @@ int zk_msm_g2(zk_context* ctx, const void* d_points, const void* d_scalars, size
  * widest window) and the number of signed-digit windows.  CPU only. */
 int zk_msm_config(size_t n, int g2, int* window_bits, int* windows);
 
+/* KZG commitment over G1 (replaces KZGCommitment::commit / ::open,
+ * src/prover/groth16.cuh:197-207, groth16.cu:393-438).  d_srs_g1: device
+ * zk_g1_affine [tau^i]_1, i < degree; d_coeffs: device Fr (Montgomery), f_i
+ * ascending, `degree` coefficients.  zk_kzg_commit writes sum f_i [tau^i]_1
+ * (affine, as zk_msm_g1).  zk_kzg_open writes the opening proof
+ * sum q_i [tau^i]_1 with q = (f - f(z)) / (x - z) (synthetic division on the
+ * GPU; degree <= 1 gives infinity, as the reference) and, when f_z is not
+ * NULL, f(z) (Montgomery Fr).  z: Montgomery Fr.  The verifier equation is
+ * e(C - f(z) G1, G2) = e(proof, [tau]_2 - z G2). */
+int zk_kzg_commit(zk_context* ctx, const void* d_srs_g1, const void* d_coeffs, size_t degree, void* h_commitment,
+                  void* stream);
+int zk_kzg_open(zk_context* ctx, const void* d_srs_g1, const void* d_coeffs, size_t degree, const uint64_t z[4],
+                void* h_proof, uint64_t f_z[4], void* stream);
+
 /* Host-pointer drop-ins with the reference's exact signature semantics:
  * h_points are reference G1Affine / G2Affine structs (72 / 136 bytes),
  * h_scalars are Fr, h_result receives a reference G1Jacobian / G2Jacobian
