@@ -9,6 +9,7 @@
 
 #include <algorithm>
 #include <condition_variable>
+#include <functional>
 #include <mutex>
 #include <random>
 #include <thread>
@@ -558,10 +559,15 @@ int zk_prove(zk_context* ctx, const zk_pk* pk, const zk_r1cs* c, const void* h_w
   const size_t n = c->n;
   ZK_TRY(ctx->ensure(ctx->scratch_b, n * 32 * 3));
   ZK_TRY(ctx->ensure(ctx->scratch_c, n * 32 + m * 32 + 64));
-  for (int j = 0; j < ZK_JOBS; j++) {
+  // Streams: the context stream (witness upload, quotient, then the H MSM),
+  // one for the G2 MSM and one for the G1 MSMs over the witness (A, B1 and
+  // L as one multi-set MSM).  A process gets 4 hardware queues; streams
+  // beyond that share a queue and their kernels then run strictly in order.
+  constexpr int JOB_STREAMS = 2, S_G2 = 0, S_G1 = 1;
+  for (int j = 0; j < JOB_STREAMS; j++)
     if (!ctx->job_stream[j]) ZK_HIP(ctx, hipStreamCreateWithFlags(&ctx->job_stream[j], hipStreamNonBlocking));
+  for (int j = 0; j < ZK_JOBS; j++)
     if (!ctx->job_ws[j]) ctx->job_ws[j] = msm_workspace_new();
-  }
   uint8_t* base = (uint8_t*)ctx->scratch_c.p;
   void* d_h = base;
   void* d_w = base + n * 32;
@@ -573,7 +579,6 @@ int zk_prove(zk_context* ctx, const zk_pk* pk, const zk_r1cs* c, const void* h_w
   std::mt19937_64 rng(blind_seed);
   Fr r = random_nonzero(rng);
   Fr s = random_nonzero(rng);
-  const uint8_t* w8 = (const uint8_t*)d_w;
   uint64_t a_msm[8], b2_msm[16], l_msm[8], h_msm[8], b1_msm[8];
   memset(l_msm, 0, sizeof(l_msm));
   const size_t na = std::min(m, pk->nA);
@@ -581,23 +586,14 @@ int zk_prove(zk_context* ctx, const zk_pk* pk, const zk_r1cs* c, const void* h_w
   const long npriv_l = std::min<long>((long)pk->nL, (long)m - 1 - pk->npub);
   const size_t nh = std::min(n, pk->nH);
   const size_t nb1 = std::min(m, pk->nB1);
-  // The five MSMs are independent (groth16.cu:776-827): each runs on its own
-  // stream with its own workspace from its own host thread, so that their
-  // latency-bound phases overlap.  A, B2, L and B1 need only the witness; H
-  // waits for the quotient computed meanwhile on the context stream.
-  struct Job {
-    bool g2;
-    const void* recs;
-    const void* scalars;
-    size_t n;
-    uint64_t* out;
-    int rc;
-  } jobs[ZK_JOBS] = {{false, pk->A, d_w, na, a_msm, ZK_OK},
-                     {true, pk->B2, d_w, nb2, b2_msm, ZK_OK},
-                     {false, pk->L, w8 + 32 * (1 + pk->npub), npriv_l > 0 ? (size_t)npriv_l : 0, l_msm, ZK_OK},
-                     {false, pk->H, d_h, nh, h_msm, ZK_OK},
-                     {false, pk->B1, d_w, nb1, b1_msm, ZK_OK}};
-  constexpr int JOB_B2 = 1, JOB_H = 3;
+  // The five MSMs are independent (groth16.cu:776-827).  A, B1 and L multiply
+  // slices of the witness, so they run as one three-set MSM sharing the digit
+  // sort and the latency-bound combine and reduction; B2 (G2) runs beside it;
+  // H follows the quotient on the context stream.  Each is driven from its
+  // own host thread (the MSM reads bucket statistics back mid-way).
+  // Job slots (timings): 0 A, 1 B2, 2 L, 3 H, 4 B1; A, L and B1 share one run.
+  constexpr int JOB_G1 = 0, JOB_B2 = 1, JOB_H = 3;
+  int rc_g1 = ZK_OK, rc_b2 = ZK_OK, rc_h = ZK_OK;
   // The G2 MSM is the longest: its accumulation runs first on its own and the
   // G1 MSMs start once it is enqueued (their streams wait for it), so that they
   // fill the GPU during the G2 MSM's latency-bound combine and reduction.
@@ -614,41 +610,60 @@ int zk_prove(zk_context* ctx, const zk_pk* pk, const zk_r1cs* c, const void* h_w
       }
       cv.notify_all();
     }
+    bool wait_on(hipStream_t s, hipEvent_t e) {
+      std::unique_lock<std::mutex> lk(m);
+      cv.wait(lk, [&] { return open; });
+      return !recorded || hipStreamWaitEvent(s, e, 0) == hipSuccess;
+    }
   } gate;
   MsmHook hook;
   hook.ev = ev[NEV - 1];
   hook.fn = [](void* a) { ((Gate*)a)->release(true); };
   hook.arg = &gate;
-  auto run_job = [&](int j) {
-    Job& jb = jobs[j];
-    hipStream_t js = ctx->job_stream[j];
-    if (j != JOB_B2) {
-      std::unique_lock<std::mutex> lk(gate.m);
-      gate.cv.wait(lk, [&] { return gate.open; });
-      if (gate.recorded && hipStreamWaitEvent(js, hook.ev, 0) != hipSuccess) {
-        jb.rc = ctx->fail(ZK_ERR_HIP, "prove: stream wait");
-        return;
-      }
-    }
-    if (hipEventRecord(ev[4 + 2 * j], js) != hipSuccess) {
-      jb.rc = ctx->fail(ZK_ERR_HIP, "prove: event record");
-    } else {
-      jb.rc = jb.n ? msm_recs_ws(ctx, ctx->job_ws[j], jb.g2, jb.recs, jb.scalars, jb.n, jb.out, js,
-                                 j == JOB_B2 ? &hook : nullptr)
-                   : ZK_OK;
-      if (hipEventRecord(ev[5 + 2 * j], js) != hipSuccess && jb.rc == ZK_OK)
-        jb.rc = ctx->fail(ZK_ERR_HIP, "prove: event record");
-    }
-    if (j == JOB_B2) gate.release(false);  // no-op when the hook already ran
+  auto record = [&](int slot, hipStream_t s, int& rc) {
+    if (hipEventRecord(ev[slot], s) != hipSuccess && rc == ZK_OK) rc = ctx->fail(ZK_ERR_HIP, "prove: event record");
   };
-  for (int j = 0; j < ZK_JOBS; j++)
-    if (j != JOB_H) ZK_HIP(ctx, hipStreamWaitEvent(ctx->job_stream[j], ev[1], 0));
+  auto run_b2 = [&] {
+    hipStream_t js = ctx->job_stream[S_G2];
+    record(4 + 2 * JOB_B2, js, rc_b2);
+    if (rc_b2 == ZK_OK && nb2)
+      rc_b2 = msm_recs_ws(ctx, ctx->job_ws[JOB_B2], true, pk->B2, d_w, nb2, b2_msm, js, &hook);
+    record(5 + 2 * JOB_B2, js, rc_b2);
+    gate.release(false);  // no-op when the hook already ran
+  };
+  auto run_g1 = [&] {
+    hipStream_t js = ctx->job_stream[S_G1];
+    if (!gate.wait_on(js, hook.ev)) {
+      rc_g1 = ctx->fail(ZK_ERR_HIP, "prove: stream wait");
+      return;
+    }
+    record(4 + 2 * JOB_G1, js, rc_g1);
+    const void* recs[3];
+    size_t lo[3], cnt[3];
+    uint64_t* outs[3];
+    int ns = 0;
+    auto add = [&](const void* r, size_t l, size_t k, uint64_t* o) {
+      if (k == 0) return;  // empty set: the result stays the identity
+      recs[ns] = r;
+      lo[ns] = l;
+      cnt[ns] = k;
+      outs[ns++] = o;
+    };
+    memset(a_msm, 0, sizeof(a_msm));
+    memset(b1_msm, 0, sizeof(b1_msm));
+    add(pk->A, 0, na, a_msm);
+    add(pk->B1, 0, nb1, b1_msm);
+    add(pk->L, 1 + (size_t)pk->npub, npriv_l > 0 ? (size_t)npriv_l : 0, l_msm);
+    if (rc_g1 == ZK_OK && ns) rc_g1 = msm_g1_sets_ws(ctx, ctx->job_ws[JOB_G1], ns, recs, lo, cnt, d_w, m, outs, js);
+    record(5 + 2 * JOB_G1, js, rc_g1);
+  };
+  for (int j = 0; j < JOB_STREAMS; j++) ZK_HIP(ctx, hipStreamWaitEvent(ctx->job_stream[j], ev[1], 0));
   std::vector<std::thread> workers;
-  for (int j : {JOB_B2, 0, 2, 4}) {  // the G2 job first: the others wait for it
+  for (const std::function<void()>& fn : {std::function<void()>(run_b2), std::function<void()>(run_g1)}) {
     try {
-      workers.emplace_back(run_job, j);
+      workers.emplace_back(fn);  // the G2 job first: the G1 job waits for it
     } catch (...) {
-      run_job(j);  // no thread available: run it here
+      fn();  // no thread available: run it here
     }
   }
   int qrc = quotient_run(ctx, c, d_w, d_h, ctx->scratch_b.p, st, check_witness != 0, d_bad);
@@ -658,16 +673,22 @@ int zk_prove(zk_context* ctx, const zk_pk* pk, const zk_r1cs* c, const void* h_w
       qrc = ctx->fail(ZK_ERR_HIP, "prove: witness check read-back");
   }
   if (qrc == ZK_OK && hipEventRecord(ev[2], st) != hipSuccess) qrc = ctx->fail(ZK_ERR_HIP, "prove: event record");
-  if (qrc == ZK_OK && hipStreamWaitEvent(ctx->job_stream[JOB_H], ev[2], 0) != hipSuccess)
-    qrc = ctx->fail(ZK_ERR_HIP, "prove: stream wait");
-  if (qrc == ZK_OK) run_job(JOB_H);
+  if (qrc == ZK_OK) {  // H after the quotient, same stream
+    if (!gate.wait_on(st, hook.ev)) rc_h = ctx->fail(ZK_ERR_HIP, "prove: stream wait");
+    record(4 + 2 * JOB_H, st, rc_h);
+    if (rc_h == ZK_OK && nh) rc_h = msm_recs_ws(ctx, ctx->job_ws[JOB_H], false, pk->H, d_h, nh, h_msm, st);
+    else if (!nh) memset(h_msm, 0, sizeof(h_msm));
+    record(5 + 2 * JOB_H, st, rc_h);
+  }
   for (auto& t : workers) t.join();
   ZK_TRY(qrc);
   if (check_witness) {
     ZK_HIP(ctx, hipStreamSynchronize(st));
     if (bad) return ctx->fail(ZK_ERR_WITNESS, "witness does not satisfy the R1CS");
   }
-  for (const Job& jb : jobs) ZK_TRY(jb.rc);
+  ZK_TRY(rc_b2);
+  ZK_TRY(rc_g1);
+  ZK_TRY(rc_h);
   // host assembly (groth16.cu:769-840): C = L + H + s A + r (beta1 + B1)
   G1 A = g1_from_words(pk->alpha1).add(na > 0 ? g1_from_words(a_msm) : G1::inf());
   A = A.add(g1_from_words(pk->delta1).mul(r));
@@ -706,14 +727,15 @@ int zk_prove(zk_context* ctx, const zk_pk* pk, const zk_r1cs* c, const void* h_w
     timings[0] = t;  // total
     (void)hipEventElapsedTime(&t, ev[0], ev[2]);
     timings[1] = t;  // witness upload + quotient (+ check)
-    // each MSM from its start to its result on the host (they overlap)
-    for (int j = 0; j < ZK_JOBS; j++) {
-      (void)hipEventElapsedTime(&t, ev[4 + 2 * j], ev[5 + 2 * j]);
-      timings[2 + j] = t;  // A, B (G2), L, H, B1
-    }
+    // each MSM from its start to its result on the host (they overlap); A,
+    // L and B1 are one run and report its time
+    const int slot_of[ZK_JOBS] = {0, 1, 0, 3, 0};  // A, B (G2), L, H, B1
     float last = 0;
     for (int j = 0; j < ZK_JOBS; j++) {
-      (void)hipEventElapsedTime(&t, ev[0], ev[5 + 2 * j]);
+      const int e = slot_of[j];
+      (void)hipEventElapsedTime(&t, ev[4 + 2 * e], ev[5 + 2 * e]);
+      timings[2 + j] = t;
+      (void)hipEventElapsedTime(&t, ev[0], ev[5 + 2 * e]);
       last = std::max(last, t);
     }
     (void)hipEventElapsedTime(&t, ev[0], ev[3]);

@@ -463,26 +463,58 @@ __global__ __launch_bounds__(PLACE_T) void k_msm_place(const uint2* __restrict__
 }
 
 // ------------------------------------------------------------------ accumulate
+// Issue priority of the MSM's waves.  Inside a proof the G2 MSM is the
+// critical path while four G1 MSMs run beside it on other streams; raising
+// its waves' priority lets the SIMD arbiter serve its latency-bound chains
+// (combine, bucket reduction) first and hand the remaining issue slots to the
+// G1 work, instead of splitting them evenly.
+template <class F>
+__device__ __forceinline__ void msm_priority() {
+  if constexpr (sizeof(F) == sizeof(fq2)) __builtin_amdgcn_s_setprio(2);
+}
+
+// Chunk partials of buckets that span chunks; base set s uses the slots
+// [s * nchunks, (s + 1) * nchunks).
 template <class F>
 struct ChunkSlots {
   uint32_t* hkey;
   uint32_t* tkey;
   xyzz<F>* hpt;
   xyzz<F>* tpt;
+  __device__ ChunkSlots at(uint32_t set, uint32_t nchunks) const {
+    const size_t o = (size_t)set * nchunks;
+    return ChunkSlots{hkey + o, tkey + o, hpt + o, tpt + o};
+  }
+};
+
+// Point sets sharing one scalar vector (and so one sorted digit list): set s
+// takes the scalars with index i in [lo[s], hi[s]) and the point recs[s][i -
+// lo[s]]; entries outside the range add nothing to that set's buckets.
+constexpr int MSM_SETS = 3;
+struct BaseSets {
+  const uint4* recs[MSM_SETS];
+  uint32_t lo[MSM_SETS], hi[MSM_SETS];
 };
 
 // Chunk ch covers sorted positions [ch*L0, ch*L0 + L0) of window
 // ch / chunks_per_window; positions past the window's entry count are empty.
+// blockIdx.y selects the base set; its buckets start at set * nbuckets.
 template <class F>
-__global__ __launch_bounds__(256) void k_msm_accumulate(const uint2* __restrict__ sorted,
-                                                        const uint4* __restrict__ recs,
+__global__ __launch_bounds__(256) void k_msm_accumulate(const uint2* __restrict__ sorted, BaseSets sets,
                                                         const uint32_t* __restrict__ start,
                                                         const uint32_t* __restrict__ end,
                                                         const uint32_t* __restrict__ wstat, uint32_t nchunks,
                                                         uint32_t chunks_per_window, uint32_t n_pad, uint32_t L0,
-                                                        xyzz<F>* __restrict__ buckets, ChunkSlots<F> slots) {
+                                                        size_t nbuckets, xyzz<F>* __restrict__ buckets,
+                                                        ChunkSlots<F> all_slots) {
+  msm_priority<F>();
   const uint32_t ch = blockIdx.x * blockDim.x + threadIdx.x;
   if (ch >= nchunks) return;
+  const uint32_t set = blockIdx.y;
+  const uint4* __restrict__ recs = sets.recs[set];
+  const uint32_t ilo = sets.lo[set], ilen = sets.hi[set] - ilo;
+  buckets += set * nbuckets;
+  const ChunkSlots<F> slots = all_slots.at(set, nchunks);
   const uint32_t w = ch / chunks_per_window;
   const uint32_t total = w * n_pad + wstat[2 * w];
   const uint32_t lo = ch * L0;
@@ -509,8 +541,9 @@ __global__ __launch_bounds__(256) void k_msm_accumulate(const uint2* __restrict_
         empty = true;
       }
       const uint32_t v = e.y;
+      const uint32_t i = (v & 0x7fffffffu) - ilo;  // wraps below lo
       F x, y;
-      if (!load_rec(recs, v & 0x7fffffffu, x, y)) {
+      if (i < ilen && !load_rec(recs, i, x, y)) {
         if (v >> 31) y = fneg(y);
         if (empty) {
           xyzz_set_affine(acc, x, y);
@@ -538,11 +571,13 @@ __global__ __launch_bounds__(256) void k_msm_accumulate(const uint2* __restrict_
 
 // One level of the tree over the chunk partials of buckets spanning chunks.
 template <class F>
-__global__ __launch_bounds__(256) void k_msm_combine(ChunkSlots<F> slots, const uint32_t* __restrict__ start,
+__global__ __launch_bounds__(256) void k_msm_combine(ChunkSlots<F> all_slots, const uint32_t* __restrict__ start,
                                                      const uint32_t* __restrict__ end, uint32_t nchunks,
                                                      uint32_t L0, uint32_t step) {
+  msm_priority<F>();
   const uint32_t ch = blockIdx.x * blockDim.x + threadIdx.x;
   if (ch >= nchunks) return;
+  const ChunkSlots<F> slots = all_slots.at(blockIdx.y, nchunks);
   const uint32_t tk = slots.tkey[ch];
   if (tk != KEY_INVALID) {
     const uint32_t c1 = (end[tk] - 1) / L0;
@@ -562,11 +597,15 @@ __global__ __launch_bounds__(256) void k_msm_combine(ChunkSlots<F> slots, const 
 // tree levels plus the final store; each level costs a launch and an EC-add
 // latency).
 template <class F>
-__global__ __launch_bounds__(256) void k_msm_combine_serial(ChunkSlots<F> slots, const uint32_t* __restrict__ end,
-                                                            uint32_t nchunks, uint32_t L0,
+__global__ __launch_bounds__(256) void k_msm_combine_serial(ChunkSlots<F> all_slots,
+                                                            const uint32_t* __restrict__ end, uint32_t nchunks,
+                                                            uint32_t L0, size_t nbuckets,
                                                             xyzz<F>* __restrict__ buckets) {
+  msm_priority<F>();
   const uint32_t ch = blockIdx.x * blockDim.x + threadIdx.x;
   if (ch >= nchunks) return;
+  const ChunkSlots<F> slots = all_slots.at(blockIdx.y, nchunks);
+  buckets += blockIdx.y * nbuckets;
   const uint32_t tk = slots.tkey[ch];
   if (tk == KEY_INVALID) return;
   const uint32_t c1 = (end[tk] - 1) / L0;
@@ -576,10 +615,13 @@ __global__ __launch_bounds__(256) void k_msm_combine_serial(ChunkSlots<F> slots,
 }
 
 template <class F>
-__global__ __launch_bounds__(256) void k_msm_finalize(ChunkSlots<F> slots, uint32_t nchunks,
+__global__ __launch_bounds__(256) void k_msm_finalize(ChunkSlots<F> all_slots, uint32_t nchunks, size_t nbuckets,
                                                       xyzz<F>* __restrict__ buckets) {
+  msm_priority<F>();
   const uint32_t ch = blockIdx.x * blockDim.x + threadIdx.x;
   if (ch >= nchunks) return;
+  const ChunkSlots<F> slots = all_slots.at(blockIdx.y, nchunks);
+  buckets += blockIdx.y * nbuckets;
   const uint32_t tk = slots.tkey[ch];
   if (tk != KEY_INVALID) buckets[tk] = slots.tpt[ch];
 }
@@ -636,23 +678,27 @@ __device__ __forceinline__ xyzz<F> wg_sum(xyzz<F> v, xyzz<F>* sh, int T) {
 }
 
 // Level 1: block k of window w (blockIdx.x = w*K + k), T = blockDim.x threads
-// of G buckets each (G = 2^log2g).
+// of G buckets each (G = 2^log2g).  Windows of several base sets follow each
+// other (W_set windows per set); the sorted-list bounds start/end are those
+// of the window within its set.
 template <class F, int TMAX>
 __global__ __launch_bounds__(TMAX) void k_msm_reduce1(const xyzz<F>* __restrict__ buckets,
                                                       const uint32_t* __restrict__ start,
                                                       const uint32_t* __restrict__ end, uint32_t B1, uint32_t K,
-                                                      int log2g, xyzz<F>* __restrict__ P, xyzz<F>* __restrict__ RUN) {
+                                                      uint32_t W_set, int log2g, xyzz<F>* __restrict__ P,
+                                                      xyzz<F>* __restrict__ RUN) {
+  msm_priority<F>();
   __shared__ xyzz<F> sh[TMAX];
   const int T = blockDim.x, G = 1 << log2g;
   const uint32_t w = blockIdx.x / K, k = blockIdx.x % K;
   const uint32_t t = threadIdx.x;
-  const uint32_t kb = w * B1 + (k * T + t) * G;  // key of this thread's first bucket
+  const uint32_t kb = w * B1 + (k * T + t) * G;                // bucket of this thread's first entry
+  const uint32_t sb = (w % W_set) * B1 + (k * T + t) * G;      // its key in the sorted list
   xyzz<F> run, acc;
   xyzz_set_inf(run);
   xyzz_set_inf(acc);
   for (int i = G - 1; i >= 0; i--) {
-    const uint32_t key = kb + i;
-    if (end[key] > start[key]) xyzz_add(run, buckets[key]);
+    if (end[sb + i] > start[sb + i]) xyzz_add(run, buckets[kb + i]);
     xyzz_add(acc, run);
   }
   xyzz<F> sr = wg_suffix_scan<F>(run, sh, T);
@@ -671,6 +717,7 @@ __global__ __launch_bounds__(TMAX) void k_msm_reduce1(const xyzz<F>* __restrict_
 template <class F, int KMAX>
 __global__ __launch_bounds__(KMAX) void k_msm_reduce2(const xyzz<F>* __restrict__ P, const xyzz<F>* __restrict__ RUN,
                                                       uint32_t K, int log2tg, xyzz<F>* __restrict__ out) {
+  msm_priority<F>();
   __shared__ xyzz<F> sh[KMAX];
   const uint32_t w = blockIdx.x, t = threadIdx.x;
   xyzz<F> run, acc;
@@ -795,13 +842,18 @@ static void host_finish(const std::vector<xyzz<F>>& parts, int W, int per_w, uin
   HostSide<F>::out(ax, ay, out);
 }
 
-// MSM over prepared point records (internal form, see Rec<F>).  `recs` may be
-// the workspace's own conversion buffer or a proving key's resident queries.
+// MSMs of `nsets` point sets over one scalar vector of n entries (see
+// BaseSets): one digit sort, then accumulation, chunk combine and bucket
+// reduction for all sets in the same launches (the set is a grid dimension),
+// so the sets share every latency-bound step.  Point records are in the
+// internal form (see Rec<F>): the workspace's conversion buffer or a proving
+// key's resident queries.  outs[s] receives set s's affine result.
 template <class F>
-static int msm_run_recs(zk_context* ctx, MsmWorkspace& ws, const uint4* recs, const void* d_scalars, size_t n,
-                        uint64_t* out, hipStream_t st, const MsmHook* hook = nullptr) {
+static int msm_run_sets(zk_context* ctx, MsmWorkspace& ws, const BaseSets& sets, int nsets, const void* d_scalars,
+                        size_t n, uint64_t* const* outs, hipStream_t st, const MsmHook* hook = nullptr) {
   constexpr int OUTW = sizeof(F) == sizeof(fq) ? 8 : 16;
-  memset(out, 0, OUTW * 8);
+  if (nsets < 1 || nsets > MSM_SETS) return ctx->fail(ZK_ERR_INVALID, "msm: 1 to 3 point sets");
+  for (int k = 0; k < nsets; k++) memset(outs[k], 0, OUTW * 8);
   if (n == 0) return ZK_OK;
   if (n > MSM_MAX_N) return ctx->fail(ZK_ERR_SIZE, "msm: n above 2^26");
   constexpr bool G2 = sizeof(F) != sizeof(fq);
@@ -830,11 +882,11 @@ static int msm_run_recs(zk_context* ctx, MsmWorkspace& ws, const uint4* recs, co
   ZK_TRY(ctx->ensure(ws.start, nbuckets * 4));
   ZK_TRY(ctx->ensure(ws.end, nbuckets * 4));
   ZK_TRY(ctx->ensure(ws.wstat, (size_t)W * 8));
-  ZK_TRY(ctx->ensure(ws.buckets, nbuckets * sizeof(xyzz<F>)));
-  ZK_TRY(ctx->ensure(ws.hkey, (size_t)nchunks * 4));
-  ZK_TRY(ctx->ensure(ws.tkey, (size_t)nchunks * 4));
-  ZK_TRY(ctx->ensure(ws.hpt, (size_t)nchunks * sizeof(xyzz<F>)));
-  ZK_TRY(ctx->ensure(ws.tpt, (size_t)nchunks * sizeof(xyzz<F>)));
+  ZK_TRY(ctx->ensure(ws.buckets, nsets * nbuckets * sizeof(xyzz<F>)));
+  ZK_TRY(ctx->ensure(ws.hkey, (size_t)nsets * nchunks * 4));
+  ZK_TRY(ctx->ensure(ws.tkey, (size_t)nsets * nchunks * 4));
+  ZK_TRY(ctx->ensure(ws.hpt, (size_t)nsets * nchunks * sizeof(xyzz<F>)));
+  ZK_TRY(ctx->ensure(ws.tpt, (size_t)nsets * nchunks * sizeof(xyzz<F>)));
   if (!ws.h_stat) ZK_HIP(ctx, hipHostMalloc((void**)&ws.h_stat, 2 * 32 * 4, hipHostMallocDefault));
   if (!ws.stat_ready) ZK_HIP(ctx, hipEventCreateWithFlags(&ws.stat_ready, hipEventDisableTiming));
 
@@ -878,8 +930,9 @@ static int msm_run_recs(zk_context* ctx, MsmWorkspace& ws, const uint4* recs, co
   }
 
   ChunkSlots<F> slots{(uint32_t*)ws.hkey.p, (uint32_t*)ws.tkey.p, (xyzz<F>*)ws.hpt.p, (xyzz<F>*)ws.tpt.p};
-  ZK_LAUNCH(ctx, st, "msm_accumulate", k_msm_accumulate<F>, dim3(cdiv(nchunks, 256)), dim3(256), 0, sorted, recs,
-            start, end, wstat, nchunks, cpw, n_pad, L0, buckets, slots);
+  const uint32_t gx = cdiv(nchunks, 256);
+  ZK_LAUNCH(ctx, st, "msm_accumulate", k_msm_accumulate<F>, dim3(gx, nsets), dim3(256), 0, sorted, sets, start, end,
+            wstat, nchunks, cpw, n_pad, L0, nbuckets, buckets, slots);
   if (hook) {
     ZK_HIP(ctx, hipEventRecord(hook->ev, st));
     hook->fn(hook->arg);
@@ -891,13 +944,13 @@ static int msm_run_recs(zk_context* ctx, MsmWorkspace& ws, const uint4* recs, co
   for (int w = 0; w < W; w++) maxrun = std::max(maxrun, ws.h_stat[2 * w + 1]);
   const uint32_t max_span = (maxrun + L0 - 2) / L0 + 1;  // chunks spanned by the largest bucket
   if (max_span <= MSM_SERIAL_SPAN + 1) {
-    ZK_LAUNCH(ctx, st, "msm_combine", k_msm_combine_serial<F>, dim3(cdiv(nchunks, 256)), dim3(256), 0, slots, end,
-              nchunks, L0, buckets);
+    ZK_LAUNCH(ctx, st, "msm_combine", k_msm_combine_serial<F>, dim3(gx, nsets), dim3(256), 0, slots, end, nchunks,
+              L0, nbuckets, buckets);
   } else {
     for (uint32_t step = 1; step < max_span; step <<= 1)
-      ZK_LAUNCH(ctx, st, "msm_combine", k_msm_combine<F>, dim3(cdiv(nchunks, 256)), dim3(256), 0, slots, start,
-                end, nchunks, L0, step);
-    ZK_LAUNCH(ctx, st, "msm_combine", k_msm_finalize<F>, dim3(cdiv(nchunks, 256)), dim3(256), 0, slots, nchunks,
+      ZK_LAUNCH(ctx, st, "msm_combine", k_msm_combine<F>, dim3(gx, nsets), dim3(256), 0, slots, start, end, nchunks,
+                L0, step);
+    ZK_LAUNCH(ctx, st, "msm_combine", k_msm_finalize<F>, dim3(gx, nsets), dim3(256), 0, slots, nchunks, nbuckets,
               buckets);
   }
 
@@ -916,24 +969,39 @@ static int msm_run_recs(zk_context* ctx, MsmWorkspace& ws, const uint4* recs, co
   }
   if (T1 < 1 || T1 > TMAX || (T1 & (T1 - 1)) || K < 1 || (size_t)K * ((size_t)T1 << log2g) != B)
     return ctx->fail(ZK_ERR_INVALID, "msm: unsupported reduction shape");
-  ZK_TRY(ctx->ensure(ws.seg, (size_t)K * W * sizeof(xyzz<F>)));
-  ZK_TRY(ctx->ensure(ws.grp, (size_t)K * W * sizeof(xyzz<F>)));
-  ZK_TRY(ctx->ensure(ws.win, (size_t)W * sizeof(xyzz<F>)));
+  const uint32_t WS = (uint32_t)W * nsets;  // windows of all sets
+  ZK_TRY(ctx->ensure(ws.seg, (size_t)K * WS * sizeof(xyzz<F>)));
+  ZK_TRY(ctx->ensure(ws.grp, (size_t)K * WS * sizeof(xyzz<F>)));
+  ZK_TRY(ctx->ensure(ws.win, (size_t)WS * sizeof(xyzz<F>)));
   xyzz<F>* Pk = (xyzz<F>*)ws.seg.p;
   xyzz<F>* RUNk = (xyzz<F>*)ws.grp.p;
   xyzz<F>* win = (xyzz<F>*)ws.win.p;
-  ZK_LAUNCH(ctx, st, "msm_reduce", (k_msm_reduce1<F, TMAX>), dim3(K * W), dim3(T1), 0, buckets, start, end, B, K,
-            log2g, Pk, RUNk);
+  ZK_LAUNCH(ctx, st, "msm_reduce", (k_msm_reduce1<F, TMAX>), dim3(K * WS), dim3(T1), 0, buckets, start, end, B, K,
+            (uint32_t)W, log2g, Pk, RUNk);
   int log2tg = log2g;
   while ((1 << (log2tg - log2g)) < T1) log2tg++;
   uint32_t k2 = 1;
   while (k2 < K) k2 <<= 1;
-  ZK_LAUNCH(ctx, st, "msm_reduce2", (k_msm_reduce2<F, KMAX>), dim3(W), dim3(k2), 0, Pk, RUNk, K, log2tg, win);
-  std::vector<xyzz<F>> parts((size_t)W);
+  ZK_LAUNCH(ctx, st, "msm_reduce2", (k_msm_reduce2<F, KMAX>), dim3(WS), dim3(k2), 0, Pk, RUNk, K, log2tg, win);
+  std::vector<xyzz<F>> parts((size_t)WS);
   ZK_HIP(ctx, hipMemcpyAsync(parts.data(), win, parts.size() * sizeof(xyzz<F>), hipMemcpyDeviceToHost, st));
   ZK_HIP(ctx, hipStreamSynchronize(st));
-  host_finish<F>(parts, W, 1, out);
+  for (int k = 0; k < nsets; k++)
+    host_finish<F>(std::vector<xyzz<F>>(parts.begin() + (size_t)k * W, parts.begin() + (size_t)(k + 1) * W), W, 1,
+                   outs[k]);
   return ZK_OK;
+}
+
+// One point set over all n scalars.
+template <class F>
+static int msm_run_recs(zk_context* ctx, MsmWorkspace& ws, const uint4* recs, const void* d_scalars, size_t n,
+                        uint64_t* out, hipStream_t st, const MsmHook* hook = nullptr) {
+  BaseSets sets{};
+  sets.recs[0] = recs;
+  sets.lo[0] = 0;
+  sets.hi[0] = (uint32_t)std::min<size_t>(n, 0xffffffffu);
+  uint64_t* outs[1] = {out};
+  return msm_run_sets<F>(ctx, ws, sets, 1, d_scalars, n, outs, st, hook);
 }
 
 template <class F>
@@ -963,6 +1031,19 @@ int msm_g2_run(zk_context* ctx, const void* d_points, const void* d_scalars, siz
 }
 
 MsmWorkspace* msm_workspace_new() { return new MsmWorkspace(); }
+
+int msm_g1_sets_ws(zk_context* ctx, MsmWorkspace* ws, int nsets, const void* const* recs, const size_t* lo,
+                   const size_t* count, const void* d_scalars, size_t n, uint64_t* const* outs, hipStream_t st) {
+  if (!ws || nsets < 1 || nsets > MSM_SETS) return ctx->fail(ZK_ERR_INVALID, "msm: 1 to 3 point sets");
+  BaseSets sets{};
+  for (int k = 0; k < nsets; k++) {
+    if (lo[k] + count[k] > n) return ctx->fail(ZK_ERR_INVALID, "msm: point set beyond the scalars");
+    sets.recs[k] = (const uint4*)recs[k];
+    sets.lo[k] = (uint32_t)lo[k];
+    sets.hi[k] = (uint32_t)(lo[k] + count[k]);
+  }
+  return msm_run_sets<fq>(ctx, *ws, sets, nsets, d_scalars, n, outs, st);
+}
 
 int msm_recs_ws(zk_context* ctx, MsmWorkspace* ws, bool g2, const void* d_recs, const void* d_scalars, size_t n,
                 uint64_t* out, hipStream_t st, const MsmHook* hook) {

@@ -142,6 +142,11 @@ struct MsmHook {
 // MSM over records with an explicit workspace (one per concurrent caller)
 int msm_recs_ws(zk_context* ctx, MsmWorkspace* ws, bool g2, const void* d_recs, const void* d_scalars, size_t n,
                 uint64_t* out_affine, hipStream_t st, const MsmHook* after_accumulate = nullptr);
+// G1 MSMs of up to 3 point sets over one scalar vector of n entries, sharing
+// the digit sort and every latency-bound step: set k multiplies recs[k][j] by
+// scalar lo[k] + j for j < count[k]; outs[k] gets its affine result.
+int msm_g1_sets_ws(zk_context* ctx, MsmWorkspace* ws, int nsets, const void* const* recs, const size_t* lo,
+                   const size_t* count, const void* d_scalars, size_t n, uint64_t* const* outs, hipStream_t st);
 
 // ---- fixed base (pointgen.hip)
 int g1_generator_mul(zk_context* ctx, const void* d_scalars, size_t n, void* d_out, hipStream_t st);
