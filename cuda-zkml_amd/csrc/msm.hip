@@ -35,6 +35,7 @@
 #include <vector>
 
 #include "curve.hpp"
+#include "curve_split.hpp"
 #include "host_bn254.hpp"
 #include "zk_internal.hpp"
 
@@ -569,25 +570,44 @@ __global__ __launch_bounds__(256) void k_msm_accumulate(const uint2* __restrict_
   slots.tkey[ch] = tk;
 }
 
+// The chunk combine and the bucket reduction are chains of dependent point
+// additions run by comparatively few threads.  They work on Lanes<F>: one
+// lane per point for G1, a lane pair per point for G2 (see curve_split.hpp),
+// so a G2 chain runs about twice as fast.  `item` is the pair index; both
+// lanes of a pair always take the same branches.
+template <class F>
+__device__ __forceinline__ uint32_t lane_item() {
+  return (blockIdx.x * blockDim.x + threadIdx.x) / Lanes<F>::N;
+}
+
 // One level of the tree over the chunk partials of buckets spanning chunks.
 template <class F>
 __global__ __launch_bounds__(256) void k_msm_combine(ChunkSlots<F> all_slots, const uint32_t* __restrict__ start,
                                                      const uint32_t* __restrict__ end, uint32_t nchunks,
                                                      uint32_t L0, uint32_t step) {
+  typedef Lanes<F> LN;
   msm_priority<F>();
-  const uint32_t ch = blockIdx.x * blockDim.x + threadIdx.x;
+  const uint32_t ch = lane_item<F>();
   if (ch >= nchunks) return;
   const ChunkSlots<F> slots = all_slots.at(blockIdx.y, nchunks);
   const uint32_t tk = slots.tkey[ch];
   if (tk != KEY_INVALID) {
     const uint32_t c1 = (end[tk] - 1) / L0;
-    if (ch + step <= c1) xyzz_add(slots.tpt[ch], slots.hpt[ch + step]);
+    if (ch + step <= c1) {
+      auto v = LN::load(slots.tpt[ch]);
+      xyzz_add(v, LN::load(slots.hpt[ch + step]));
+      LN::store(slots.tpt[ch], v);
+    }
   }
   const uint32_t hk = slots.hkey[ch];
   if (hk != KEY_INVALID) {
     const uint32_t c0 = start[hk] / L0, c1 = (end[hk] - 1) / L0;
     const uint32_t j = ch - c0;
-    if ((j % (2 * step)) == 0 && ch + step <= c1) xyzz_add(slots.hpt[ch], slots.hpt[ch + step]);
+    if ((j % (2 * step)) == 0 && ch + step <= c1) {
+      auto v = LN::load(slots.hpt[ch]);
+      xyzz_add(v, LN::load(slots.hpt[ch + step]));
+      LN::store(slots.hpt[ch], v);
+    }
   }
 }
 
@@ -601,24 +621,25 @@ __global__ __launch_bounds__(256) void k_msm_combine_serial(ChunkSlots<F> all_sl
                                                             const uint32_t* __restrict__ end, uint32_t nchunks,
                                                             uint32_t L0, size_t nbuckets,
                                                             xyzz<F>* __restrict__ buckets) {
+  typedef Lanes<F> LN;
   msm_priority<F>();
-  const uint32_t ch = blockIdx.x * blockDim.x + threadIdx.x;
+  const uint32_t ch = lane_item<F>();
   if (ch >= nchunks) return;
   const ChunkSlots<F> slots = all_slots.at(blockIdx.y, nchunks);
   buckets += blockIdx.y * nbuckets;
   const uint32_t tk = slots.tkey[ch];
   if (tk == KEY_INVALID) return;
   const uint32_t c1 = (end[tk] - 1) / L0;
-  xyzz<F> acc = slots.tpt[ch];
-  for (uint32_t j = ch + 1; j <= c1; j++) xyzz_add(acc, slots.hpt[j]);
-  buckets[tk] = acc;
+  auto acc = LN::load(slots.tpt[ch]);
+  for (uint32_t j = ch + 1; j <= c1; j++) xyzz_add(acc, LN::load(slots.hpt[j]));
+  LN::store(buckets[tk], acc);
 }
 
 template <class F>
 __global__ __launch_bounds__(256) void k_msm_finalize(ChunkSlots<F> all_slots, uint32_t nchunks, size_t nbuckets,
                                                       xyzz<F>* __restrict__ buckets) {
   msm_priority<F>();
-  const uint32_t ch = blockIdx.x * blockDim.x + threadIdx.x;
+  const uint32_t ch = blockIdx.x * blockDim.x + threadIdx.x;  // a plain copy: one lane per point
   if (ch >= nchunks) return;
   const ChunkSlots<F> slots = all_slots.at(blockIdx.y, nchunks);
   buckets += blockIdx.y * nbuckets;
@@ -638,102 +659,112 @@ __global__ __launch_bounds__(256) void k_msm_finalize(ChunkSlots<F> all_slots, u
 // group.  Outputs per group: P_k (that sum) and RUN_k = SR_0.
 // Level 2 (one workgroup per window, K groups):
 //   sum_b b S_b = sum_k P_k + T G sum_{s >= 1} SRUN_s,  same scan and tree.
+// "Thread" t is a lane pair for G2 (Lanes<F>); T = blockDim.x / Lanes<F>::N.
 
-// Inclusive suffix scan over the T values held by the threads of a
-// workgroup (T = blockDim.x); returns this thread's sum_{u >= t} v_u.
-template <class F>
-__device__ __forceinline__ xyzz<F> wg_suffix_scan(xyzz<F> v, xyzz<F>* sh, int T) {
-  const int t = threadIdx.x;
-  sh[t] = v;
+// Inclusive suffix scan over the T values held by the items of a workgroup;
+// returns this item's sum_{u >= t} v_u.
+template <class F, class R>
+__device__ __forceinline__ xyzz<R> wg_suffix_scan(xyzz<R> v, xyzz<F>* sh, int T) {
+  typedef Lanes<F> LN;
+  const int t = threadIdx.x / LN::N;
+  LN::store(sh[t], v);
   __syncthreads();
   for (int d = 1; d < T; d <<= 1) {
-    xyzz<F> o;
+    xyzz<R> o;
     const bool has = t + d < T;
-    if (has) o = sh[t + d];
+    if (has) o = LN::load(sh[t + d]);
     __syncthreads();
     if (has) {
       xyzz_add(v, o);
-      sh[t] = v;
+      LN::store(sh[t], v);
     }
     __syncthreads();
   }
   return v;
 }
 
-// Sum of the T values of a workgroup (T a power of two), valid in thread 0.
-template <class F>
-__device__ __forceinline__ xyzz<F> wg_sum(xyzz<F> v, xyzz<F>* sh, int T) {
-  const int t = threadIdx.x;
+// Sum of the T values of a workgroup (T a power of two), valid in item 0.
+template <class F, class R>
+__device__ __forceinline__ xyzz<R> wg_sum(xyzz<R> v, xyzz<F>* sh, int T) {
+  typedef Lanes<F> LN;
+  const int t = threadIdx.x / LN::N;
   __syncthreads();
-  sh[t] = v;
+  LN::store(sh[t], v);
   __syncthreads();
   for (int h = T / 2; h >= 1; h >>= 1) {
     if (t < h) {
-      xyzz_add(v, sh[t + h]);
-      sh[t] = v;
+      xyzz_add(v, LN::load(sh[t + h]));
+      LN::store(sh[t], v);
     }
     __syncthreads();
   }
   return v;
 }
 
-// Level 1: block k of window w (blockIdx.x = w*K + k), T = blockDim.x threads
-// of G buckets each (G = 2^log2g).  Windows of several base sets follow each
-// other (W_set windows per set); the sorted-list bounds start/end are those
-// of the window within its set.
+// Level 1: block k of window w (blockIdx.x = w*K + k), T items of G buckets
+// each (G = 2^log2g).  Windows of several base sets follow each other (W_set
+// windows per set); the sorted-list bounds start/end are those of the window
+// within its set.
 template <class F, int TMAX>
-__global__ __launch_bounds__(TMAX) void k_msm_reduce1(const xyzz<F>* __restrict__ buckets,
-                                                      const uint32_t* __restrict__ start,
-                                                      const uint32_t* __restrict__ end, uint32_t B1, uint32_t K,
-                                                      uint32_t W_set, int log2g, xyzz<F>* __restrict__ P,
-                                                      xyzz<F>* __restrict__ RUN) {
+__global__ __launch_bounds__(TMAX * Lanes<F>::N) void k_msm_reduce1(const xyzz<F>* __restrict__ buckets,
+                                                                    const uint32_t* __restrict__ start,
+                                                                    const uint32_t* __restrict__ end, uint32_t B1,
+                                                                    uint32_t K, uint32_t W_set, int log2g,
+                                                                    xyzz<F>* __restrict__ P,
+                                                                    xyzz<F>* __restrict__ RUN) {
+  typedef Lanes<F> LN;
+  typedef typename LN::R R;
   msm_priority<F>();
   __shared__ xyzz<F> sh[TMAX];
-  const int T = blockDim.x, G = 1 << log2g;
+  const int T = blockDim.x / LN::N, G = 1 << log2g;
   const uint32_t w = blockIdx.x / K, k = blockIdx.x % K;
-  const uint32_t t = threadIdx.x;
-  const uint32_t kb = w * B1 + (k * T + t) * G;                // bucket of this thread's first entry
-  const uint32_t sb = (w % W_set) * B1 + (k * T + t) * G;      // its key in the sorted list
-  xyzz<F> run, acc;
+  const uint32_t t = threadIdx.x / LN::N;
+  const uint32_t kb = w * B1 + (k * T + t) * G;            // bucket of this item's first entry
+  const uint32_t sb = (w % W_set) * B1 + (k * T + t) * G;  // its key in the sorted list
+  xyzz<R> run, acc;
   xyzz_set_inf(run);
   xyzz_set_inf(acc);
   for (int i = G - 1; i >= 0; i--) {
-    if (end[sb + i] > start[sb + i]) xyzz_add(run, buckets[kb + i]);
+    if (end[sb + i] > start[sb + i]) xyzz_add(run, LN::load(buckets[kb + i]));
     xyzz_add(acc, run);
   }
-  xyzz<F> sr = wg_suffix_scan<F>(run, sh, T);
+  xyzz<R> sr = wg_suffix_scan<F, R>(run, sh, T);
   if (t >= 1) {
     for (int d = 0; d < log2g; d++) xyzz_dbl(sr);
     xyzz_add(acc, sr);
   } else {
-    RUN[blockIdx.x] = sr;  // thread 0 holds the group total
+    LN::store(RUN[blockIdx.x], sr);  // item 0 holds the group total
   }
-  xyzz<F> tot = wg_sum<F>(acc, sh, T);
-  if (t == 0) P[blockIdx.x] = tot;
+  xyzz<R> tot = wg_sum<F, R>(acc, sh, T);
+  if (t == 0) LN::store(P[blockIdx.x], tot);
 }
 
-// Level 2: one workgroup per window over its K group results (blockDim.x a
-// power of two >= K); log2tg = log2(T*G) of level 1.
+// Level 2: one workgroup per window over its K group results (a power of two
+// >= K items); log2tg = log2(T*G) of level 1.
 template <class F, int KMAX>
-__global__ __launch_bounds__(KMAX) void k_msm_reduce2(const xyzz<F>* __restrict__ P, const xyzz<F>* __restrict__ RUN,
-                                                      uint32_t K, int log2tg, xyzz<F>* __restrict__ out) {
+__global__ __launch_bounds__(KMAX * Lanes<F>::N) void k_msm_reduce2(const xyzz<F>* __restrict__ P,
+                                                                    const xyzz<F>* __restrict__ RUN, uint32_t K,
+                                                                    int log2tg, xyzz<F>* __restrict__ out) {
+  typedef Lanes<F> LN;
+  typedef typename LN::R R;
   msm_priority<F>();
   __shared__ xyzz<F> sh[KMAX];
-  const uint32_t w = blockIdx.x, t = threadIdx.x;
-  xyzz<F> run, acc;
+  const uint32_t w = blockIdx.x, t = threadIdx.x / LN::N;
+  const int T = blockDim.x / LN::N;
+  xyzz<R> run, acc;
   xyzz_set_inf(run);
   xyzz_set_inf(acc);
   if (t < K) {
-    run = RUN[w * K + t];
-    acc = P[w * K + t];
+    run = LN::load(RUN[w * K + t]);
+    acc = LN::load(P[w * K + t]);
   }
-  xyzz<F> sr = wg_suffix_scan<F>(run, sh, blockDim.x);
+  xyzz<R> sr = wg_suffix_scan<F, R>(run, sh, T);
   if (t >= 1 && t < K) {
     for (int d = 0; d < log2tg; d++) xyzz_dbl(sr);
     xyzz_add(acc, sr);
   }
-  xyzz<F> tot = wg_sum<F>(acc, sh, blockDim.x);
-  if (t == 0) out[w] = tot;
+  xyzz<R> tot = wg_sum<F, R>(acc, sh, T);
+  if (t == 0) LN::store(out[w], tot);
 }
 
 // ------------------------------------------------------------------ workspace
@@ -931,6 +962,7 @@ static int msm_run_sets(zk_context* ctx, MsmWorkspace& ws, const BaseSets& sets,
 
   ChunkSlots<F> slots{(uint32_t*)ws.hkey.p, (uint32_t*)ws.tkey.p, (xyzz<F>*)ws.hpt.p, (xyzz<F>*)ws.tpt.p};
   const uint32_t gx = cdiv(nchunks, 256);
+  const uint32_t gxl = cdiv((size_t)nchunks * Lanes<F>::N, 256);  // combine: Lanes<F>::N lanes per chunk
   ZK_LAUNCH(ctx, st, "msm_accumulate", k_msm_accumulate<F>, dim3(gx, nsets), dim3(256), 0, sorted, sets, start, end,
             wstat, nchunks, cpw, n_pad, L0, nbuckets, buckets, slots);
   if (hook) {
@@ -944,19 +976,20 @@ static int msm_run_sets(zk_context* ctx, MsmWorkspace& ws, const BaseSets& sets,
   for (int w = 0; w < W; w++) maxrun = std::max(maxrun, ws.h_stat[2 * w + 1]);
   const uint32_t max_span = (maxrun + L0 - 2) / L0 + 1;  // chunks spanned by the largest bucket
   if (max_span <= MSM_SERIAL_SPAN + 1) {
-    ZK_LAUNCH(ctx, st, "msm_combine", k_msm_combine_serial<F>, dim3(gx, nsets), dim3(256), 0, slots, end, nchunks,
+    ZK_LAUNCH(ctx, st, "msm_combine", k_msm_combine_serial<F>, dim3(gxl, nsets), dim3(256), 0, slots, end, nchunks,
               L0, nbuckets, buckets);
   } else {
     for (uint32_t step = 1; step < max_span; step <<= 1)
-      ZK_LAUNCH(ctx, st, "msm_combine", k_msm_combine<F>, dim3(gx, nsets), dim3(256), 0, slots, start, end, nchunks,
+      ZK_LAUNCH(ctx, st, "msm_combine", k_msm_combine<F>, dim3(gxl, nsets), dim3(256), 0, slots, start, end, nchunks,
                 L0, step);
     ZK_LAUNCH(ctx, st, "msm_combine", k_msm_finalize<F>, dim3(gx, nsets), dim3(256), 0, slots, nchunks, nbuckets,
               buckets);
   }
 
   // bucket reduction: level 1 (T threads x G buckets per group), level 2 per window
+  // items per workgroup (a G2 item is a lane pair: 256 lanes either way)
   constexpr int TMAX = sizeof(F) == sizeof(fq) ? 256 : 128;
-  constexpr int KMAX = 256;
+  constexpr int KMAX = TMAX;
   // measured: T = TMAX; G = 8 for 2^15 buckets per window, else 4
   int T1 = TMAX, log2g = B >= 32768 ? 3 : 2;
   // shrink the group for small windows: T1 * G <= B
@@ -976,13 +1009,14 @@ static int msm_run_sets(zk_context* ctx, MsmWorkspace& ws, const BaseSets& sets,
   xyzz<F>* Pk = (xyzz<F>*)ws.seg.p;
   xyzz<F>* RUNk = (xyzz<F>*)ws.grp.p;
   xyzz<F>* win = (xyzz<F>*)ws.win.p;
-  ZK_LAUNCH(ctx, st, "msm_reduce", (k_msm_reduce1<F, TMAX>), dim3(K * WS), dim3(T1), 0, buckets, start, end, B, K,
-            (uint32_t)W, log2g, Pk, RUNk);
+  ZK_LAUNCH(ctx, st, "msm_reduce", (k_msm_reduce1<F, TMAX>), dim3(K * WS), dim3(T1 * Lanes<F>::N), 0, buckets, start,
+            end, B, K, (uint32_t)W, log2g, Pk, RUNk);
   int log2tg = log2g;
   while ((1 << (log2tg - log2g)) < T1) log2tg++;
   uint32_t k2 = 1;
   while (k2 < K) k2 <<= 1;
-  ZK_LAUNCH(ctx, st, "msm_reduce2", (k_msm_reduce2<F, KMAX>), dim3(WS), dim3(k2), 0, Pk, RUNk, K, log2tg, win);
+  ZK_LAUNCH(ctx, st, "msm_reduce2", (k_msm_reduce2<F, KMAX>), dim3(WS), dim3(k2 * Lanes<F>::N), 0, Pk, RUNk, K,
+            log2tg, win);
   std::vector<xyzz<F>> parts((size_t)WS);
   ZK_HIP(ctx, hipMemcpyAsync(parts.data(), win, parts.size() * sizeof(xyzz<F>), hipMemcpyDeviceToHost, st));
   ZK_HIP(ctx, hipStreamSynchronize(st));
