@@ -86,6 +86,7 @@ void zk_destroy(zk_context* ctx) {
   }
   for (DevBuf* b : {&ctx->scratch_a, &ctx->scratch_b, &ctx->scratch_c})
     if (b->p) (void)hipFree(b->p);
+  if (ctx->h_flag) (void)hipHostFree(ctx->h_flag);
   if (ctx->g1_table) (void)hipFree(ctx->g1_table);
   if (ctx->g2_table) (void)hipFree(ctx->g2_table);
   (void)hipStreamDestroy(ctx->stream);

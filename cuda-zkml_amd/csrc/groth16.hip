@@ -68,6 +68,7 @@ struct Csr3 {
 // out[mat * n + row] = sum_e w[col_e] * v_e  (A.w, B.w, C.w in evaluation form,
 // groth16.cu:275-294).  One thread per (row, matrix).
 __global__ void k_spmv3(uint4* __restrict__ out, const uint4* __restrict__ w, Csr3 m, size_t n) {
+  quotient_priority();
   const size_t row = blockIdx.x * (size_t)blockDim.x + threadIdx.x;
   const int mat = blockIdx.y;
   if (row >= n) return;
@@ -80,6 +81,7 @@ __global__ void k_spmv3(uint4* __restrict__ out, const uint4* __restrict__ w, Cs
 // Row check (A.w)(B.w) = C.w for rows < nc (circuit.cuh:93-124).  With raw
 // Montgomery words fmul(a, b) = ab 2^251 and fmul(c, 2^256) = c 2^251.
 __global__ void k_check_rows(const uint4* __restrict__ abc, size_t n, size_t nc, uint32_t* __restrict__ bad) {
+  quotient_priority();
   const size_t row = blockIdx.x * (size_t)blockDim.x + threadIdx.x;
   if (row >= nc) return;
   const uint32_t K256[8] = {0x4ffffffbu, 0xac96341cu, 0x9f60cd29u, 0x36fc7695u,
@@ -540,8 +542,8 @@ int zk_prove(zk_context* ctx, const zk_pk* pk, const zk_r1cs* c, const void* h_w
              uint64_t blind_seed, int check_witness, uint8_t proof_out[256], double* timings) {
   if (!ctx || !pk || !c || !proof_out || (m && !h_witness)) return ZK_ERR_INVALID;
   // events: 0 start, 1 witness resident, 2 quotient done, 3 end,
-  // 4 + 2j / 5 + 2j start / end of MSM job j, last: G2 accumulation enqueued
-  constexpr int NEV = 5 + 2 * ZK_JOBS;
+  // 4 + 2j / 5 + 2j start / end of MSM job j
+  constexpr int NEV = 4 + 2 * ZK_JOBS;
   hipEvent_t ev[NEV];
   for (auto& e : ev) ZK_HIP(ctx, hipEventCreate(&e));
   struct EvGuard {
@@ -594,49 +596,17 @@ int zk_prove(zk_context* ctx, const zk_pk* pk, const zk_r1cs* c, const void* h_w
   // Job slots (timings): 0 A, 1 B2, 2 L, 3 H, 4 B1; A, L and B1 share one run.
   constexpr int JOB_G1 = 0, JOB_B2 = 1, JOB_H = 3;
   int rc_g1 = ZK_OK, rc_b2 = ZK_OK, rc_h = ZK_OK;
-  // The G2 MSM is the longest: its accumulation runs first on its own and the
-  // G1 MSMs start once it is enqueued (their streams wait for it), so that they
-  // fill the GPU during the G2 MSM's latency-bound combine and reduction.
-  struct Gate {
-    std::mutex m;
-    std::condition_variable cv;
-    bool open = false, recorded = false;
-    void release(bool rec) {
-      {
-        std::lock_guard<std::mutex> lk(m);
-        if (open) return;
-        open = true;
-        recorded = rec;
-      }
-      cv.notify_all();
-    }
-    bool wait_on(hipStream_t s, hipEvent_t e) {
-      std::unique_lock<std::mutex> lk(m);
-      cv.wait(lk, [&] { return open; });
-      return !recorded || hipStreamWaitEvent(s, e, 0) == hipSuccess;
-    }
-  } gate;
-  MsmHook hook;
-  hook.ev = ev[NEV - 1];
-  hook.fn = [](void* a) { ((Gate*)a)->release(true); };
-  hook.arg = &gate;
   auto record = [&](int slot, hipStream_t s, int& rc) {
     if (hipEventRecord(ev[slot], s) != hipSuccess && rc == ZK_OK) rc = ctx->fail(ZK_ERR_HIP, "prove: event record");
   };
   auto run_b2 = [&] {
     hipStream_t js = ctx->job_stream[S_G2];
     record(4 + 2 * JOB_B2, js, rc_b2);
-    if (rc_b2 == ZK_OK && nb2)
-      rc_b2 = msm_recs_ws(ctx, ctx->job_ws[JOB_B2], true, pk->B2, d_w, nb2, b2_msm, js, &hook);
+    if (rc_b2 == ZK_OK && nb2) rc_b2 = msm_recs_ws(ctx, ctx->job_ws[JOB_B2], true, pk->B2, d_w, nb2, b2_msm, js);
     record(5 + 2 * JOB_B2, js, rc_b2);
-    gate.release(false);  // no-op when the hook already ran
   };
   auto run_g1 = [&] {
     hipStream_t js = ctx->job_stream[S_G1];
-    if (!gate.wait_on(js, hook.ev)) {
-      rc_g1 = ctx->fail(ZK_ERR_HIP, "prove: stream wait");
-      return;
-    }
     record(4 + 2 * JOB_G1, js, rc_g1);
     const void* recs[3];
     size_t lo[3], cnt[3];
@@ -661,20 +631,22 @@ int zk_prove(zk_context* ctx, const zk_pk* pk, const zk_r1cs* c, const void* h_w
   std::vector<std::thread> workers;
   for (const std::function<void()>& fn : {std::function<void()>(run_b2), std::function<void()>(run_g1)}) {
     try {
-      workers.emplace_back(fn);  // the G2 job first: the G1 job waits for it
+      workers.emplace_back(fn);
     } catch (...) {
       fn();  // no thread available: run it here
     }
   }
   int qrc = quotient_run(ctx, c, d_w, d_h, ctx->scratch_b.p, st, check_witness != 0, d_bad);
-  uint32_t bad = 0;
+  // the check's count goes to pinned memory: the copy does not block this
+  // thread, which goes on to enqueue H right behind the quotient
   if (qrc == ZK_OK && check_witness) {
-    if (hipMemcpyAsync(&bad, d_bad, 4, hipMemcpyDeviceToHost, st) != hipSuccess)
+    if (!ctx->h_flag && hipHostMalloc((void**)&ctx->h_flag, 4, hipHostMallocDefault) != hipSuccess)
+      qrc = ctx->fail(ZK_ERR_OOM, "prove: pinned flag");
+    if (qrc == ZK_OK && hipMemcpyAsync(ctx->h_flag, d_bad, 4, hipMemcpyDeviceToHost, st) != hipSuccess)
       qrc = ctx->fail(ZK_ERR_HIP, "prove: witness check read-back");
   }
   if (qrc == ZK_OK && hipEventRecord(ev[2], st) != hipSuccess) qrc = ctx->fail(ZK_ERR_HIP, "prove: event record");
   if (qrc == ZK_OK) {  // H after the quotient, same stream
-    if (!gate.wait_on(st, hook.ev)) rc_h = ctx->fail(ZK_ERR_HIP, "prove: stream wait");
     record(4 + 2 * JOB_H, st, rc_h);
     if (rc_h == ZK_OK && nh) rc_h = msm_recs_ws(ctx, ctx->job_ws[JOB_H], false, pk->H, d_h, nh, h_msm, st);
     else if (!nh) memset(h_msm, 0, sizeof(h_msm));
@@ -684,7 +656,7 @@ int zk_prove(zk_context* ctx, const zk_pk* pk, const zk_r1cs* c, const void* h_w
   ZK_TRY(qrc);
   if (check_witness) {
     ZK_HIP(ctx, hipStreamSynchronize(st));
-    if (bad) return ctx->fail(ZK_ERR_WITNESS, "witness does not satisfy the R1CS");
+    if (*ctx->h_flag) return ctx->fail(ZK_ERR_WITNESS, "witness does not satisfy the R1CS");
   }
   ZK_TRY(rc_b2);
   ZK_TRY(rc_g1);

@@ -137,6 +137,7 @@ __global__ __launch_bounds__(NTT_THREADS) void k_ntt_pass_mid(uint4* __restrict_
                                                                PassArgs a, const uint32_t* __restrict__ twr,
                                                                const uint32_t* __restrict__ twp,
                                                                const uint32_t* __restrict__ pre) {
+  quotient_priority();
   __shared__ uint32_t s[NL * NTT_TILE];
   const int R = 1 << a.logR, T = a.T;
   const size_t boff = (size_t)blockIdx.y * a.n;
@@ -174,6 +175,7 @@ __global__ __launch_bounds__(NTT_THREADS) void k_ntt_pass_last(uint4* __restrict
                                                                 const uint32_t* __restrict__ pre,
                                                                 const uint32_t* __restrict__ post, fr scale,
                                                                 int scale_en) {
+  quotient_priority();
   __shared__ uint32_t s[NL * NTT_TILE];
   const int R = 1 << a.logR, T = a.T;
   const int E = R * T;
@@ -227,6 +229,7 @@ __global__ void k_fill_pow_table(uint32_t* __restrict__ t, size_t count, uint32_
 // fmul(., z 2^266) = (ab - c) z 2^256: three multiplies per element.
 __global__ void k_quotient_pointwise(uint4* __restrict__ h, const uint4* __restrict__ A, const uint4* __restrict__ B,
                                      const uint4* __restrict__ C, size_t n, fr kc, fr zk) {
+  quotient_priority();
   size_t i = blockIdx.x * (size_t)blockDim.x + threadIdx.x;
   if (i >= n) return;
   fr t = fmul(load_elem(A, i), load_elem(B, i));

@@ -460,7 +460,7 @@ int zk_statement_v2_build(const zk_layer* layers, int num_layers, const int64_t*
     out_size[(size_t)i] = l.out_size;
     switch (l.type) {
       case ZK_LAYER_LINEAR:
-        if (l.in_size < 0 || l.out_size < 0 || ((size_t)l.in_size * l.out_size && !l.weights) ||
+        if (l.in_size < 0 || l.out_size < 0 || ((size_t)l.in_size * l.out_size != 0 && !l.weights) ||
             (l.out_size && !l.bias))
           return fail("LINEAR layer " + std::to_string(i) + ": bad sizes or missing weights");
         break;

@@ -74,6 +74,7 @@ struct zk_context {
   // streams and workspaces of the concurrent MSMs inside zk_prove
   hipStream_t job_stream[zk::ZK_JOBS] = {};
   zk::MsmWorkspace* job_ws[zk::ZK_JOBS] = {};
+  uint32_t* h_flag = nullptr;  // pinned word: the proof's witness-check count
   // profiling
   bool profiling = false;
   std::map<std::string, zk::KernelStat> stats;
@@ -96,6 +97,11 @@ struct zk_context {
 };
 
 namespace zk {
+
+// Issue priority of the quotient's kernels (sparse products, NTTs, pointwise
+// step).  In a proof they run beside the G2 MSM's accumulation and the H MSM
+// waits for them: their waves outrank the MSM waves sharing a SIMD.
+__device__ __forceinline__ void quotient_priority() { __builtin_amdgcn_s_setprio(3); }
 
 // Launch helper with error capture.
 #define ZK_LAUNCH(ctx, st, name, kernel, grid, block, shmem, ...)                            \
