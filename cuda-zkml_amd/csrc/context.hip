@@ -84,7 +84,7 @@ void zk_destroy(zk_context* ctx) {
     if (ctx->job_ws[j]) msm_workspace_free(ctx->job_ws[j]);
     if (ctx->job_stream[j]) (void)hipStreamDestroy(ctx->job_stream[j]);
   }
-  for (DevBuf* b : {&ctx->scratch_a, &ctx->scratch_b, &ctx->scratch_c})
+  for (DevBuf* b : {&ctx->scratch_a, &ctx->scratch_b, &ctx->scratch_c, &ctx->scratch_d})
     if (b->p) (void)hipFree(b->p);
   if (ctx->h_flag) (void)hipHostFree(ctx->h_flag);
   if (ctx->g1_table) (void)hipFree(ctx->g1_table);

@@ -26,10 +26,14 @@ struct zk_r1cs {
   size_t n = 0;
   // CSR per matrix (A, B, C), rows < n; values are the reference's Montgomery
   // words multiplied by 32 so that fmul(w, v') = w v in Montgomery form.
-  uint32_t* rowptr[3] = {nullptr, nullptr, nullptr};
   uint32_t* col[3] = {nullptr, nullptr, nullptr};
   uint4* val[3] = {nullptr, nullptr, nullptr};
   size_t nnz[3] = {0, 0, 0};
+  // rows cut into segments of at most SPMV_SEG nonzeros: segment s covers
+  // nonzeros [seg[s].x, seg[s].y); row r owns segments [segptr[r], segptr[r+1])
+  uint32_t* segptr[3] = {nullptr, nullptr, nullptr};
+  uint2* seg[3] = {nullptr, nullptr, nullptr};
+  size_t nseg[3] = {0, 0, 0};
   // host COO copies for setup (QAP evaluation at tau)
   std::vector<zk_sparse_entry> coo[3];
 };
@@ -59,22 +63,41 @@ __device__ __forceinline__ void st_fr(uint4* __restrict__ p, size_t i, const fr&
   p[2 * i + 1] = make_uint4(w[4], w[5], w[6], w[7]);
 }
 
+constexpr uint32_t SPMV_SEG = 8;  // nonzeros per segment
+
 struct Csr3 {
-  const uint32_t* rowptr[3];
+  const uint32_t* segptr[3];
+  const uint2* seg[3];
   const uint32_t* col[3];
   const uint4* val[3];
+  size_t nseg[3];
+  size_t part_off[3];  // first partial of each matrix
 };
 
-// out[mat * n + row] = sum_e w[col_e] * v_e  (A.w, B.w, C.w in evaluation form,
-// groth16.cu:275-294).  One thread per (row, matrix).
-__global__ void k_spmv3(uint4* __restrict__ out, const uint4* __restrict__ w, Csr3 m, size_t n) {
+// A.w, B.w, C.w in evaluation form (groth16.cu:275-294) in two steps so that
+// no thread walks a long row: one thread per (segment, matrix) forms the
+// segment's partial sum sum_e w[col_e] * v_e ...
+__global__ void k_spmv_seg(uint4* __restrict__ part, const uint4* __restrict__ w, Csr3 m) {
+  quotient_priority();
+  const size_t s = blockIdx.x * (size_t)blockDim.x + threadIdx.x;
+  const int mat = blockIdx.y;
+  if (s >= m.nseg[mat]) return;
+  const uint2 r = m.seg[mat][s];
+  fr acc = fe_zero<FrP>();
+  for (uint32_t k = r.x; k < r.y; k++) acc = fadd(acc, fmul(ld_fr(w, m.col[mat][k]), ld_fr(m.val[mat], k)));
+  st_fr(part, m.part_off[mat] + s, acc);
+}
+
+// ... then one thread per (row, matrix) adds its segments' partials:
+// out[mat * n + row].
+__global__ void k_spmv_rows(uint4* __restrict__ out, const uint4* __restrict__ part, Csr3 m, size_t n) {
   quotient_priority();
   const size_t row = blockIdx.x * (size_t)blockDim.x + threadIdx.x;
   const int mat = blockIdx.y;
   if (row >= n) return;
-  const uint32_t b = m.rowptr[mat][row], e = m.rowptr[mat][row + 1];
+  const uint32_t b = m.segptr[mat][row], e = m.segptr[mat][row + 1];
   fr acc = fe_zero<FrP>();
-  for (uint32_t k = b; k < e; k++) acc = fadd(acc, fmul(ld_fr(w, m.col[mat][k]), ld_fr(m.val[mat], k)));
+  for (uint32_t k = b; k < e; k++) acc = fadd(acc, ld_fr(part, m.part_off[mat] + k));
   st_fr(out, (size_t)mat * n + row, acc);
 }
 
@@ -193,13 +216,23 @@ int quotient_run(zk_context* ctx, const zk_r1cs* c, const void* d_w, void* d_h, 
                  bool check, uint32_t* d_bad) {
   const size_t n = c->n;
   Csr3 m;
+  size_t nparts = 0, segmax = 1;
   for (int k = 0; k < 3; k++) {
-    m.rowptr[k] = c->rowptr[k];
+    m.segptr[k] = c->segptr[k];
+    m.seg[k] = c->seg[k];
     m.col[k] = c->col[k];
     m.val[k] = c->val[k];
+    m.nseg[k] = c->nseg[k];
+    m.part_off[k] = nparts;
+    nparts += c->nseg[k];
+    segmax = std::max(segmax, c->nseg[k]);
   }
-  ZK_LAUNCH(ctx, st, "quotient_spmv", k_spmv3, dim3(cdiv(n, 256), 3), dim3(256), 0, (uint4*)d_abc,
-            (const uint4*)d_w, m, n);
+  ZK_TRY(ctx->ensure(ctx->scratch_d, std::max<size_t>(nparts, 1) * 32));
+  uint4* part = (uint4*)ctx->scratch_d.p;
+  ZK_LAUNCH(ctx, st, "quotient_spmv", k_spmv_seg, dim3(cdiv(segmax, 256), 3), dim3(256), 0, part, (const uint4*)d_w,
+            m);
+  ZK_LAUNCH(ctx, st, "quotient_spmv", k_spmv_rows, dim3(cdiv(n, 256), 3), dim3(256), 0, (uint4*)d_abc,
+            (const uint4*)part, m, n);
   if (check) {
     ZK_HIP(ctx, hipMemsetAsync(d_bad, 0, 4, st));
     ZK_LAUNCH(ctx, st, "witness_check", k_check_rows, dim3(cdiv((size_t)c->nc, 256)), dim3(256), 0,
@@ -419,14 +452,30 @@ int zk_r1cs_create(zk_context* ctx, int num_constraints, int num_variables, int 
       memcpy(&val[(size_t)p * 4], v.v, 32);
     }
     c->nnz[k] = nnz;
-    if (hipMalloc(&c->rowptr[k], rowptr.size() * 4) != hipSuccess ||
-        hipMalloc(&c->col[k], std::max<size_t>(nnz, 1) * 4) != hipSuccess ||
+    // segments of at most SPMV_SEG nonzeros per row
+    std::vector<uint32_t> segptr(c->n + 1, 0);
+    std::vector<uint2> seg;
+    for (size_t r = 0; r < c->n; r++) {
+      segptr[r] = (uint32_t)seg.size();
+      for (uint32_t b = rowptr[r]; b < rowptr[r + 1]; b += SPMV_SEG)
+        seg.push_back(make_uint2(b, std::min<uint32_t>(b + SPMV_SEG, rowptr[r + 1])));
+    }
+    segptr[c->n] = (uint32_t)seg.size();
+    c->nseg[k] = seg.size();
+    if (hipMalloc(&c->segptr[k], segptr.size() * 4) != hipSuccess ||
+        hipMalloc(&c->seg[k], std::max<size_t>(seg.size(), 1) * sizeof(uint2)) != hipSuccess ||
+        hipMemcpy(c->segptr[k], segptr.data(), segptr.size() * 4, hipMemcpyHostToDevice) != hipSuccess ||
+        (!seg.empty() && hipMemcpy(c->seg[k], seg.data(), seg.size() * sizeof(uint2), hipMemcpyHostToDevice) !=
+                             hipSuccess)) {
+      st = ctx->fail(ZK_ERR_OOM, "r1cs allocation failed");
+      break;
+    }
+    if (hipMalloc(&c->col[k], std::max<size_t>(nnz, 1) * 4) != hipSuccess ||
         hipMalloc(&c->val[k], std::max<size_t>(nnz, 1) * 32) != hipSuccess) {
       st = ctx->fail(ZK_ERR_OOM, "r1cs allocation failed");
       break;
     }
-    if (hipMemcpy(c->rowptr[k], rowptr.data(), rowptr.size() * 4, hipMemcpyHostToDevice) != hipSuccess ||
-        (nnz && hipMemcpy(c->col[k], col.data(), nnz * 4, hipMemcpyHostToDevice) != hipSuccess) ||
+    if ((nnz && hipMemcpy(c->col[k], col.data(), nnz * 4, hipMemcpyHostToDevice) != hipSuccess) ||
         (nnz && hipMemcpy(c->val[k], val.data(), nnz * 32, hipMemcpyHostToDevice) != hipSuccess))
       st = ctx->fail(ZK_ERR_HIP, "r1cs upload failed");
   }
@@ -441,9 +490,10 @@ int zk_r1cs_create(zk_context* ctx, int num_constraints, int num_variables, int 
 void zk_r1cs_destroy(zk_r1cs* c) {
   if (!c) return;
   for (int k = 0; k < 3; k++) {
-    if (c->rowptr[k]) (void)hipFree(c->rowptr[k]);
     if (c->col[k]) (void)hipFree(c->col[k]);
     if (c->val[k]) (void)hipFree(c->val[k]);
+    if (c->segptr[k]) (void)hipFree(c->segptr[k]);
+    if (c->seg[k]) (void)hipFree(c->seg[k]);
   }
   delete c;
 }

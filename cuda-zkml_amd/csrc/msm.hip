@@ -30,8 +30,10 @@
 //                W*c doublings on the CPU (serial chain: a CPU core beats a
 //                lone wave64 by an order of magnitude on it).
 #include <string.h>
+#include <stdlib.h>
 
 #include <algorithm>
+#include <thread>
 #include <vector>
 
 #include "curve.hpp"
@@ -1020,9 +1022,21 @@ static int msm_run_sets(zk_context* ctx, MsmWorkspace& ws, const BaseSets& sets,
   std::vector<xyzz<F>> parts((size_t)WS);
   ZK_HIP(ctx, hipMemcpyAsync(parts.data(), win, parts.size() * sizeof(xyzz<F>), hipMemcpyDeviceToHost, st));
   ZK_HIP(ctx, hipStreamSynchronize(st));
-  for (int k = 0; k < nsets; k++)
+  // window combination on the host (W * c doublings per set): one thread per set
+  auto finish = [&](int k) {
     host_finish<F>(std::vector<xyzz<F>>(parts.begin() + (size_t)k * W, parts.begin() + (size_t)(k + 1) * W), W, 1,
                    outs[k]);
+  };
+  std::vector<std::thread> helpers;
+  for (int k = 1; k < nsets; k++) {
+    try {
+      helpers.emplace_back(finish, k);
+    } catch (...) {
+      finish(k);  // no thread available
+    }
+  }
+  finish(0);
+  for (auto& t : helpers) t.join();
   return ZK_OK;
 }
 

@@ -97,24 +97,71 @@ __device__ __forceinline__ void lds_put(uint32_t* s, int idx, const fr& x) {
 
 __device__ __forceinline__ uint32_t bitrev(uint32_t x, int bits) { return __brev(x) >> (32 - bits); }
 
-// In-LDS radix-2 DIT over the rows of a (R x T) tile stored row-major
-// (index j*T + c); rows were stored bit-reversed, results come out natural.
-__device__ __forceinline__ void tile_dit(uint32_t* s, int logR, int T, const uint32_t* __restrict__ twr, int twr_count) {
+// Twiddles w_R^t, t < R/2: staged in LDS (plane-major) when R/2 <= NTT_TWL
+// so the stage loop reads no global memory; the single-pass transforms of
+// 2^9 and 2^10 points read the table in place.
+constexpr int NTT_TWL = 128;
+struct TwView {
+  const uint32_t* p;
+  int stride;  // words between planes
+};
+
+__device__ __forceinline__ TwView stage_twiddles(uint32_t* tw, const uint32_t* __restrict__ twr, int half) {
+  if (half > NTT_TWL) return TwView{twr, half};
+  for (int e = threadIdx.x; e < half; e += NTT_THREADS) {
+#pragma unroll
+    for (int l = 0; l < NL; l++) tw[l * NTT_TWL + e] = twr[(size_t)l * half + e];
+  }
+  return TwView{tw, NTT_TWL};
+}
+
+__device__ __forceinline__ fr tw_get(const TwView& tw, int idx) {
+  fr x;
+#pragma unroll
+  for (int l = 0; l < NL; l++) x.l[l] = tw.p[l * tw.stride + idx];
+  return x;
+}
+
+// In-LDS DIT over the rows of a (R x T) tile stored row-major (index j*T + c);
+// rows were stored bit-reversed, results come out natural.  Two radix-2
+// stages per LDS round trip (a radix-2^2 step on four rows held in
+// registers), a single radix-2 stage first when log2 R is odd.  tw: w_R^t,
+// t < R/2, in LDS.
+__device__ __forceinline__ void tile_dit(uint32_t* s, const TwView& tw, int logR, int T) {
   const int R = 1 << logR;
-  const int nbf = (R >> 1) * T;
-  for (int st = 0; st < logR; st++) {
+  int st = 0;
+  if (logR & 1) {  // stage 0: twiddle 1, pairs (2g, 2g + 1)
+    for (int b = threadIdx.x; b < (R >> 1) * T; b += NTT_THREADS) {
+      const int c = b % T, g = b / T;
+      const int i0 = (2 * g) * T + c, i1 = i0 + T;
+      const fr x0 = lds_get(s, i0), x1 = lds_get(s, i1);
+      lds_put(s, i0, fadd(x0, x1));
+      lds_put(s, i1, fsub(x0, x1));
+    }
+    __syncthreads();
+    st = 1;
+  }
+  for (; st < logR; st += 2) {
     const int h = 1 << st;
-    const int tstep = R >> (st + 1);
-    for (int b = threadIdx.x; b < nbf; b += NTT_THREADS) {
+    const int tq = R >> (st + 2);  // twiddle stride of w_{4h} in the w_R table
+    for (int b = threadIdx.x; b < (R >> 2) * T; b += NTT_THREADS) {
       const int c = b % T, q = b / T;
       const int k = q & (h - 1);
-      const int j0 = ((q >> st) << (st + 1)) + k;
-      const int j1 = j0 + h;
-      fr x0 = lds_get(s, j0 * T + c);
-      fr x1 = lds_get(s, j1 * T + c);
-      if (k != 0) x1 = fmul(x1, load_table(twr, twr_count, (size_t)k * tstep));
-      lds_put(s, j0 * T + c, fadd(x0, x1));
-      lds_put(s, j1 * T + c, fsub(x0, x1));
+      const int j0 = ((q >> st) << (st + 2)) + k;
+      const int i0 = j0 * T + c, i1 = i0 + h * T, i2 = i1 + h * T, i3 = i2 + h * T;
+      fr x0 = lds_get(s, i0), x1 = lds_get(s, i1), x2 = lds_get(s, i2), x3 = lds_get(s, i3);
+      if (k != 0) {
+        const fr w2 = tw_get(tw, 2 * k * tq);  // w_{2h}^k
+        x1 = fmul(x1, w2);
+        x3 = fmul(x3, w2);
+      }
+      const fr y0 = fadd(x0, x1), y1 = fsub(x0, x1), y2 = fadd(x2, x3), y3 = fsub(x2, x3);
+      const fr z2 = k != 0 ? fmul(y2, tw_get(tw, k * tq)) : y2;  // w_{4h}^k
+      const fr z3 = fmul(y3, tw_get(tw, (k + h) * tq));           // w_{4h}^(k+h)
+      lds_put(s, i0, fadd(y0, z2));
+      lds_put(s, i2, fsub(y0, z2));
+      lds_put(s, i1, fadd(y1, z3));
+      lds_put(s, i3, fsub(y1, z3));
     }
     __syncthreads();
   }
@@ -139,10 +186,12 @@ __global__ __launch_bounds__(NTT_THREADS) void k_ntt_pass_mid(uint4* __restrict_
                                                                const uint32_t* __restrict__ pre) {
   quotient_priority();
   __shared__ uint32_t s[NL * NTT_TILE];
+  __shared__ uint32_t tws[NL * NTT_TWL];
   const int R = 1 << a.logR, T = a.T;
   const size_t boff = (size_t)blockIdx.y * a.n;
   src += 2 * boff;
   dst += 2 * boff;
+  const TwView tw = stage_twiddles(tws, twr, R >> 1);
   const uint32_t tiles_per_u = a.S / T;
   const size_t u = blockIdx.x / tiles_per_u;
   const uint32_t m0 = (blockIdx.x % tiles_per_u) * T;
@@ -155,7 +204,7 @@ __global__ __launch_bounds__(NTT_THREADS) void k_ntt_pass_mid(uint4* __restrict_
     lds_put(s, bitrev(j, a.logR) * T + c, x);
   }
   __syncthreads();
-  tile_dit(s, a.logR, T, twr, R >> 1);
+  tile_dit(s, tw, a.logR, T);
   const size_t twp_count = (size_t)R * a.S;
   for (int e = threadIdx.x; e < NTT_TILE; e += NTT_THREADS) {
     const int c = e % T, k = e / T;
@@ -177,11 +226,13 @@ __global__ __launch_bounds__(NTT_THREADS) void k_ntt_pass_last(uint4* __restrict
                                                                 int scale_en) {
   quotient_priority();
   __shared__ uint32_t s[NL * NTT_TILE];
+  __shared__ uint32_t tws[NL * NTT_TWL];
   const int R = 1 << a.logR, T = a.T;
   const int E = R * T;
   const size_t boff = (size_t)blockIdx.y * a.n;
   src += 2 * boff;
   dst += 2 * boff;
+  const TwView tw = stage_twiddles(tws, twr, R >> 1);
   const uint32_t tiles_per_v = a.R0 / T;
   const uint32_t v = blockIdx.x / tiles_per_v;     // middle digit k_1 (P == 3) or 0
   const uint32_t k0s = (blockIdx.x % tiles_per_v) * T;
@@ -194,7 +245,7 @@ __global__ __launch_bounds__(NTT_THREADS) void k_ntt_pass_last(uint4* __restrict
     lds_put(s, bitrev(j, a.logR) * T + c, x);
   }
   __syncthreads();
-  tile_dit(s, a.logR, T, twr, R >> 1);
+  tile_dit(s, tw, a.logR, T);
   const size_t kstride = (size_t)a.R0 * a.R1;  // = n / R
   for (int e = threadIdx.x; e < E; e += NTT_THREADS) {
     const int c = e % T, k = e / T;

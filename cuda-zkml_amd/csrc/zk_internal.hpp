@@ -67,7 +67,7 @@ struct zk_context {
   std::map<uint64_t, void*> coset_tables;
   zk::MsmWorkspace* msm_ws = nullptr;
   zk::MsmWorkspace* msm_ws_g2 = nullptr;
-  zk::DevBuf scratch_a, scratch_b, scratch_c;
+  zk::DevBuf scratch_a, scratch_b, scratch_c, scratch_d;
   // fixed-base tables for the generators (device), built on first use
   void* g1_table = nullptr;
   void* g2_table = nullptr;
