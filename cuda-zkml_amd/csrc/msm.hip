@@ -137,6 +137,26 @@ __device__ __forceinline__ void std_to_coord(const uint32_t* e, fq2& a) {
 
 // External points (zk_g1_affine / zk_g2_affine: Montgomery R = 2^256, x = y =
 // 0 for infinity) -> records.
+// Issue priority of the MSM's waves.  Inside a proof several MSMs and the
+// quotient share the GPU.  The accumulation is throughput-bound and always
+// ready to issue; the digit sort and the chunk combine / bucket reduction are
+// short or latency-bound and sit on some MSM's critical path.  Those waves
+// run at priority 2 so that the SIMD arbiter serves them first and the
+// accumulation takes the remaining issue slots (at equal priority a lone
+// chain wave would get a fraction of its SIMD; at lower priority next to an
+// always-ready accumulation it would starve).
+__device__ __forceinline__ void msm_short_priority() { __builtin_amdgcn_s_setprio(2); }
+template <class F>
+__device__ __forceinline__ void msm_priority() {
+  msm_short_priority();
+}
+// The G2 accumulation is the longest throughput phase of a proof and starts
+// its MSM's critical path: priority 1, above the G1 accumulations (0).
+template <class F>
+__device__ __forceinline__ void msm_accumulate_priority() {
+  if constexpr (sizeof(F) == sizeof(fq2)) __builtin_amdgcn_s_setprio(1);
+}
+
 template <class F>
 __global__ void k_msm_convert(uint4* __restrict__ recs, const uint32_t* __restrict__ ext, size_t n) {
   size_t i = blockIdx.x * (size_t)blockDim.x + threadIdx.x;
@@ -171,6 +191,7 @@ __host__ __device__ __forceinline__ int window_width(int w, int W) {
 }
 
 __global__ void k_msm_digits(uint32_t* __restrict__ dig, const uint4* __restrict__ scalars, size_t n, int W) {
+  msm_short_priority();
   size_t i = blockIdx.x * (size_t)blockDim.x + threadIdx.x;
   if (i >= n) return;
   uint4 a = scalars[2 * i], b = scalars[2 * i + 1];
@@ -230,6 +251,7 @@ __global__ void k_msm_digits(uint32_t* __restrict__ dig, const uint4* __restrict
 template <int BMAX>
 __global__ __launch_bounds__(SORT_T) void k_msm_hist(const uint32_t* __restrict__ dig, size_t n, uint32_t slice,
                                                      uint32_t S, uint32_t B, uint32_t* __restrict__ H) {
+  msm_short_priority();
   __shared__ uint32_t h[BMAX];
   const uint32_t s = blockIdx.x, w = blockIdx.y, t = threadIdx.x;
   for (uint32_t i = t; i < B; i += SORT_T) h[i] = 0;
@@ -262,6 +284,7 @@ __global__ __launch_bounds__(SORT_T) void k_msm_hist(const uint32_t* __restrict_
 __global__ __launch_bounds__(SCAN_T) void k_msm_colscan(uint32_t* __restrict__ H, uint32_t S, uint32_t B,
                                                         uint32_t* __restrict__ tot, uint32_t* __restrict__ lex,
                                                         uint32_t* __restrict__ bsum, uint32_t* __restrict__ bmax) {
+  msm_short_priority();
   __shared__ uint32_t wsum[SCAN_T / 64], wmx[SCAN_T / 64];
   const uint32_t t = threadIdx.x, lane = t & 63, wv = t >> 6;
   const uint32_t k = blockIdx.x * SCAN_T + t;
@@ -309,6 +332,7 @@ __global__ __launch_bounds__(SCAN_T) void k_msm_colscan(uint32_t* __restrict__ H
 __global__ __launch_bounds__(256) void k_msm_bscan(const uint32_t* __restrict__ bsum, const uint32_t* __restrict__ bmax,
                                                    uint32_t nb, uint32_t* __restrict__ boff,
                                                    uint32_t* __restrict__ wstat) {
+  msm_short_priority();
   __shared__ uint32_t wsum[4], wmx[4];
   const uint32_t w = blockIdx.x, t = threadIdx.x, lane = t & 63, wv = t >> 6;
   const uint32_t v = t < nb ? bsum[w * nb + t] : 0u;
@@ -347,6 +371,7 @@ __global__ __launch_bounds__(SORT_T) void k_msm_scatter(const uint32_t* __restri
                                                         const uint32_t* __restrict__ tot,
                                                         uint32_t* __restrict__ start, uint32_t* __restrict__ end,
                                                         uint2* __restrict__ out) {
+  msm_short_priority();
   __shared__ uint32_t cur[BMAX];
   const uint32_t s = blockIdx.x, w = blockIdx.y, t = threadIdx.x;
   const uint32_t* hp = H + ((size_t)w * S + s) * B;
@@ -398,6 +423,7 @@ __global__ __launch_bounds__(SORT_T) void k_msm_scatter_coarse(const uint32_t* _
                                                                const uint32_t* __restrict__ tot,
                                                                uint32_t* __restrict__ start,
                                                                uint32_t* __restrict__ end, uint2* __restrict__ tmp) {
+  msm_short_priority();
   __shared__ uint32_t cur[MSM_NCB];
   const uint32_t s = blockIdx.x, w = blockIdx.y, t = threadIdx.x;
   const uint32_t* hp = H + ((size_t)w * S + s) * B;
@@ -442,6 +468,7 @@ __global__ __launch_bounds__(SORT_T) void k_msm_scatter_coarse(const uint32_t* _
 __global__ __launch_bounds__(PLACE_T) void k_msm_place(const uint2* __restrict__ tmp, uint32_t B, uint32_t BPC,
                                                        const uint32_t* __restrict__ start,
                                                        const uint32_t* __restrict__ end, uint2* __restrict__ out) {
+  msm_short_priority();
   __shared__ uint32_t cur[MSM_BPC_MAX];
   const uint32_t cb = blockIdx.x, w = blockIdx.y, t = threadIdx.x;
   const uint32_t k0 = w * B + cb * BPC;
@@ -466,15 +493,6 @@ __global__ __launch_bounds__(PLACE_T) void k_msm_place(const uint2* __restrict__
 }
 
 // ------------------------------------------------------------------ accumulate
-// Issue priority of the MSM's waves.  Inside a proof the G2 MSM is the
-// critical path while four G1 MSMs run beside it on other streams; raising
-// its waves' priority lets the SIMD arbiter serve its latency-bound chains
-// (combine, bucket reduction) first and hand the remaining issue slots to the
-// G1 work, instead of splitting them evenly.
-template <class F>
-__device__ __forceinline__ void msm_priority() {
-  if constexpr (sizeof(F) == sizeof(fq2)) __builtin_amdgcn_s_setprio(2);
-}
 
 // Chunk partials of buckets that span chunks; base set s uses the slots
 // [s * nchunks, (s + 1) * nchunks).
@@ -510,7 +528,7 @@ __global__ __launch_bounds__(256) void k_msm_accumulate(const uint2* __restrict_
                                                         uint32_t chunks_per_window, uint32_t n_pad, uint32_t L0,
                                                         size_t nbuckets, xyzz<F>* __restrict__ buckets,
                                                         ChunkSlots<F> all_slots) {
-  msm_priority<F>();
+  msm_accumulate_priority<F>();
   const uint32_t ch = blockIdx.x * blockDim.x + threadIdx.x;
   if (ch >= nchunks) return;
   const uint32_t set = blockIdx.y;
