@@ -11,15 +11,20 @@ full Groth16 proves, each checked by the product's verifier:
   prove_config1         config 1's quantized MLP statement (domain 2^13)
   prove_2_16_synthetic  a uniform-witness config-5-shaped R1CS, domain 2^16
   prove_2_22_config5    config 5 at its full 2^22 constraints
-the 2^22 NTT of config 2, and the CPU oracle's restatement of the reference
-MSM on the host cores (cpu_baseline).  Prints one JSON line.
+the 2^22 NTT of config 2, the G1 MSM at config 3's other sizes and with its
+witness-like scalars, the G2 MSM of a 2^16 prove, and the CPU oracle's
+restatement of the reference algorithms (MSM, NTT, prove) on the host cores,
+on one thread and on all the process may use (cpu_baseline), each output
+compared with the GPU's.  Prints one JSON line.
 
     python bench.py [--gpus 1] [--steps K] [--warmup W]
 """
 import argparse
 import json
 import os
+import shutil
 import sys
+import tempfile
 import time
 
 import numpy as np
@@ -48,6 +53,40 @@ def msm_algorithmic_mults(n, c):
 
 def best_c(n):
     return min(range(8, 22), key=lambda c: msm_algorithmic_mults(n, c))
+
+
+def host_cpu():
+    """What the process runs on: logical CPUs it may use, the machine's
+    logical CPU and socket counts and the CPU model (from /proc/cpuinfo)."""
+    info = {"usable_cpus": len(os.sched_getaffinity(0)), "omp_num_threads": os.environ.get("OMP_NUM_THREADS")}
+    try:
+        txt = open("/proc/cpuinfo").read()
+        info["logical_cpus"] = txt.count("processor\t:")
+        info["sockets"] = len({l.split(":")[1].strip() for l in txt.splitlines() if l.startswith("physical id")})
+        info["model"] = next((l.split(":", 1)[1].strip() for l in txt.splitlines() if l.startswith("model name")), None)
+    except OSError:
+        pass
+    return info
+
+
+def mont_words(vals):
+    """v 2^256 mod r for Python ints v, as (k, 4) uint64 words (Montgomery form)."""
+    b = b"".join(((v << 256) % R_ORDER).to_bytes(32, "little") for v in vals)
+    return np.frombuffer(b, dtype=np.uint64).reshape(-1, 4).copy()
+
+
+def witness_like_scalars(n, rng, uniform):
+    """BASELINE config 3 (ii): 70% in [0, 2^16), 10% r - [1, 2^16), 20%
+    uniform, in Montgomery form (uniform words below r are valid as they are)."""
+    small = mont_words(range(1 << 16))
+    neg = mont_words([R_ORDER - v for v in range(1 << 16)])
+    s = uniform.copy()
+    u = rng.random(n)
+    m = u < 0.7
+    s[m] = small[rng.integers(0, 1 << 16, size=int(m.sum()))]
+    m = (u >= 0.7) & (u < 0.8)
+    s[m] = neg[rng.integers(1, 1 << 16, size=int(m.sum()))]
+    return s
 
 
 def main():
@@ -94,7 +133,9 @@ def main():
     for _ in range(args.warmup):
         res = ctx.msm_g1(dp, ds, n)
     ctx.sync()
-    ctx.set_profiling(True)
+    # timed region: HIP events bracket only the dominant kernel (each timed
+    # launch adds two event records to the stream)
+    ctx.set_profiling(True, only="msm_accumulate")
     ctx.reset_kernel_stats()
     t0 = time.perf_counter()
     for _ in range(args.steps):
@@ -102,10 +143,19 @@ def main():
     ctx.sync()
     t1 = time.perf_counter()
     ms_step = (t1 - t0) * 1e3 / args.steps
+    cnt, ms = ctx.kernel_stats("msm_accumulate")
+    acc_stat = {"ms_per_step": ms / args.steps, "launches_per_step": cnt / args.steps}
+    # per-kernel breakdown from a separate, untimed pass with every kernel bracketed
+    prof_steps = 5
+    ctx.set_profiling(True)
+    ctx.reset_kernel_stats()
+    for _ in range(prof_steps):
+        ctx.msm_g1(dp, ds, n)
+    ctx.sync()
     kernels = {}
     for name in ctx.kernel_names():
         cnt, ms = ctx.kernel_stats(name)
-        kernels[name] = {"ms_per_step": ms / args.steps, "launches_per_step": cnt / args.steps}
+        kernels[name] = {"ms_per_step": ms / prof_steps, "launches_per_step": cnt / prof_steps}
     ctx.set_profiling(False)
     mpoints = n / (ms_step * 1e-3) / 1e6
     log(f"[bench] MSM 2^{args.log_n}: {ms_step:.3f} ms/step, {mpoints:.1f} Mpoints/s")
@@ -113,20 +163,65 @@ def main():
     # roofline of the dominant kernel (bucket accumulation): every sorted
     # (window, point) entry costs one mixed XYZZ addition = 10 field mults.
     c, windows = zkml_amd.Context.msm_config(n)
-    acc = kernels.get("msm_accumulate", {"ms_per_step": float("nan"), "launches_per_step": 1})
-    acc_ms = acc["ms_per_step"] / max(acc["launches_per_step"], 1)
+    acc_ms = acc_stat["ms_per_step"] / max(acc_stat["launches_per_step"], 1)
     acc_mads = n * windows * 10 * MADS_PER_FIELD_MUL
     achieved = acc_mads / (acc_ms * 1e-3) / 1e12
     # HBM bytes per launch of the same kernel, from the committed rocprofv3
     # FETCH_SIZE / WRITE_SIZE runs (profiles/msm_2e20_pmc_traffic.md), scaled by
     # the counters' reading for a plain copy of known size
-    traffic = None
+    traffic = pmc = None
     tpath = os.path.join(ROOT, "profiles", "msm_2e20_pmc_traffic.json")
     if args.log_n == 20 and os.path.exists(tpath):
-        traffic = json.load(open(tpath)).get("msm_accumulate_bytes_per_launch")
+        prof = json.load(open(tpath))
+        traffic = prof.get("msm_accumulate_bytes_per_launch")
+        # issue counters of the same kernel from the committed rocprofv3 run
+        # (a separate process: counters are not collected here)
+        pmc = {k_: prof.get(k_) for k_ in ("sq_insts_valu_per_launch", "sq_active_inst_valu_per_launch", "valu_busy",
+                                            "clock_ghz", "lane_instructions_per_mixed_add")}
+        pmc["source"] = "profiles/msm_2e20_pmc_traffic.md"
     # whole-MSM VALU fraction with BASELINE.md's algorithmic count
     f_mults = msm_algorithmic_mults(n, best_c(n))
     msm_frac = f_mults * MADS_PER_FIELD_MUL / (ms_step * 1e-3) / 1e12 / PEAK_MAD_TOPS
+
+    # ---------------- G1 MSM at config 3's other sizes and scalar mix, G2 at 2^16
+    def time_msm(fn, d_pts, d_sc, count, reps):
+        fn(d_pts, d_sc, count)
+        ctx.sync()
+        t0 = time.perf_counter()
+        for _ in range(reps):
+            fn(d_pts, d_sc, count)
+        ctx.sync()
+        return (time.perf_counter() - t0) * 1e3 / reps
+
+    def msm_entry(ms, count, g2=False):
+        mults = msm_algorithmic_mults(count, best_c(count)) * (3 if g2 else 1)  # Fp2 mult = 3 Fp mults
+        return {"ms": round(ms, 4), "Mpoints_per_s": round(count / (ms * 1e-3) / 1e6, 2),
+                "field_mults_per_s": float(f"{mults / (ms * 1e-3):.4g}"),
+                "valu_frac": round(mults * MADS_PER_FIELD_MUL / (ms * 1e-3) / 1e12 / PEAK_MAD_TOPS, 4)}
+
+    msm_more = {}
+    sk = witness_like_scalars(n, rng, s)
+    d_sk = ctx.upload(sk)
+    msm_more[f"g1_2_{args.log_n}_witness_like"] = msm_entry(time_msm(ctx.msm_g1, dp, d_sk, n, 10), n)
+    del d_sk
+    for ln_ in (16, 18):
+        msm_more[f"g1_2_{ln_}"] = msm_entry(time_msm(ctx.msm_g1, dp, ds, 1 << ln_, 20), 1 << ln_)
+    n22 = 1 << 22
+    k22 = zkml_amd.random_fr(n22, rng)
+    d_k22 = ctx.upload(k22)
+    dp22 = ctx.alloc(n22 * 64)
+    ctx.g1_generator_mul(d_k22, n22, dp22)
+    ds22 = ctx.upload(zkml_amd.random_fr(n22, rng))
+    msm_more["g1_2_22"] = msm_entry(time_msm(ctx.msm_g1, dp22, ds22, n22, 5), n22)
+    del d_k22, dp22, ds22, k22
+    n16 = 1 << 16
+    d_k2 = ctx.upload(k[:n16].copy())
+    dp2 = ctx.alloc(n16 * 128)
+    ctx.g2_generator_mul(d_k2, n16, dp2)
+    msm_more["g2_2_16"] = msm_entry(time_msm(ctx.msm_g2, dp2, ds, n16, 20), n16, g2=True)
+    del d_k2, dp2
+    for key, v in msm_more.items():
+        log(f"[bench] MSM {key}: {v['ms']:.3f} ms, {v['Mpoints_per_s']} Mpoints/s")
 
     # ---------------- NTT 2^22 (config 2)
     ntt = {}
@@ -136,7 +231,7 @@ def main():
     do = ctx.alloc((1 << ln) * 32)
     ctx.ntt(do, da, ln)
     ctx.sync()
-    ctx.set_profiling(True)
+    ctx.set_profiling(True, only="ntt_pass")
     ctx.reset_kernel_stats()
     reps = 10
     t0 = time.perf_counter()
@@ -152,27 +247,35 @@ def main():
            "hbm_frac": round(64 * (1 << ln) / (kms * 1e-3) / 1e9 / PEAK_HBM_GBS, 4),
            "valu_frac": round(((1 << ln) // 2 * ln) * MADS_PER_FIELD_MUL / (kms * 1e-3) / 1e12 / PEAK_MAD_TOPS, 4)}
     log(f"[bench] NTT 2^22: {kms:.3f} ms")
+    ntt_out = ctx.d2h(do, (1 << ln, 4))
     del da, do
 
     # ---------------- full prove at 2^16
     prove = prove_syn = prove22 = prove_c1 = None
+    work = tempfile.TemporaryDirectory()
+    kept = {}  # config 4: statement, PK path and GPU proof, for the CPU prove
     if not args.no_prove:
-        import tempfile
         from statements import load as load_statement
 
-        def prove_case(stmt, reps, label):
+        def prove_case(stmt, reps, label, keep=False):
             """GPU setup, then `reps` proves of a statement (nc, nv, npub, A, B, C,
             w) with the witness handed over from host memory; the proof is
-            checked with the product's verifier."""
+            checked with the product's verifier.  Loading the PK (file read and
+            upload) is timed on its own, outside the proves."""
             nc, nv, npub, A, B, C, w = stmt
             log(f"[bench] {label}: {nc} constraints, GPU setup")
             r = ctx.r1cs(nc, nv, npub, A, B, C)
-            with tempfile.TemporaryDirectory() as td:
-                t0 = time.perf_counter()
-                ctx.setup(r, 0xDEADBEEF42, os.path.join(td, "pk.bin"), os.path.join(td, "vk.bin"))
-                t_setup = time.perf_counter() - t0
-                pk = ctx.load_pk(os.path.join(td, "pk.bin"))
-                vk_bytes = open(os.path.join(td, "vk.bin"), "rb").read()
+            td = tempfile.mkdtemp(dir=work.name)
+            pk_path = os.path.join(td, "pk.bin")
+            t0 = time.perf_counter()
+            ctx.setup(r, 0xDEADBEEF42, pk_path, os.path.join(td, "vk.bin"))
+            t_setup = time.perf_counter() - t0
+            t0 = time.perf_counter()
+            pk = ctx.load_pk(pk_path)
+            t_load = time.perf_counter() - t0
+            vk_bytes = open(os.path.join(td, "vk.bin"), "rb").read()
+            if not keep:
+                shutil.rmtree(td)
             ctx.prove(pk, r, w, npub, 0xCAFEBABE)  # warm-up (workspaces, plans)
             times, parts, proof = [], None, None
             for _ in range(reps):
@@ -186,9 +289,12 @@ def main():
                 pub[i] = [(x >> (64 * k)) & (2**64 - 1) for k in range(4)]
             ok = zkml_amd.verify(vk_bytes, proof, pub)
             out = {"constraints": nc, "variables": nv, "public": npub, "domain": 1 << r.log_n,
-                   "ms": round(float(np.median(times)), 3), "setup_s": round(t_setup, 2), "proof_verifies": ok,
+                   "ms": round(float(np.median(times)), 3), "min_ms": round(float(np.min(times)), 3),
+                   "setup_s": round(t_setup, 2), "pk_load_s": round(t_load, 3), "proof_verifies": ok,
                    "breakdown_ms": {k_: round(v, 3) for k_, v in parts.items()}}
             log(f"[bench] {label}: {out['ms']:.3f} ms (median of {reps}), setup {t_setup:.1f} s, verifies: {ok}")
+            if keep:
+                kept.update(stmt=stmt, pk_path=pk_path, proof=proof)
             pk.close()
             r.close()
             return out
@@ -198,31 +304,69 @@ def main():
             return nc, w.shape[0], 4, A, B, C, w
 
         def fixture(name):
-            nc, nv, npub, _npriv, A, B, C, w = load_statement(name)
+            nc, nv, npub, npriv, A, B, C, w = load_statement(name)
+            if name == "config4":
+                kept["npriv"] = npriv
             return nc, nv, npub, A, B, C, w
 
-        prove = prove_case(fixture("config4"), 7, "prove config 4 (2^16)")
+        prove = prove_case(fixture("config4"), 7, "prove config 4 (2^16)", keep=True)
         prove_c1 = prove_case(fixture("config1"), 7, "prove config 1 (2^13)")
         prove_syn = prove_case(synthetic((1 << 16) - 64, 16), 5, "prove 2^16 synthetic")
         prove22 = prove_case(synthetic(1 << 22, 22), 3, "prove 2^22 (config 5)")
 
     # ---------------- CPU baseline (oracle restatement of the reference MSM)
+    # On one thread (the reference's host code) and on every thread OpenMP may
+    # use (windows, butterflies and rows in parallel); each output is compared
+    # with the GPU's for the same input.
     cpu = None
     if not args.no_cpu:
-        from bindings import oracle, ptr
+        from bindings import OracleR1CS, oracle, ptr
         lib = oracle()
-        sample = 1 << 18
-        pts = ctx.d2h(dp, (n, 8))[:sample].copy()
-        sc = np.ascontiguousarray(s[:sample])
-        out = np.zeros(8, dtype=np.uint64)
-        threads = 1
-        t0 = time.perf_counter()
-        lib.orc_msm_g1(ptr(pts), ptr(sc), sample, 0, threads, ptr(out))
-        dt = time.perf_counter() - t0
-        cpu = {"value": round(sample / dt / 1e6, 4), "unit": "Mpoints/s", "cores": threads, "kind": "port",
-               "sample": f"G1 MSM over the first 2^18 of the same points/scalars, reference Pippenger "
-                         f"(MSMConfig windows, Jacobian mixed adds, serial running sums), {dt:.2f} s"}
-        log(f"[bench] CPU baseline: {cpu['value']} Mpoints/s ({dt:.2f} s)")
+        all_threads = int(lib.orc_threads_max())
+        pts = ctx.d2h(dp, (n, 8))
+        sc = np.ascontiguousarray(s)
+        msm_cpu = {}
+        for threads in sorted({1, all_threads}):
+            out = np.zeros(8, dtype=np.uint64)
+            t0 = time.perf_counter()
+            lib.orc_msm_g1(ptr(pts), ptr(sc), n, 0, threads, ptr(out))
+            dt = time.perf_counter() - t0
+            msm_cpu[threads] = {"s": round(dt, 3), "Mpoints_per_s": round(n / dt / 1e6, 4),
+                                "equals_gpu": bool(np.array_equal(out, res))}
+            log(f"[bench] CPU MSM 2^{args.log_n}, {threads} threads: {dt:.2f} s, equals GPU: "
+                f"{msm_cpu[threads]['equals_gpu']}")
+        del pts
+        ntt_cpu = {}
+        for threads in sorted({1, all_threads}):
+            b = np.ascontiguousarray(a.copy())
+            t0 = time.perf_counter()
+            lib.orc_ntt(ptr(b), ln, 0, threads)
+            dt = time.perf_counter() - t0
+            ntt_cpu[threads] = {"ms": round(dt * 1e3, 1), "equals_gpu": bool(np.array_equal(b, ntt_out))}
+            log(f"[bench] CPU NTT 2^{ln}, {threads} threads: {dt * 1e3:.0f} ms")
+        prove_cpu = None
+        if kept:
+            nc, nv, npub, A, B, C, w = kept["stmt"]
+            oc = OracleR1CS(nc, nv, npub, kept["npriv"], [(M["row"], M["col"], M["value"]) for M in (A, B, C)])
+            prove_cpu = {}
+            for threads in sorted({1, all_threads}):
+                t0 = time.perf_counter()
+                rc, proof_o, _ = oc.prove(kept["pk_path"], w, 0xCAFEBABE, threads=threads)
+                dt = time.perf_counter() - t0
+                prove_cpu[threads] = {"ms": round(dt * 1e3, 1), "equals_gpu": rc == 0 and proof_o == kept["proof"]}
+                log(f"[bench] CPU prove config 4, {threads} threads: {dt * 1e3:.0f} ms, equals GPU: "
+                    f"{prove_cpu[threads]['equals_gpu']}")
+        top = msm_cpu[all_threads]
+        cpu = {"value": top["Mpoints_per_s"], "unit": "Mpoints/s", "cores": all_threads, "kind": "port",
+               "sample": f"G1 MSM over the same 2^{args.log_n} points/scalars, reference Pippenger (MSMConfig "
+                         f"windows, Jacobian mixed adds, serial running sums; one window per OpenMP thread), "
+                         f"{top['s']} s on {all_threads} threads",
+               "single_thread": msm_cpu[1], "all_threads": top,
+               "ntt_2_22_ms": {"1": ntt_cpu[1], str(all_threads): ntt_cpu[all_threads]},
+               "prove_2_16_ms": None if prove_cpu is None else {"1": prove_cpu[1],
+                                                                str(all_threads): prove_cpu[all_threads]},
+               "host": host_cpu()}
+    work.cleanup()
 
     line = {
         "metric": "Groth16 prove ms at 2^16 constraints; G1 MSM Mpoints/s at 2^20",
@@ -243,6 +387,10 @@ def main():
                      "unit": "T mad32/s", "frac": round(achieved / PEAK_MAD_TOPS, 4), "traffic": traffic,
                      "kernel": "msm_accumulate", "kernel_ms": round(acc_ms, 4)},
         "msm_valu_frac_whole": round(msm_frac, 4),
+        "field_mults_per_s": float(f"{f_mults / (ms_step * 1e-3):.4g}"),
+        "field_mults_per_step": f_mults,
+        "pmc_msm_accumulate": pmc,
+        "msm_more": msm_more,
         "kernels_ms_per_step": {k_: round(v["ms_per_step"], 4) for k_, v in kernels.items()},
         "prove_2_16": prove,
         "prove_2_16_synthetic": prove_syn,

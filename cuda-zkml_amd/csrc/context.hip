@@ -23,7 +23,7 @@ int zk_context::ensure(DevBuf& b, size_t bytes) {
 
 zk::TimingToken zk_context::tic(const char* name, hipStream_t st) {
   zk::TimingToken t;
-  if (!profiling) return t;
+  if (!profiling || (!profile_only.empty() && profile_only != name)) return t;
   t.name = name;
   (void)hipEventCreate(&t.a);
   (void)hipEventCreate(&t.b);
@@ -162,6 +162,13 @@ int zk_set_profiling(zk_context* ctx, int enable) {
   if (!ctx) return ZK_ERR_INVALID;
   ctx->collect();
   ctx->profiling = enable != 0;
+  return ZK_OK;
+}
+
+int zk_set_profiling_only(zk_context* ctx, const char* kernel) {
+  if (!ctx) return ZK_ERR_INVALID;
+  ctx->collect();
+  ctx->profile_only = kernel ? kernel : "";
   return ZK_OK;
 }
 

@@ -646,6 +646,22 @@ int zk_prove(zk_context* ctx, const zk_pk* pk, const zk_r1cs* c, const void* h_w
   // Job slots (timings): 0 A, 1 B2, 2 L, 3 H, 4 B1; A, L and B1 share one run.
   constexpr int JOB_G1 = 0, JOB_B2 = 1, JOB_H = 3;
   int rc_g1 = ZK_OK, rc_b2 = ZK_OK, rc_h = ZK_OK;
+  // Assembly (groth16.cu:769-840): A = alpha1 + A_msm + r delta1,
+  // B = beta2 + B2_msm + s delta2, C = L + H + s A + r (beta1 + B1_msm), the
+  // last term only when B1 is not empty.  Split by what each part waits for:
+  // pre_a = alpha1 + r delta1, pre_b = beta2 + s delta2 and
+  // pre_c = s pre_a + r beta1 need no MSM and are computed on a host thread
+  // while the GPU works; g1_tail = s A_msm + L + r B1_msm as soon as the G1
+  // job returns; what is left after the last MSM is three additions and the
+  // affine conversions.
+  G1 pre_a = G1::inf(), pre_c = G1::inf(), g1_tail = G1::inf();
+  G2 pre_b = G2::inf();
+  auto precompute = [&] {
+    pre_a = g1_from_words(pk->alpha1).add(g1_from_words(pk->delta1).mul(r));
+    pre_b = g2_from_words(pk->beta2).add(g2_from_words(pk->delta2).mul(s));
+    pre_c = pre_a.mul(s);
+    if (nb1 > 0) pre_c = pre_c.add(g1_from_words(pk->beta1).mul(r));
+  };
   auto record = [&](int slot, hipStream_t s, int& rc) {
     if (hipEventRecord(ev[slot], s) != hipSuccess && rc == ZK_OK) rc = ctx->fail(ZK_ERR_HIP, "prove: event record");
   };
@@ -676,10 +692,15 @@ int zk_prove(zk_context* ctx, const zk_pk* pk, const zk_r1cs* c, const void* h_w
     add(pk->L, 1 + (size_t)pk->npub, npriv_l > 0 ? (size_t)npriv_l : 0, l_msm);
     if (rc_g1 == ZK_OK && ns) rc_g1 = msm_g1_sets_ws(ctx, ctx->job_ws[JOB_G1], ns, recs, lo, cnt, d_w, m, outs, js);
     record(5 + 2 * JOB_G1, js, rc_g1);
+    if (rc_g1 == ZK_OK) {
+      g1_tail = g1_from_words(a_msm).mul(s).add(g1_from_words(l_msm));
+      if (nb1 > 0) g1_tail = g1_tail.add(g1_from_words(b1_msm).mul(r));
+    }
   };
   for (int j = 0; j < JOB_STREAMS; j++) ZK_HIP(ctx, hipStreamWaitEvent(ctx->job_stream[j], ev[1], 0));
   std::vector<std::thread> workers;
-  for (const std::function<void()>& fn : {std::function<void()>(run_b2), std::function<void()>(run_g1)}) {
+  for (const std::function<void()>& fn :
+       {std::function<void()>(run_b2), std::function<void()>(run_g1), std::function<void()>(precompute)}) {
     try {
       workers.emplace_back(fn);
     } catch (...) {
@@ -711,19 +732,14 @@ int zk_prove(zk_context* ctx, const zk_pk* pk, const zk_r1cs* c, const void* h_w
   ZK_TRY(rc_b2);
   ZK_TRY(rc_g1);
   ZK_TRY(rc_h);
-  // host assembly (groth16.cu:769-840): C = L + H + s A + r (beta1 + B1)
-  G1 A = g1_from_words(pk->alpha1).add(na > 0 ? g1_from_words(a_msm) : G1::inf());
-  A = A.add(g1_from_words(pk->delta1).mul(r));
-  G2 B = g2_from_words(pk->beta2).add(nb2 > 0 ? g2_from_words(b2_msm) : G2::inf());
-  B = B.add(g2_from_words(pk->delta2).mul(s));
+  // the rest of the assembly; an empty A, L, H or B1 set left its result at
+  // the identity (all-zero words)
+  const G1 A = pre_a.add(g1_from_words(a_msm));
+  const G2 B = pre_b.add(nb2 > 0 ? g2_from_words(b2_msm) : G2::inf());
+  const G1 Cj = g1_tail.add(g1_from_words(h_msm)).add(pre_c);
   uint64_t Aw[8], Bw[16], Cw[8];
   g1_to_words(A, Aw);
   g2_to_words(B, Bw);
-  G1 Cj = G1::inf();
-  if (npriv_l > 0) Cj = Cj.add(g1_from_words(l_msm));
-  if (nh > 0) Cj = Cj.add(g1_from_words(h_msm));
-  Cj = Cj.add(g1_from_words(Aw).mul(s));
-  if (nb1 > 0) Cj = Cj.add(g1_from_words(pk->beta1).add(g1_from_words(b1_msm)).mul(r));
   g1_to_words(Cj, Cw);
   // 256-byte serialization in standard form (groth16.cu:1058-1074)
   uint8_t* o = proof_out;

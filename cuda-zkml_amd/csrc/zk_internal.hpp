@@ -77,6 +77,7 @@ struct zk_context {
   uint32_t* h_flag = nullptr;  // pinned word: the proof's witness-check count
   // profiling
   bool profiling = false;
+  std::string profile_only;  // when set, only kernels of this name are timed
   std::map<std::string, zk::KernelStat> stats;
   std::vector<zk::PendingTiming> pending;
   std::string stat_names;

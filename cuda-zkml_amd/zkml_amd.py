@@ -60,6 +60,7 @@ def lib():
         for f in ("zk_memcpy_h2d", "zk_memcpy_d2h", "zk_memcpy_d2d"):
             getattr(L, f).argtypes = [vp, vp, vp, ctypes.c_size_t]
         L.zk_set_profiling.argtypes = [vp, ctypes.c_int]
+        L.zk_set_profiling_only.argtypes = [vp, ctypes.c_char_p]
         L.zk_kernel_stats.argtypes = [vp, ctypes.c_char_p, ctypes.POINTER(ctypes.c_uint64),
                                       ctypes.POINTER(ctypes.c_double)]
         L.zk_reset_kernel_stats.argtypes = [vp]
@@ -233,7 +234,9 @@ class Context:
         self._check(lib().zk_synchronize(self.h), "synchronize")
 
     # ---- profiling
-    def set_profiling(self, on):
+    def set_profiling(self, on, only=None):
+        """Per-kernel HIP-event timing; `only` restricts it to one kernel name."""
+        self._check(lib().zk_set_profiling_only(self.h, only.encode() if only else None))
         self._check(lib().zk_set_profiling(self.h, 1 if on else 0))
 
     def kernel_stats(self, name):

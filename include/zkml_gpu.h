@@ -71,6 +71,10 @@ int zk_memcpy_d2d(zk_context* ctx, void* d_dst, const void* d_src, size_t bytes)
 /* Per-kernel timing with HIP events recorded on the stream each kernel is
  * launched on (off by default).  Names: see zk_kernel_stats_names(). */
 int zk_set_profiling(zk_context* ctx, int enable);
+/* Time only the kernels of this name (NULL or "": all).  Each timed launch
+ * adds two event records to its stream, so a throughput run times just the
+ * kernel it reports. */
+int zk_set_profiling_only(zk_context* ctx, const char* kernel);
 int zk_kernel_stats(zk_context* ctx, const char* kernel, uint64_t* launches, double* total_ms);
 int zk_reset_kernel_stats(zk_context* ctx);
 const char* zk_kernel_stats_names(zk_context* ctx);
