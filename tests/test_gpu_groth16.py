@@ -154,3 +154,42 @@ def test_prove_2_16_matches_oracle(ctx, tmp_path):
         pub = tmp_path / "pub.bin"
         write_public(pub, circ.public())
         assert ref().ref_verify_files(str(vk_path).encode(), str(pf).encode(), str(pub).encode()) == 1
+
+
+def test_prove_2_22_config5_verifies(ctx, tmp_path):
+    """BASELINE config 5 at its full 2^22 constraints (3 nonzeros per A and B
+    row, C the fresh product variable).  The oracle's CPU prove is too slow at
+    this size, so the pins are size-independent: the proof is accepted by the
+    product's verifier and by the reference's own (oracle/_ref), a changed
+    public input is rejected, and a second prove with the same seed gives the
+    same bytes."""
+    import zkml_amd
+    nc, npub = 1 << 22, 4
+    A, B, C, w = zkml_amd.synthetic_r1cs(nc, npub, 16, 22)
+    r = ctx.r1cs(nc, w.shape[0], npub, A, B, C)
+    del A, B, C
+    assert r.log_n == 22
+    pk_path, vk_path = tmp_path / "pk.bin", tmp_path / "vk.bin"
+    print("[prove 2^22] setup", flush=True)
+    ctx.setup(r, SETUP_SEED, pk_path, vk_path)
+    pk = ctx.load_pk(pk_path)
+    os.remove(pk_path)
+    print("[prove 2^22] prove", flush=True)
+    proof, _ = ctx.prove(pk, r, w, npub, PROVE_SEED)
+    again, _ = ctx.prove(pk, r, w, npub, PROVE_SEED)
+    assert proof == again
+    pub = [Z.from_mont(Z.from_limbs([int(x) for x in w[1 + i]]), Z.R) for i in range(npub)]
+    pub_words = np.array([Z.limbs(v) for v in pub], dtype=np.uint64)
+    vk = vk_path.read_bytes()
+    assert zkml_amd.verify(vk, proof, pub_words)
+    bad = pub_words.copy()
+    bad[0, 0] ^= 1
+    assert not zkml_amd.verify(vk, proof, bad)
+    if ref_available():
+        pf = tmp_path / "proof.bin"
+        pf.write_bytes(proof)
+        pubf = tmp_path / "pub.bin"
+        write_public(pubf, pub)
+        assert ref().ref_verify_files(str(vk_path).encode(), str(pf).encode(), str(pubf).encode()) == 1
+    pk.close()
+    r.close()

@@ -201,6 +201,68 @@ def test_msm_g1_closed_form_large(ctx, log_n, dist):
     assert np.array_equal(again, got)
 
 
+def add_mod_r(a, b):
+    """(a + b) mod r on (n, 4) uint64 words below r, vectorized.  Montgomery
+    forms add like the values they stand for."""
+    import zkml_amd
+    s = np.empty_like(a)
+    carry = np.zeros(a.shape[0], dtype=np.uint64)
+    for k in range(4):
+        t = a[:, k] + b[:, k]
+        c1 = t < a[:, k]
+        t2 = t + carry
+        s[:, k] = t2
+        carry = (c1 | (t2 < t)).astype(np.uint64)
+    assert not carry.any()  # a + b < 2r < 2^256
+    r = zkml_amd.R_WORDS
+    ge = np.ones(a.shape[0], dtype=bool)  # s >= r, decided from the top word down
+    decided = np.zeros(a.shape[0], dtype=bool)
+    for k in range(3, -1, -1):
+        gt, lt = s[:, k] > r[k], s[:, k] < r[k]
+        ge = np.where(~decided & gt, True, np.where(~decided & lt, False, ge))
+        decided |= gt | lt
+    borrow = np.zeros(a.shape[0], dtype=np.uint64)
+    out = s.copy()
+    for k in range(4):
+        t = s[:, k] - r[k]
+        b1 = s[:, k] < r[k]
+        t2 = t - borrow
+        out[:, k] = t2
+        borrow = (b1 | (t < borrow)).astype(np.uint64)
+    return np.where(ge[:, None], out, s)
+
+
+def test_add_mod_r_helper():
+    rng = np.random.default_rng(4)
+    a, b = rand_std(500, rng), rand_std(500, rng)
+    a[0] = std_words([Z.R - 1])[0]
+    b[0] = std_words([1])[0]
+    got = from_std_arr(add_mod_r(a, b))
+    assert got == [(x + y) % Z.R for x, y in zip(from_std_arr(a), from_std_arr(b))]
+
+
+@pytest.mark.parametrize("g2", [False, True])
+def test_msm_2_22_linearity(ctx, g2):
+    """BASELINE config 3 / config 5 at 2^22 points, where a Python closed form
+    is too slow: MSM(P, s) + MSM(P, t) = MSM(P, s + t) and
+    MSM(P, s) + MSM(P, s) = MSM(P, 2s), uniform scalars."""
+    n = 1 << 22
+    rng = np.random.default_rng(22 + g2)
+    dp = gpu_points(ctx, rand_std(n, rng), g2=g2)  # any words below r are valid Montgomery scalars
+    s, t = rand_std(n, rng), rand_std(n, rng)
+    run = ctx.msm_g2 if g2 else ctx.msm_g1
+    G, from_words = (Z.g2, Z.g2_from_words) if g2 else (Z.g1, Z.g1_from_words)
+    res = {}
+    for name, sc in (("s", s), ("t", t), ("s+t", add_mod_r(s, t)), ("2s", add_mod_r(s, s))):
+        ds = ctx.upload(sc)
+        print(f"[msm 2^22 {'g2' if g2 else 'g1'}] scalars {name}", flush=True)
+        res[name] = from_words(run(dp, ds, n))
+        del ds
+    assert res["s"] is not None and res["t"] is not None
+    assert G.padd(res["s"], res["t"]) == res["s+t"]
+    assert G.padd(res["s"], res["s"]) == res["2s"]
+
+
 # ------------------------------------------------------------------ G2
 @pytest.mark.parametrize("n", [1, 16, 129, 700])
 def test_msm_g2_vs_oracle(ctx, n):
