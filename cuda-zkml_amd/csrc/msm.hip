@@ -901,7 +901,7 @@ static void host_finish(const std::vector<xyzz<F>>& parts, int W, int per_w, uin
 // key's resident queries.  outs[s] receives set s's affine result.
 template <class F>
 static int msm_run_sets(zk_context* ctx, MsmWorkspace& ws, const BaseSets& sets, int nsets, const void* d_scalars,
-                        size_t n, uint64_t* const* outs, hipStream_t st, const MsmHook* hook = nullptr) {
+                        size_t n, uint64_t* const* outs, hipStream_t st) {
   constexpr int OUTW = sizeof(F) == sizeof(fq) ? 8 : 16;
   if (nsets < 1 || nsets > MSM_SETS) return ctx->fail(ZK_ERR_INVALID, "msm: 1 to 3 point sets");
   for (int k = 0; k < nsets; k++) memset(outs[k], 0, OUTW * 8);
@@ -912,10 +912,16 @@ static int msm_run_sets(zk_context* ctx, MsmWorkspace& ws, const BaseSets& sets,
   const int W = (MSM_BITS + c - 1) / c;
   const uint32_t B = 1u << (c - 1);  // buckets per window
   const size_t nbuckets = (size_t)W * B;
-  // entries per accumulation thread: MSM_L0, halved below 2^23 entries so
-  // that small inputs still spread over enough threads (measured: shorter
-  // chunks deepen the chunk-combine tree and cost more than they save)
-  const uint32_t L0 = (size_t)W * n >= ((size_t)1 << 23) ? MSM_L0 : MSM_L0 / 2;
+  // entries per accumulation thread, by the entry count W*n: short chunks
+  // give small MSMs enough threads (a thread's chunk is a serial chain of
+  // additions), long chunks keep the chunk-combine tree of large ones shallow.
+  // Measured on MI355X over 2^10 .. 2^20 points, G1 and G2, uniform and
+  // witness-like scalars.
+  const size_t entries = (size_t)W * n;
+  const uint32_t L0 = entries >= ((size_t)1 << 23)   ? MSM_L0
+                      : entries >= ((size_t)1 << 20) ? MSM_L0 / 2
+                      : entries >= ((size_t)1 << 18) ? MSM_L0 / 4
+                                                     : MSM_L0 / 8;
   const uint32_t n_pad = (uint32_t)((n + L0 - 1) / L0 * L0);
   const uint32_t cpw = n_pad / L0;  // chunks per window
   const uint32_t nchunks = cpw * (uint32_t)W;
@@ -985,10 +991,6 @@ static int msm_run_sets(zk_context* ctx, MsmWorkspace& ws, const BaseSets& sets,
   const uint32_t gxl = cdiv((size_t)nchunks * Lanes<F>::N, 256);  // combine: Lanes<F>::N lanes per chunk
   ZK_LAUNCH(ctx, st, "msm_accumulate", k_msm_accumulate<F>, dim3(gx, nsets), dim3(256), 0, sorted, sets, start, end,
             wstat, nchunks, cpw, n_pad, L0, nbuckets, buckets, slots);
-  if (hook) {
-    ZK_HIP(ctx, hipEventRecord(hook->ev, st));
-    hook->fn(hook->arg);
-  }
   // the largest bucket decides the depth of the chunk-combine tree; its
   // read-back overlaps the accumulation
   ZK_HIP(ctx, hipEventSynchronize(ws.stat_ready));
@@ -1061,13 +1063,13 @@ static int msm_run_sets(zk_context* ctx, MsmWorkspace& ws, const BaseSets& sets,
 // One point set over all n scalars.
 template <class F>
 static int msm_run_recs(zk_context* ctx, MsmWorkspace& ws, const uint4* recs, const void* d_scalars, size_t n,
-                        uint64_t* out, hipStream_t st, const MsmHook* hook = nullptr) {
+                        uint64_t* out, hipStream_t st) {
   BaseSets sets{};
   sets.recs[0] = recs;
   sets.lo[0] = 0;
   sets.hi[0] = (uint32_t)std::min<size_t>(n, 0xffffffffu);
   uint64_t* outs[1] = {out};
-  return msm_run_sets<F>(ctx, ws, sets, 1, d_scalars, n, outs, st, hook);
+  return msm_run_sets<F>(ctx, ws, sets, 1, d_scalars, n, outs, st);
 }
 
 template <class F>
@@ -1112,10 +1114,10 @@ int msm_g1_sets_ws(zk_context* ctx, MsmWorkspace* ws, int nsets, const void* con
 }
 
 int msm_recs_ws(zk_context* ctx, MsmWorkspace* ws, bool g2, const void* d_recs, const void* d_scalars, size_t n,
-                uint64_t* out, hipStream_t st, const MsmHook* hook) {
+                uint64_t* out, hipStream_t st) {
   if (!ws) return ctx->fail(ZK_ERR_INVALID, "msm: no workspace");
-  if (g2) return msm_run_recs<fq2>(ctx, *ws, (const uint4*)d_recs, d_scalars, n, out, st, hook);
-  return msm_run_recs<fq>(ctx, *ws, (const uint4*)d_recs, d_scalars, n, out, st, hook);
+  if (g2) return msm_run_recs<fq2>(ctx, *ws, (const uint4*)d_recs, d_scalars, n, out, st);
+  return msm_run_recs<fq>(ctx, *ws, (const uint4*)d_recs, d_scalars, n, out, st);
 }
 
 int msm_g1_recs(zk_context* ctx, const void* d_recs, const void* d_scalars, size_t n, uint64_t out[8],

@@ -14,22 +14,6 @@
 
 namespace zk {
 
-
-// p - 2, little-endian words (exponent of the Fermat inverse in Fq)
-__constant__ uint32_t PG_QM2[8] = {0xd87cfd45u, 0x3c208c16u, 0x6871ca8du, 0x97816a91u,
-                                   0x8181585du, 0xb85045b6u, 0xe131a029u, 0x30644e72u};
-
-__device__ __forceinline__ fq finv(const fq& a) {
-  uint32_t e[8];
-#pragma unroll
-  for (int i = 0; i < 8; i++) e[i] = PG_QM2[i];
-  return fpow(a, e);
-}
-__device__ __forceinline__ fq2 finv(const fq2& a) {
-  fq n = finv(fadd(fsqr(a.c0), fsqr(a.c1)));
-  return fq2{fmul(a.c0, n), fneg(fmul(a.c1, n))};
-}
-
 __device__ __forceinline__ void put_ext(uint32_t* o, const fq& a) { to_mont256(a, o); }
 __device__ __forceinline__ void put_ext(uint32_t* o, const fq2& a) {
   to_mont256(a.c0, o);
@@ -84,30 +68,17 @@ __global__ __launch_bounds__(128) void k_fixed_base(uint32_t* __restrict__ out, 
       xyzz_madd(acc[j], x, y);
     }
   }
-  // shared inversion of d_j = ZZ_j * ZZZ_j
-  F pre[PG_PER], d[PG_PER];
-  F prod;
-  fset_one(prod);
+  F x[PG_PER], y[PG_PER];
+  bool inf[PG_PER];
+  xyzz_to_affine_batch<F, PG_PER>(acc, x, y, inf);
   for (int j = 0; j < PG_PER; j++) {
-    pre[j] = prod;
-    if (!xyzz_is_inf(acc[j])) {
-      d[j] = fmul(acc[j].zz, acc[j].zzz);
-      prod = fmul(prod, d[j]);
-    }
-  }
-  F inv = finv(prod);
-  for (int j = PG_PER - 1; j >= 0; j--) {
     const size_t i = base + j;
     uint32_t o[2 * EW];
-    if (xyzz_is_inf(acc[j])) {
+    if (inf[j]) {
       for (int k = 0; k < 2 * EW; k++) o[k] = 0;
     } else {
-      F di = fmul(inv, pre[j]);
-      inv = fmul(inv, d[j]);
-      F x = fmul(acc[j].x, fmul(di, acc[j].zzz));
-      F y = fmul(acc[j].y, fmul(di, acc[j].zz));
-      put_ext(o, x);
-      put_ext(o + EW, y);
+      put_ext(o, x[j]);
+      put_ext(o + EW, y[j]);
     }
     if (i < n)
       for (int k = 0; k < 2 * EW; k++) out[i * 2 * EW + k] = o[k];

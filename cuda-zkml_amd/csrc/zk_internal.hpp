@@ -139,16 +139,9 @@ int recs_from_std(zk_context* ctx, bool g2, void* d_recs, const void* d_std, con
 size_t rec_bytes(bool g2);
 MsmWorkspace* msm_workspace_new();
 void msm_workspace_free(MsmWorkspace* ws);
-// Callback after the accumulation kernel is enqueued: `ev` is recorded on the
-// MSM's stream right after it, then `fn` runs on the calling thread.
-struct MsmHook {
-  hipEvent_t ev = nullptr;
-  void (*fn)(void*) = nullptr;
-  void* arg = nullptr;
-};
 // MSM over records with an explicit workspace (one per concurrent caller)
 int msm_recs_ws(zk_context* ctx, MsmWorkspace* ws, bool g2, const void* d_recs, const void* d_scalars, size_t n,
-                uint64_t* out_affine, hipStream_t st, const MsmHook* after_accumulate = nullptr);
+                uint64_t* out_affine, hipStream_t st);
 // G1 MSMs of up to 3 point sets over one scalar vector of n entries, sharing
 // the digit sort and every latency-bound step: set k multiplies recs[k][j] by
 // scalar lo[k] + j for j < count[k]; outs[k] gets its affine result.
