@@ -690,7 +690,8 @@ int zk_prove(zk_context* ctx, const zk_pk* pk, const zk_r1cs* c, const void* h_w
     add(pk->A, 0, na, a_msm);
     add(pk->B1, 0, nb1, b1_msm);
     add(pk->L, 1 + (size_t)pk->npub, npriv_l > 0 ? (size_t)npriv_l : 0, l_msm);
-    if (rc_g1 == ZK_OK && ns) rc_g1 = msm_g1_sets_ws(ctx, ctx->job_ws[JOB_G1], ns, recs, lo, cnt, d_w, m, outs, js);
+    if (rc_g1 == ZK_OK && ns)
+      rc_g1 = msm_g1_sets_ws(ctx, ctx->job_ws[JOB_G1], ns, recs, lo, cnt, d_w, m, outs, js, /*beside=*/true);
     record(5 + 2 * JOB_G1, js, rc_g1);
     if (rc_g1 == ZK_OK) {
       g1_tail = g1_from_words(a_msm).mul(s).add(g1_from_words(l_msm));
@@ -719,7 +720,8 @@ int zk_prove(zk_context* ctx, const zk_pk* pk, const zk_r1cs* c, const void* h_w
   if (qrc == ZK_OK && hipEventRecord(ev[2], st) != hipSuccess) qrc = ctx->fail(ZK_ERR_HIP, "prove: event record");
   if (qrc == ZK_OK) {  // H after the quotient, same stream
     record(4 + 2 * JOB_H, st, rc_h);
-    if (rc_h == ZK_OK && nh) rc_h = msm_recs_ws(ctx, ctx->job_ws[JOB_H], false, pk->H, d_h, nh, h_msm, st);
+    if (rc_h == ZK_OK && nh)
+      rc_h = msm_recs_ws(ctx, ctx->job_ws[JOB_H], false, pk->H, d_h, nh, h_msm, st, /*beside=*/true);
     else if (!nh) memset(h_msm, 0, sizeof(h_msm));
     record(5 + 2 * JOB_H, st, rc_h);
   }

@@ -901,7 +901,7 @@ static void host_finish(const std::vector<xyzz<F>>& parts, int W, int per_w, uin
 // key's resident queries.  outs[s] receives set s's affine result.
 template <class F>
 static int msm_run_sets(zk_context* ctx, MsmWorkspace& ws, const BaseSets& sets, int nsets, const void* d_scalars,
-                        size_t n, uint64_t* const* outs, hipStream_t st) {
+                        size_t n, uint64_t* const* outs, hipStream_t st, bool beside = false) {
   constexpr int OUTW = sizeof(F) == sizeof(fq) ? 8 : 16;
   if (nsets < 1 || nsets > MSM_SETS) return ctx->fail(ZK_ERR_INVALID, "msm: 1 to 3 point sets");
   for (int k = 0; k < nsets; k++) memset(outs[k], 0, OUTW * 8);
@@ -917,11 +917,14 @@ static int msm_run_sets(zk_context* ctx, MsmWorkspace& ws, const BaseSets& sets,
   // additions), long chunks keep the chunk-combine tree of large ones shallow.
   // Measured on MI355X over 2^10 .. 2^20 points, G1 and G2, uniform and
   // witness-like scalars.
+  // Beside other kernels (see msm_recs_ws) a G1 chunk is one step shorter
+  // (measured in the 2^16 proof: 1.97 -> 1.87 ms).
   const size_t entries = (size_t)W * n;
-  const uint32_t L0 = entries >= ((size_t)1 << 23)   ? MSM_L0
-                      : entries >= ((size_t)1 << 20) ? MSM_L0 / 2
-                      : entries >= ((size_t)1 << 18) ? MSM_L0 / 4
-                                                     : MSM_L0 / 8;
+  const uint32_t L0_alone = entries >= ((size_t)1 << 23)   ? MSM_L0
+                            : entries >= ((size_t)1 << 20) ? MSM_L0 / 2
+                            : entries >= ((size_t)1 << 18) ? MSM_L0 / 4
+                                                           : MSM_L0 / 8;
+  const uint32_t L0 = beside && !G2 ? std::max<uint32_t>(L0_alone / 2, MSM_L0 / 8) : L0_alone;
   const uint32_t n_pad = (uint32_t)((n + L0 - 1) / L0 * L0);
   const uint32_t cpw = n_pad / L0;  // chunks per window
   const uint32_t nchunks = cpw * (uint32_t)W;
@@ -1063,13 +1066,13 @@ static int msm_run_sets(zk_context* ctx, MsmWorkspace& ws, const BaseSets& sets,
 // One point set over all n scalars.
 template <class F>
 static int msm_run_recs(zk_context* ctx, MsmWorkspace& ws, const uint4* recs, const void* d_scalars, size_t n,
-                        uint64_t* out, hipStream_t st) {
+                        uint64_t* out, hipStream_t st, bool beside = false) {
   BaseSets sets{};
   sets.recs[0] = recs;
   sets.lo[0] = 0;
   sets.hi[0] = (uint32_t)std::min<size_t>(n, 0xffffffffu);
   uint64_t* outs[1] = {out};
-  return msm_run_sets<F>(ctx, ws, sets, 1, d_scalars, n, outs, st);
+  return msm_run_sets<F>(ctx, ws, sets, 1, d_scalars, n, outs, st, beside);
 }
 
 template <class F>
@@ -1101,7 +1104,8 @@ int msm_g2_run(zk_context* ctx, const void* d_points, const void* d_scalars, siz
 MsmWorkspace* msm_workspace_new() { return new MsmWorkspace(); }
 
 int msm_g1_sets_ws(zk_context* ctx, MsmWorkspace* ws, int nsets, const void* const* recs, const size_t* lo,
-                   const size_t* count, const void* d_scalars, size_t n, uint64_t* const* outs, hipStream_t st) {
+                   const size_t* count, const void* d_scalars, size_t n, uint64_t* const* outs, hipStream_t st,
+                   bool beside) {
   if (!ws || nsets < 1 || nsets > MSM_SETS) return ctx->fail(ZK_ERR_INVALID, "msm: 1 to 3 point sets");
   BaseSets sets{};
   for (int k = 0; k < nsets; k++) {
@@ -1110,14 +1114,14 @@ int msm_g1_sets_ws(zk_context* ctx, MsmWorkspace* ws, int nsets, const void* con
     sets.lo[k] = (uint32_t)lo[k];
     sets.hi[k] = (uint32_t)(lo[k] + count[k]);
   }
-  return msm_run_sets<fq>(ctx, *ws, sets, nsets, d_scalars, n, outs, st);
+  return msm_run_sets<fq>(ctx, *ws, sets, nsets, d_scalars, n, outs, st, beside);
 }
 
 int msm_recs_ws(zk_context* ctx, MsmWorkspace* ws, bool g2, const void* d_recs, const void* d_scalars, size_t n,
-                uint64_t* out, hipStream_t st) {
+                uint64_t* out, hipStream_t st, bool beside) {
   if (!ws) return ctx->fail(ZK_ERR_INVALID, "msm: no workspace");
-  if (g2) return msm_run_recs<fq2>(ctx, *ws, (const uint4*)d_recs, d_scalars, n, out, st);
-  return msm_run_recs<fq>(ctx, *ws, (const uint4*)d_recs, d_scalars, n, out, st);
+  if (g2) return msm_run_recs<fq2>(ctx, *ws, (const uint4*)d_recs, d_scalars, n, out, st, beside);
+  return msm_run_recs<fq>(ctx, *ws, (const uint4*)d_recs, d_scalars, n, out, st, beside);
 }
 
 int msm_g1_recs(zk_context* ctx, const void* d_recs, const void* d_scalars, size_t n, uint64_t out[8],

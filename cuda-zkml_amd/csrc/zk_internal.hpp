@@ -139,14 +139,18 @@ int recs_from_std(zk_context* ctx, bool g2, void* d_recs, const void* d_std, con
 size_t rec_bytes(bool g2);
 MsmWorkspace* msm_workspace_new();
 void msm_workspace_free(MsmWorkspace* ws);
-// MSM over records with an explicit workspace (one per concurrent caller)
+// MSM over records with an explicit workspace (one per concurrent caller).
+// beside: the MSM shares the GPU with other kernels (a proof); a G1 MSM then
+// gives each accumulation thread half as many entries, so its waves free CU
+// slots for the other streams' kernels sooner.
 int msm_recs_ws(zk_context* ctx, MsmWorkspace* ws, bool g2, const void* d_recs, const void* d_scalars, size_t n,
-                uint64_t* out_affine, hipStream_t st);
+                uint64_t* out_affine, hipStream_t st, bool beside = false);
 // G1 MSMs of up to 3 point sets over one scalar vector of n entries, sharing
 // the digit sort and every latency-bound step: set k multiplies recs[k][j] by
 // scalar lo[k] + j for j < count[k]; outs[k] gets its affine result.
 int msm_g1_sets_ws(zk_context* ctx, MsmWorkspace* ws, int nsets, const void* const* recs, const size_t* lo,
-                   const size_t* count, const void* d_scalars, size_t n, uint64_t* const* outs, hipStream_t st);
+                   const size_t* count, const void* d_scalars, size_t n, uint64_t* const* outs, hipStream_t st,
+                   bool beside = false);
 
 // ---- fixed base (pointgen.hip)
 int g1_generator_mul(zk_context* ctx, const void* d_scalars, size_t n, void* d_out, hipStream_t st);
