@@ -89,6 +89,37 @@ def witness_like_scalars(n, rng, uniform):
     return s
 
 
+def ntt_case(ctx, ln, rng):
+    """Forward NTT of 2^ln uniform Fr elements (config 2): pass-kernel time from
+    HIP events, wall time per transform, HBM and VALU fractions.  Returns the
+    figures, the input and the output (for the CPU baseline's check)."""
+    import zkml_amd
+    a = zkml_amd.random_fr(1 << ln, rng)
+    da = ctx.upload(a)
+    do = ctx.alloc((1 << ln) * 32)
+    ctx.ntt(do, da, ln)
+    ctx.sync()
+    ctx.set_profiling(True, only="ntt_pass")
+    ctx.reset_kernel_stats()
+    reps = 10
+    t0 = time.perf_counter()
+    for _ in range(reps):
+        ctx.ntt(do, da, ln)
+    ctx.sync()
+    wall = (time.perf_counter() - t0) * 1e3 / reps
+    _, kms = ctx.kernel_stats("ntt_pass")
+    ctx.set_profiling(False)
+    kms /= reps
+    ntt = {"log_n": ln, "ms": round(kms, 4), "wall_ms": round(wall, 4),
+           "hbm_GBps_alg": round(64 * (1 << ln) / (kms * 1e-3) / 1e9, 1),
+           "hbm_frac": round(64 * (1 << ln) / (kms * 1e-3) / 1e9 / PEAK_HBM_GBS, 4),
+           "valu_frac": round(((1 << ln) // 2 * ln) * MADS_PER_FIELD_MUL / (kms * 1e-3) / 1e12 / PEAK_MAD_TOPS, 4)}
+    log(f"[bench] NTT 2^{ln}: {kms:.3f} ms")
+    out = ctx.d2h(do, (1 << ln, 4))
+    del da, do
+    return ntt, a, out
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -97,6 +128,8 @@ def main():
     ap.add_argument("--log-n", type=int, default=20)
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
     ap.add_argument("--no-prove", action="store_true")
+    ap.add_argument("--msm-only", action="store_true",
+                    help="only the 2^20 G1 MSM steps (the run the rocprofv3 counter summaries profile)")
     ap.add_argument("--copy-calibration", type=int, default=0, metavar="MIB",
                     help="only run a plain device copy of MIB MiB (torch's copy kernel), the reference for "
                          "scaling rocprofv3 FETCH_SIZE / WRITE_SIZE readings to bytes")
@@ -200,55 +233,37 @@ def main():
                 "valu_frac": round(mults * MADS_PER_FIELD_MUL / (ms * 1e-3) / 1e12 / PEAK_MAD_TOPS, 4)}
 
     msm_more = {}
-    sk = witness_like_scalars(n, rng, s)
-    d_sk = ctx.upload(sk)
-    msm_more[f"g1_2_{args.log_n}_witness_like"] = msm_entry(time_msm(ctx.msm_g1, dp, d_sk, n, 10), n)
-    del d_sk
-    for ln_ in (16, 18):
-        msm_more[f"g1_2_{ln_}"] = msm_entry(time_msm(ctx.msm_g1, dp, ds, 1 << ln_, 20), 1 << ln_)
-    n22 = 1 << 22
-    k22 = zkml_amd.random_fr(n22, rng)
-    d_k22 = ctx.upload(k22)
-    dp22 = ctx.alloc(n22 * 64)
-    ctx.g1_generator_mul(d_k22, n22, dp22)
-    ds22 = ctx.upload(zkml_amd.random_fr(n22, rng))
-    msm_more["g1_2_22"] = msm_entry(time_msm(ctx.msm_g1, dp22, ds22, n22, 5), n22)
-    del d_k22, dp22, ds22, k22
-    n16 = 1 << 16
-    d_k2 = ctx.upload(k[:n16].copy())
-    dp2 = ctx.alloc(n16 * 128)
-    ctx.g2_generator_mul(d_k2, n16, dp2)
-    msm_more["g2_2_16"] = msm_entry(time_msm(ctx.msm_g2, dp2, ds, n16, 20), n16, g2=True)
-    del d_k2, dp2
+    if args.msm_only:
+        args.no_prove = args.no_cpu = True
+    else:
+        sk = witness_like_scalars(n, rng, s)
+        d_sk = ctx.upload(sk)
+        msm_more[f"g1_2_{args.log_n}_witness_like"] = msm_entry(time_msm(ctx.msm_g1, dp, d_sk, n, 10), n)
+        del d_sk
+        for ln_ in (16, 18):
+            msm_more[f"g1_2_{ln_}"] = msm_entry(time_msm(ctx.msm_g1, dp, ds, 1 << ln_, 20), 1 << ln_)
+        n22 = 1 << 22
+        k22 = zkml_amd.random_fr(n22, rng)
+        d_k22 = ctx.upload(k22)
+        dp22 = ctx.alloc(n22 * 64)
+        ctx.g1_generator_mul(d_k22, n22, dp22)
+        ds22 = ctx.upload(zkml_amd.random_fr(n22, rng))
+        msm_more["g1_2_22"] = msm_entry(time_msm(ctx.msm_g1, dp22, ds22, n22, 5), n22)
+        del d_k22, dp22, ds22, k22
+        n16 = 1 << 16
+        d_k2 = ctx.upload(k[:n16].copy())
+        dp2 = ctx.alloc(n16 * 128)
+        ctx.g2_generator_mul(d_k2, n16, dp2)
+        msm_more["g2_2_16"] = msm_entry(time_msm(ctx.msm_g2, dp2, ds, n16, 20), n16, g2=True)
+        del d_k2, dp2
     for key, v in msm_more.items():
         log(f"[bench] MSM {key}: {v['ms']:.3f} ms, {v['Mpoints_per_s']} Mpoints/s")
 
     # ---------------- NTT 2^22 (config 2)
-    ntt = {}
+    ntt = None
     ln = 22
-    a = zkml_amd.random_fr(1 << ln, rng)
-    da = ctx.upload(a)
-    do = ctx.alloc((1 << ln) * 32)
-    ctx.ntt(do, da, ln)
-    ctx.sync()
-    ctx.set_profiling(True, only="ntt_pass")
-    ctx.reset_kernel_stats()
-    reps = 10
-    t0 = time.perf_counter()
-    for _ in range(reps):
-        ctx.ntt(do, da, ln)
-    ctx.sync()
-    wall = (time.perf_counter() - t0) * 1e3 / reps
-    _, kms = ctx.kernel_stats("ntt_pass")
-    ctx.set_profiling(False)
-    kms /= reps
-    ntt = {"log_n": ln, "ms": round(kms, 4), "wall_ms": round(wall, 4),
-           "hbm_GBps_alg": round(64 * (1 << ln) / (kms * 1e-3) / 1e9, 1),
-           "hbm_frac": round(64 * (1 << ln) / (kms * 1e-3) / 1e9 / PEAK_HBM_GBS, 4),
-           "valu_frac": round(((1 << ln) // 2 * ln) * MADS_PER_FIELD_MUL / (kms * 1e-3) / 1e12 / PEAK_MAD_TOPS, 4)}
-    log(f"[bench] NTT 2^22: {kms:.3f} ms")
-    ntt_out = ctx.d2h(do, (1 << ln, 4))
-    del da, do
+    if not args.msm_only:
+        ntt, ntt_in, ntt_out = ntt_case(ctx, ln, rng)
 
     # ---------------- full prove at 2^16
     prove = prove_syn = prove22 = prove_c1 = None
@@ -276,7 +291,8 @@ def main():
             vk_bytes = open(os.path.join(td, "vk.bin"), "rb").read()
             if not keep:
                 shutil.rmtree(td)
-            ctx.prove(pk, r, w, npub, 0xCAFEBABE)  # warm-up (workspaces, plans)
+            for _ in range(3):  # warm-up (workspaces, streams, host threads)
+                ctx.prove(pk, r, w, npub, 0xCAFEBABE)
             times, parts, proof = [], None, None
             for _ in range(reps):
                 t0 = time.perf_counter()
@@ -309,10 +325,10 @@ def main():
                 kept["npriv"] = npriv
             return nc, nv, npub, A, B, C, w
 
-        prove = prove_case(fixture("config4"), 7, "prove config 4 (2^16)", keep=True)
-        prove_c1 = prove_case(fixture("config1"), 7, "prove config 1 (2^13)")
-        prove_syn = prove_case(synthetic((1 << 16) - 64, 16), 5, "prove 2^16 synthetic")
-        prove22 = prove_case(synthetic(1 << 22, 22), 3, "prove 2^22 (config 5)")
+        prove = prove_case(fixture("config4"), 41, "prove config 4 (2^16)", keep=True)
+        prove_c1 = prove_case(fixture("config1"), 41, "prove config 1 (2^13)")
+        prove_syn = prove_case(synthetic((1 << 16) - 64, 16), 21, "prove 2^16 synthetic")
+        prove22 = prove_case(synthetic(1 << 22, 22), 5, "prove 2^22 (config 5)")
 
     # ---------------- CPU baseline (oracle restatement of the reference MSM)
     # On one thread (the reference's host code) and on every thread OpenMP may
@@ -338,7 +354,7 @@ def main():
         del pts
         ntt_cpu = {}
         for threads in sorted({1, all_threads}):
-            b = np.ascontiguousarray(a.copy())
+            b = np.ascontiguousarray(ntt_in.copy())
             t0 = time.perf_counter()
             lib.orc_ntt(ptr(b), ln, 0, threads)
             dt = time.perf_counter() - t0

@@ -225,12 +225,12 @@ ZK_HD void xyzz_mul_small(xyzz<F>& p, uint32_t k) {
 }
 
 // a^-1 = a^(q-2) (Fermat); Fq2 through the norm: (c0 - c1 u) / (c0^2 + c1^2)
-__device__ __forceinline__ fq finv(const fq& a) {
+ZK_HD fq finv(const fq& a) {
   const uint32_t qm2[8] = {0xd87cfd45u, 0x3c208c16u, 0x6871ca8du, 0x97816a91u,
                            0x8181585du, 0xb85045b6u, 0xe131a029u, 0x30644e72u};  // q - 2
   return fpow(a, qm2);
 }
-__device__ __forceinline__ fq2 finv(const fq2& a) {
+ZK_HD fq2 finv(const fq2& a) {
   fq n = finv(fadd(fsqr(a.c0), fsqr(a.c1)));
   return fq2{fmul(a.c0, n), fneg(fmul(a.c1, n))};
 }
@@ -239,8 +239,7 @@ __device__ __forceinline__ fq2 finv(const fq2& a) {
 // the product of every ZZ * ZZZ (Montgomery's trick); inf[j] marks the point
 // at infinity (x, y then unset).
 template <class F, int PER>
-__device__ __forceinline__ void xyzz_to_affine_batch(const xyzz<F> (&p)[PER], F (&x)[PER], F (&y)[PER],
-                                                     bool (&inf)[PER]) {
+ZK_HD void xyzz_to_affine_batch(const xyzz<F> (&p)[PER], F (&x)[PER], F (&y)[PER], bool (&inf)[PER]) {
   F pre[PER], d[PER];
   F prod;
   fset_one(prod);

@@ -917,14 +917,16 @@ static int msm_run_sets(zk_context* ctx, MsmWorkspace& ws, const BaseSets& sets,
   // additions), long chunks keep the chunk-combine tree of large ones shallow.
   // Measured on MI355X over 2^10 .. 2^20 points, G1 and G2, uniform and
   // witness-like scalars.
-  // Beside other kernels (see msm_recs_ws) a G1 chunk is one step shorter
-  // (measured in the 2^16 proof: 1.97 -> 1.87 ms).
+  // Beside other kernels (see msm_recs_ws) a G1 chunk below the longest is
+  // one step shorter (measured in the 2^16 proof: 1.97 -> 1.87 ms; the 2^22
+  // proof's MSMs keep the longest chunks, shorter ones cost it 2 ms).
   const size_t entries = (size_t)W * n;
   const uint32_t L0_alone = entries >= ((size_t)1 << 23)   ? MSM_L0
                             : entries >= ((size_t)1 << 20) ? MSM_L0 / 2
                             : entries >= ((size_t)1 << 18) ? MSM_L0 / 4
                                                            : MSM_L0 / 8;
-  const uint32_t L0 = beside && !G2 ? std::max<uint32_t>(L0_alone / 2, MSM_L0 / 8) : L0_alone;
+  const uint32_t L0 =
+      beside && !G2 && L0_alone < (uint32_t)MSM_L0 ? std::max<uint32_t>(L0_alone / 2, MSM_L0 / 8) : L0_alone;
   const uint32_t n_pad = (uint32_t)((n + L0 - 1) / L0 * L0);
   const uint32_t cpw = n_pad / L0;  // chunks per window
   const uint32_t nchunks = cpw * (uint32_t)W;
