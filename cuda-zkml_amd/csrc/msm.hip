@@ -670,15 +670,16 @@ __global__ __launch_bounds__(256) void k_msm_finalize(ChunkSlots<F> all_slots, u
 // ------------------------------------------------------------------ bucket reduction
 // Window sum  sum_{b=1..B} b S_b,  B = 2^(c-1).
 //
-// Level 1: a workgroup of T threads owns T*G consecutive buckets (base k*T*G);
-// thread t owns buckets base + t*G + i, i = 1..G, and forms
-//   run_t = sum_i S,  acc_t = sum_i i S      (2G additions, from the top).
+// Bucket b of a window holds digit b + 1.  Level 1: K workgroups per window;
+// group k owns the buckets b = k + K p (every K-th bucket, positions
+// p = 0 .. T G - 1), its thread t the positions p = t G + i, i < G, forming
+//   run_t = sum_i S,  acc_t = sum_i (i+1) S      (2G additions, from the top).
 // With the inclusive suffix sums SR_t = sum_{u >= t} run_u (Hillis-Steele scan
-// in LDS),  sum_{b in group} (b - base) S_b = sum_t acc_t + G sum_{t >= 1} SR_t,
-// so each thread adds G*SR_t (log2 G doublings) to acc_t and a tree sums the
-// group.  Outputs per group: P_k (that sum) and RUN_k = SR_0.
-// Level 2 (one workgroup per window, K groups):
-//   sum_b b S_b = sum_k P_k + T G sum_{s >= 1} SRUN_s,  same scan and tree.
+// in LDS),  sum_p (p+1) S = sum_t acc_t + G sum_{t >= 1} SR_t,  so each thread
+// adds G*SR_t (log2 G doublings) to acc_t and a tree sums the group.  Outputs
+// per group: P_k (that sum) and RUN_k = SR_0.
+// Level 2 (k_msm_reduce2) weights group k by K and k + 1 - K, so its chain
+// holds log2 K doublings where contiguous groups would need log2(T G).
 // "Thread" t is a lane pair for G2 (Lanes<F>); T = blockDim.x / Lanes<F>::N.
 
 // Inclusive suffix scan over the T values held by the items of a workgroup;
@@ -739,13 +740,16 @@ __global__ __launch_bounds__(TMAX * Lanes<F>::N) void k_msm_reduce1(const xyzz<F
   const int T = blockDim.x / LN::N, G = 1 << log2g;
   const uint32_t w = blockIdx.x / K, k = blockIdx.x % K;
   const uint32_t t = threadIdx.x / LN::N;
-  const uint32_t kb = w * B1 + (k * T + t) * G;            // bucket of this item's first entry
-  const uint32_t sb = (w % W_set) * B1 + (k * T + t) * G;  // its key in the sorted list
+  // group k owns buckets k + K p, p = 0, 1, ...; this item the positions
+  // p = t G + i, i < G
+  const uint32_t kb = w * B1 + k;            // bucket of position 0
+  const uint32_t sb = (w % W_set) * B1 + k;  // its key in the sorted list
   xyzz<R> run, acc;
   xyzz_set_inf(run);
   xyzz_set_inf(acc);
   for (int i = G - 1; i >= 0; i--) {
-    if (end[sb + i] > start[sb + i]) xyzz_add(run, LN::load(buckets[kb + i]));
+    const uint32_t off = (t * G + i) * K;
+    if (end[sb + off] > start[sb + off]) xyzz_add(run, LN::load(buckets[kb + off]));
     xyzz_add(acc, run);
   }
   xyzz<R> sr = wg_suffix_scan<F, R>(run, sh, T);
@@ -759,32 +763,62 @@ __global__ __launch_bounds__(TMAX * Lanes<F>::N) void k_msm_reduce1(const xyzz<F
   if (t == 0) LN::store(P[blockIdx.x], tot);
 }
 
-// Level 2: one workgroup per window over its K group results (a power of two
-// >= K items); log2tg = log2(T*G) of level 1.
-template <class F, int KMAX>
-__global__ __launch_bounds__(KMAX * Lanes<F>::N) void k_msm_reduce2(const xyzz<F>* __restrict__ P,
-                                                                    const xyzz<F>* __restrict__ RUN, uint32_t K,
-                                                                    int log2tg, xyzz<F>* __restrict__ out) {
+// A point from the lane `lanes` above (ds_bpermute per 32-bit word); every
+// lane of the wave must execute it.
+template <class R>
+__device__ __forceinline__ xyzz<R> shfl_down_pt(const xyzz<R>& p, int lanes) {
+  xyzz<R> q;
+  const uint32_t* s = reinterpret_cast<const uint32_t*>(&p);
+  uint32_t* d = reinterpret_cast<uint32_t*>(&q);
+#pragma unroll
+  for (int i = 0; i < (int)(sizeof(xyzz<R>) / 4); i++) d[i] = (uint32_t)__shfl_down((int)s[i], lanes, 64);
+  return q;
+}
+
+// Level 2: one workgroup of two waves per window over its K group results
+// (K a power of two, at most one wave of items).  With P_k and RUN_k of the
+// strided groups above,
+//   sum_b (b+1) S_b = sum_k [(k+1) RUN_k + K (P_k - RUN_k)]
+//                   = sum_k [SR_k + K (P_k - RUN_k)],  SR_k = sum_{k' >= k} RUN_k'.
+// Wave 1 forms K (P_k - RUN_k) (log2 K doublings) while wave 0 forms the
+// suffix sums with lane shuffles; wave 0 then adds them and sums the items.
+template <class F>
+__global__ __launch_bounds__(128) void k_msm_reduce2(const xyzz<F>* __restrict__ P, const xyzz<F>* __restrict__ RUN,
+                                                     uint32_t K, int log2k, xyzz<F>* __restrict__ out) {
   typedef Lanes<F> LN;
   typedef typename LN::R R;
   msm_priority<F>();
-  __shared__ xyzz<F> sh[KMAX];
-  const uint32_t w = blockIdx.x, t = threadIdx.x / LN::N;
-  const int T = blockDim.x / LN::N;
-  xyzz<R> run, acc;
-  xyzz_set_inf(run);
-  xyzz_set_inf(acc);
-  if (t < K) {
-    run = LN::load(RUN[w * K + t]);
-    acc = LN::load(P[w * K + t]);
+  __shared__ xyzz<F> ku[64];
+  const uint32_t w = blockIdx.x;
+  const uint32_t t = (threadIdx.x & 63) / LN::N;  // item within its wave
+  const bool wave0 = threadIdx.x < 64;
+  xyzz<R> v;
+  xyzz_set_inf(v);
+  if (!wave0) {
+    if (t < K) {
+      xyzz<R> r = LN::load(RUN[w * K + t]);
+      v = LN::load(P[w * K + t]);
+      r.y = fneg(r.y);
+      xyzz_add(v, r);
+      for (int d = 0; d < log2k; d++) xyzz_dbl(v);
+      LN::store(ku[t], v);
+    }
+  } else {
+    if (t < K) v = LN::load(RUN[w * K + t]);
+    for (uint32_t d = 1; d < K; d <<= 1) {  // inclusive suffix scan
+      const xyzz<R> o = shfl_down_pt(v, (int)(d * LN::N));
+      if (t + d < K) xyzz_add(v, o);
+    }
   }
-  xyzz<R> sr = wg_suffix_scan<F, R>(run, sh, T);
-  if (t >= 1 && t < K) {
-    for (int d = 0; d < log2tg; d++) xyzz_dbl(sr);
-    xyzz_add(acc, sr);
+  __syncthreads();
+  if (wave0) {
+    if (t < K) xyzz_add(v, LN::load(ku[t]));
+    for (uint32_t d = K / 2; d >= 1; d >>= 1) {  // tree sum into item 0
+      const xyzz<R> o = shfl_down_pt(v, (int)(d * LN::N));
+      if (t < d) xyzz_add(v, o);
+    }
+    if (t == 0) LN::store(out[w], v);
   }
-  xyzz<R> tot = wg_sum<F, R>(acc, sh, T);
-  if (t == 0) LN::store(out[w], tot);
 }
 
 // ------------------------------------------------------------------ workspace
@@ -1016,7 +1050,7 @@ static int msm_run_sets(zk_context* ctx, MsmWorkspace& ws, const BaseSets& sets,
   // bucket reduction: level 1 (T threads x G buckets per group), level 2 per window
   // items per workgroup (a G2 item is a lane pair: 256 lanes either way)
   constexpr int TMAX = sizeof(F) == sizeof(fq) ? 256 : 128;
-  constexpr int KMAX = TMAX;
+  constexpr int KMAX = 64 / Lanes<F>::N;  // level 2 holds the K groups of a window in one wave
   // measured: T = TMAX; G = 8 for 2^15 buckets per window, else 4
   int T1 = TMAX, log2g = B >= 32768 ? 3 : 2;
   // shrink the group for small windows: T1 * G <= B
@@ -1038,14 +1072,14 @@ static int msm_run_sets(zk_context* ctx, MsmWorkspace& ws, const BaseSets& sets,
   xyzz<F>* win = (xyzz<F>*)ws.win.p;
   ZK_LAUNCH(ctx, st, "msm_reduce", (k_msm_reduce1<F, TMAX>), dim3(K * WS), dim3(T1 * Lanes<F>::N), 0, buckets, start,
             end, B, K, (uint32_t)W, log2g, Pk, RUNk);
-  int log2tg = log2g;
-  while ((1 << (log2tg - log2g)) < T1) log2tg++;
-  uint32_t k2 = 1;
-  while (k2 < K) k2 <<= 1;
-  ZK_LAUNCH(ctx, st, "msm_reduce2", (k_msm_reduce2<F, KMAX>), dim3(WS), dim3(k2 * Lanes<F>::N), 0, Pk, RUNk, K,
-            log2tg, win);
+  int log2k = 0;
+  while ((1u << log2k) < K) log2k++;
+  // one group per window: its P is the window sum (no level-2 launch, which
+  // beside other MSMs would wait for a CU with room for its two waves)
+  if (K > 1) ZK_LAUNCH(ctx, st, "msm_reduce2", k_msm_reduce2<F>, dim3(WS), dim3(128), 0, Pk, RUNk, K, log2k, win);
   std::vector<xyzz<F>> parts((size_t)WS);
-  ZK_HIP(ctx, hipMemcpyAsync(parts.data(), win, parts.size() * sizeof(xyzz<F>), hipMemcpyDeviceToHost, st));
+  ZK_HIP(ctx, hipMemcpyAsync(parts.data(), K > 1 ? win : Pk, parts.size() * sizeof(xyzz<F>), hipMemcpyDeviceToHost,
+                             st));
   ZK_HIP(ctx, hipStreamSynchronize(st));
   // window combination on the host (W * c doublings per set): one thread per set
   auto finish = [&](int k) {
