@@ -133,7 +133,21 @@ def main():
     ap.add_argument("--copy-calibration", type=int, default=0, metavar="MIB",
                     help="only run a plain device copy of MIB MiB (torch's copy kernel), the reference for "
                          "scaling rocprofv3 FETCH_SIZE / WRITE_SIZE readings to bytes")
+    ap.add_argument("--gather-calibration", type=int, default=0, metavar="MIB",
+                    help="only run a gather of random 64-byte rows from an MIB MiB table (torch index_select): "
+                         "the reference for scaling FETCH_SIZE of kernels that gather 64-byte point records")
     args = ap.parse_args()
+    if args.gather_calibration:
+        import torch
+        rows = (args.gather_calibration << 20) // 64
+        table = torch.ones((rows, 16), dtype=torch.int32, device="cuda")
+        idx = torch.randperm(rows, device="cuda")
+        for _ in range(3):
+            out = table.index_select(0, idx)
+        torch.cuda.synchronize()
+        print(json.dumps({"rows": rows, "row_bytes_read": 64, "index_bytes_read": 8, "bytes_written": rows * 64,
+                          "launches": 3, "sum": int(out[0, 0].item())}), flush=True)
+        return
     if args.copy_calibration:
         import torch
         nbytes = args.copy_calibration << 20
