@@ -410,9 +410,9 @@ int gen_points_std(zk_context* ctx, const std::vector<Fr>& k, bool g2, std::vect
 // ======================================================================
 extern "C" {
 
-int zk_r1cs_create(zk_context* ctx, int num_constraints, int num_variables, int num_public,
-                   const zk_sparse_entry* A, size_t nA, const zk_sparse_entry* B, size_t nB,
-                   const zk_sparse_entry* C, size_t nC, zk_r1cs** out) {
+static int zk_r1cs_create_impl(zk_context* ctx, int num_constraints, int num_variables, int num_public,
+                               const zk_sparse_entry* A, size_t nA, const zk_sparse_entry* B, size_t nB,
+                               const zk_sparse_entry* C, size_t nC, zk_r1cs** out) {
   if (!ctx || !out) return ZK_ERR_INVALID;
   *out = nullptr;
   if (num_constraints < 0 || num_variables <= 0 || num_public < 0 || num_public + 1 > num_variables)
@@ -487,6 +487,14 @@ int zk_r1cs_create(zk_context* ctx, int num_constraints, int num_variables, int 
   return ZK_OK;
 }
 
+int zk_r1cs_create(zk_context* ctx, int num_constraints, int num_variables, int num_public,
+                   const zk_sparse_entry* A, size_t nA, const zk_sparse_entry* B, size_t nB,
+                   const zk_sparse_entry* C, size_t nC, zk_r1cs** out) {
+  return zk::guard(ctx, [&] {
+    return zk_r1cs_create_impl(ctx, num_constraints, num_variables, num_public, A, nA, B, nB, C, nC, out);
+  });
+}
+
 void zk_r1cs_destroy(zk_r1cs* c) {
   if (!c) return;
   for (int k = 0; k < 3; k++) {
@@ -504,14 +512,19 @@ int zk_r1cs_domain(const zk_r1cs* c, int* log_n) {
   return ZK_OK;
 }
 
-int zk_quotient_h(zk_context* ctx, const zk_r1cs* c, const void* d_witness, size_t m, void* d_h, void* stream) {
+static int zk_quotient_h_impl(zk_context* ctx, const zk_r1cs* c, const void* d_witness, size_t m, void* d_h,
+                              void* stream) {
   if (!ctx || !c || !d_witness || !d_h) return ZK_ERR_INVALID;
   if (m != (size_t)c->nv) return ctx->fail(ZK_ERR_MISMATCH, "quotient: witness length != num_variables");
   ZK_TRY(ctx->ensure(ctx->scratch_b, c->n * 32 * 3));
   return quotient_run(ctx, c, d_witness, d_h, ctx->scratch_b.p, ctx->s(stream), false, nullptr);
 }
 
-int zk_pk_load(zk_context* ctx, const char* path, zk_pk** out) {
+int zk_quotient_h(zk_context* ctx, const zk_r1cs* c, const void* d_witness, size_t m, void* d_h, void* stream) {
+  return zk::guard(ctx, [&] { return zk_quotient_h_impl(ctx, c, d_witness, m, d_h, stream); });
+}
+
+static int zk_pk_load_impl(zk_context* ctx, const char* path, zk_pk** out) {
   if (!ctx || !path || !out) return ZK_ERR_INVALID;
   *out = nullptr;
   FileBuf f;
@@ -573,6 +586,10 @@ int zk_pk_load(zk_context* ctx, const char* path, zk_pk** out) {
   return ZK_OK;
 }
 
+int zk_pk_load(zk_context* ctx, const char* path, zk_pk** out) {
+  return zk::guard(ctx, [&] { return zk_pk_load_impl(ctx, path, out); });
+}
+
 void zk_pk_destroy(zk_pk* pk) {
   if (!pk) return;
   for (void* p : {pk->A, pk->B1, pk->B2, pk->L, pk->H})
@@ -588,8 +605,9 @@ int zk_pk_info(const zk_pk* pk, int* n, int* m, int* npub) {
   return ZK_OK;
 }
 
-int zk_prove(zk_context* ctx, const zk_pk* pk, const zk_r1cs* c, const void* h_witness, size_t m, int num_public,
-             uint64_t blind_seed, int check_witness, uint8_t proof_out[256], double* timings) {
+static int zk_prove_impl(zk_context* ctx, const zk_pk* pk, const zk_r1cs* c, const void* h_witness, size_t m,
+                         int num_public, uint64_t blind_seed, int check_witness, uint8_t proof_out[256],
+                         double* timings) {
   if (!ctx || !pk || !c || !proof_out || (m && !h_witness)) return ZK_ERR_INVALID;
   // events: 0 start, 1 witness resident, 2 quotient done, 3 end,
   // 4 + 2j / 5 + 2j start / end of MSM job j
@@ -656,6 +674,7 @@ int zk_prove(zk_context* ctx, const zk_pk* pk, const zk_r1cs* c, const void* h_w
   // affine conversions.
   G1 pre_a = G1::inf(), pre_c = G1::inf(), g1_tail = G1::inf();
   G2 pre_b = G2::inf();
+  int rc_pre = ZK_OK;
   auto precompute = [&] {
     pre_a = g1_from_words(pk->alpha1).add(g1_from_words(pk->delta1).mul(r));
     pre_b = g2_from_words(pk->beta2).add(g2_from_words(pk->delta2).mul(s));
@@ -699,9 +718,22 @@ int zk_prove(zk_context* ctx, const zk_pk* pk, const zk_r1cs* c, const void* h_w
     }
   };
   for (int j = 0; j < JOB_STREAMS; j++) ZK_HIP(ctx, hipStreamWaitEvent(ctx->job_stream[j], ev[1], 0));
+  // Each job reports a C++ exception (a failed host allocation) as a status;
+  // the joiner waits for the threads on every way out of this function.
+  auto job = [&](const std::function<void()>& fn, int& rc) {
+    return [&fn, &rc] {
+      try {
+        fn();
+      } catch (...) {
+        rc = ZK_ERR_OOM;
+      }
+    };
+  };
+  const std::function<void()> f_b2(run_b2), f_g1(run_g1), f_pre(precompute);
   std::vector<std::thread> workers;
-  for (const std::function<void()>& fn :
-       {std::function<void()>(run_b2), std::function<void()>(run_g1), std::function<void()>(precompute)}) {
+  ThreadJoiner joiner{workers};
+  const std::function<void()> jobs[3] = {job(f_b2, rc_b2), job(f_g1, rc_g1), job(f_pre, rc_pre)};
+  for (const std::function<void()>& fn : jobs) {
     try {
       workers.emplace_back(fn);
     } catch (...) {
@@ -725,8 +757,9 @@ int zk_prove(zk_context* ctx, const zk_pk* pk, const zk_r1cs* c, const void* h_w
     else if (!nh) memset(h_msm, 0, sizeof(h_msm));
     record(5 + 2 * JOB_H, st, rc_h);
   }
-  for (auto& t : workers) t.join();
+  joiner.join();
   ZK_TRY(qrc);
+  ZK_TRY(rc_pre);
   if (check_witness) {
     ZK_HIP(ctx, hipStreamSynchronize(st));
     if (*ctx->h_flag) return ctx->fail(ZK_ERR_WITNESS, "witness does not satisfy the R1CS");
@@ -784,7 +817,15 @@ int zk_prove(zk_context* ctx, const zk_pk* pk, const zk_r1cs* c, const void* h_w
   return ZK_OK;
 }
 
-int zk_setup(zk_context* ctx, const zk_r1cs* c, uint64_t toxic_seed, const char* pk_path, const char* vk_path) {
+int zk_prove(zk_context* ctx, const zk_pk* pk, const zk_r1cs* c, const void* h_witness, size_t m, int num_public,
+             uint64_t blind_seed, int check_witness, uint8_t proof_out[256], double* timings) {
+  return zk::guard(ctx, [&] {
+    return zk_prove_impl(ctx, pk, c, h_witness, m, num_public, blind_seed, check_witness, proof_out, timings);
+  });
+}
+
+static int zk_setup_impl(zk_context* ctx, const zk_r1cs* c, uint64_t toxic_seed, const char* pk_path,
+                         const char* vk_path) {
   if (!ctx || !c || !pk_path || !vk_path) return ZK_ERR_INVALID;
   const int log_n = c->log_n;
   const size_t n = c->n, m = c->nv;
@@ -915,6 +956,10 @@ int zk_setup(zk_context* ctx, const zk_r1cs* c, uint64_t toxic_seed, const char*
   for (int i = 0; i <= npub; i++) vkb.raw(&qic[(size_t)i * 8], 64);
   if (!vkb.write(vk_path)) return ctx->fail(ZK_ERR_IO, "cannot write verification key", vk_path);
   return ZK_OK;
+}
+
+int zk_setup(zk_context* ctx, const zk_r1cs* c, uint64_t toxic_seed, const char* pk_path, const char* vk_path) {
+  return zk::guard(ctx, [&] { return zk_setup_impl(ctx, c, toxic_seed, pk_path, vk_path); });
 }
 
 }  // extern "C"

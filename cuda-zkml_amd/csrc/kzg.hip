@@ -105,14 +105,19 @@ static fr fr_internal(const uint64_t mont[4]) {
 
 extern "C" {
 
-int zk_kzg_commit(zk_context* ctx, const void* d_srs_g1, const void* d_coeffs, size_t degree, void* h_commitment,
-                  void* stream) {
+static int zk_kzg_commit_impl(zk_context* ctx, const void* d_srs_g1, const void* d_coeffs, size_t degree,
+                              void* h_commitment, void* stream) {
   if (!ctx || !h_commitment || (degree && (!d_srs_g1 || !d_coeffs))) return ZK_ERR_INVALID;
   return zk::msm_g1_run(ctx, d_srs_g1, d_coeffs, degree, (uint64_t*)h_commitment, ctx->s(stream));
 }
 
-int zk_kzg_open(zk_context* ctx, const void* d_srs_g1, const void* d_coeffs, size_t degree, const uint64_t z[4],
-                void* h_proof, uint64_t f_z[4], void* stream) {
+int zk_kzg_commit(zk_context* ctx, const void* d_srs_g1, const void* d_coeffs, size_t degree, void* h_commitment,
+                  void* stream) {
+  return zk::guard(ctx, [&] { return zk_kzg_commit_impl(ctx, d_srs_g1, d_coeffs, degree, h_commitment, stream); });
+}
+
+static int zk_kzg_open_impl(zk_context* ctx, const void* d_srs_g1, const void* d_coeffs, size_t degree,
+                            const uint64_t z[4], void* h_proof, uint64_t f_z[4], void* stream) {
   using namespace zk;
   if (!ctx || !h_proof || !z || (degree && (!d_srs_g1 || !d_coeffs))) return ZK_ERR_INVALID;
   if (degree > MSM_MAX_N + 1) return ctx->fail(ZK_ERR_SIZE, "kzg: degree above the MSM limit");
@@ -152,6 +157,11 @@ int zk_kzg_open(zk_context* ctx, const void* d_srs_g1, const void* d_coeffs, siz
     memcpy(f_z, out, 32);
   }
   return msm_g1_run(ctx, d_srs_g1, q, nq, (uint64_t*)h_proof, st);
+}
+
+int zk_kzg_open(zk_context* ctx, const void* d_srs_g1, const void* d_coeffs, size_t degree, const uint64_t z[4],
+                void* h_proof, uint64_t f_z[4], void* stream) {
+  return zk::guard(ctx, [&] { return zk_kzg_open_impl(ctx, d_srs_g1, d_coeffs, degree, z, h_proof, f_z, stream); });
 }
 
 }  // extern "C"

@@ -1082,11 +1082,17 @@ static int msm_run_sets(zk_context* ctx, MsmWorkspace& ws, const BaseSets& sets,
                              st));
   ZK_HIP(ctx, hipStreamSynchronize(st));
   // window combination on the host (W * c doublings per set): one thread per set
+  int rc_fin[MSM_SETS] = {ZK_OK, ZK_OK, ZK_OK};
   auto finish = [&](int k) {
-    host_finish<F>(std::vector<xyzz<F>>(parts.begin() + (size_t)k * W, parts.begin() + (size_t)(k + 1) * W), W, 1,
-                   outs[k]);
+    try {
+      host_finish<F>(std::vector<xyzz<F>>(parts.begin() + (size_t)k * W, parts.begin() + (size_t)(k + 1) * W), W,
+                     1, outs[k]);
+    } catch (...) {
+      rc_fin[k] = ZK_ERR_OOM;
+    }
   };
   std::vector<std::thread> helpers;
+  ThreadJoiner joiner{helpers};
   for (int k = 1; k < nsets; k++) {
     try {
       helpers.emplace_back(finish, k);
@@ -1095,7 +1101,9 @@ static int msm_run_sets(zk_context* ctx, MsmWorkspace& ws, const BaseSets& sets,
     }
   }
   finish(0);
-  for (auto& t : helpers) t.join();
+  joiner.join();
+  for (int k = 0; k < nsets; k++)
+    if (rc_fin[k] != ZK_OK) return ctx->fail(rc_fin[k], "msm: host allocation failed");
   return ZK_OK;
 }
 
@@ -1209,14 +1217,24 @@ size_t rec_bytes(bool g2) { return g2 ? Rec<fq2>::WORDS * 4 : Rec<fq>::WORDS * 4
 // ------------------------------------------------------------------ C ABI
 extern "C" {
 
-int zk_msm_g1(zk_context* ctx, const void* d_points, const void* d_scalars, size_t n, void* h_result, void* stream) {
+static int zk_msm_g1_impl(zk_context* ctx, const void* d_points, const void* d_scalars, size_t n, void* h_result,
+                          void* stream) {
   if (!ctx || !h_result) return ZK_ERR_INVALID;
   return zk::msm_g1_run(ctx, d_points, d_scalars, n, (uint64_t*)h_result, ctx->s(stream));
 }
 
-int zk_msm_g2(zk_context* ctx, const void* d_points, const void* d_scalars, size_t n, void* h_result, void* stream) {
+int zk_msm_g1(zk_context* ctx, const void* d_points, const void* d_scalars, size_t n, void* h_result, void* stream) {
+  return zk::guard(ctx, [&] { return zk_msm_g1_impl(ctx, d_points, d_scalars, n, h_result, stream); });
+}
+
+static int zk_msm_g2_impl(zk_context* ctx, const void* d_points, const void* d_scalars, size_t n, void* h_result,
+                          void* stream) {
   if (!ctx || !h_result) return ZK_ERR_INVALID;
   return zk::msm_g2_run(ctx, d_points, d_scalars, n, (uint64_t*)h_result, ctx->s(stream));
+}
+
+int zk_msm_g2(zk_context* ctx, const void* d_points, const void* d_scalars, size_t n, void* h_result, void* stream) {
+  return zk::guard(ctx, [&] { return zk_msm_g2_impl(ctx, d_points, d_scalars, n, h_result, stream); });
 }
 
 int zk_msm_config(size_t n, int g2, int* window_bits, int* windows) {
@@ -1271,12 +1289,22 @@ static int msm_host_common(zk_context* ctx, const void* h_points, const void* h_
   return ZK_OK;
 }
 
-int zk_msm_g1_host(zk_context* ctx, const void* h_points, const void* h_scalars, int n, void* h_result_jacobian) {
+static int zk_msm_g1_host_impl(zk_context* ctx, const void* h_points, const void* h_scalars, int n,
+                               void* h_result_jacobian) {
   return msm_host_common(ctx, h_points, h_scalars, n, h_result_jacobian, false);
 }
 
-int zk_msm_g2_host(zk_context* ctx, const void* h_points, const void* h_scalars, int n, void* h_result_jacobian) {
+int zk_msm_g1_host(zk_context* ctx, const void* h_points, const void* h_scalars, int n, void* h_result_jacobian) {
+  return zk::guard(ctx, [&] { return zk_msm_g1_host_impl(ctx, h_points, h_scalars, n, h_result_jacobian); });
+}
+
+static int zk_msm_g2_host_impl(zk_context* ctx, const void* h_points, const void* h_scalars, int n,
+                               void* h_result_jacobian) {
   return msm_host_common(ctx, h_points, h_scalars, n, h_result_jacobian, true);
+}
+
+int zk_msm_g2_host(zk_context* ctx, const void* h_points, const void* h_scalars, int n, void* h_result_jacobian) {
+  return zk::guard(ctx, [&] { return zk_msm_g2_host_impl(ctx, h_points, h_scalars, n, h_result_jacobian); });
 }
 
 }  // extern "C"

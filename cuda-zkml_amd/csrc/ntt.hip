@@ -539,16 +539,26 @@ int quotient_pointwise(zk_context* ctx, void* d_h, const void* d_a, const void* 
 
 extern "C" {
 
-int zk_ntt(zk_context* ctx, void* d_out, const void* d_in, int log_n, int inverse, int batch, void* stream) {
+static int zk_ntt_impl(zk_context* ctx, void* d_out, const void* d_in, int log_n, int inverse, int batch,
+                       void* stream) {
   if (!ctx) return ZK_ERR_INVALID;
   return zk::ntt_run(ctx, d_out, d_in, log_n, inverse, batch, 0, ctx->s(stream));
 }
 
-int zk_coset_ntt(zk_context* ctx, void* d_out, const void* d_in, int log_n, uint64_t g, int inverse, int batch,
-                 void* stream) {
+int zk_ntt(zk_context* ctx, void* d_out, const void* d_in, int log_n, int inverse, int batch, void* stream) {
+  return zk::guard(ctx, [&] { return zk_ntt_impl(ctx, d_out, d_in, log_n, inverse, batch, stream); });
+}
+
+static int zk_coset_ntt_impl(zk_context* ctx, void* d_out, const void* d_in, int log_n, uint64_t g, int inverse,
+                             int batch, void* stream) {
   if (!ctx) return ZK_ERR_INVALID;
   if (g < 2) return ctx->fail(ZK_ERR_INVALID, "coset generator must be >= 2");
   return zk::ntt_run(ctx, d_out, d_in, log_n, inverse, batch, g, ctx->s(stream));
+}
+
+int zk_coset_ntt(zk_context* ctx, void* d_out, const void* d_in, int log_n, uint64_t g, int inverse, int batch,
+                 void* stream) {
+  return zk::guard(ctx, [&] { return zk_coset_ntt_impl(ctx, d_out, d_in, log_n, g, inverse, batch, stream); });
 }
 
 }  // extern "C"

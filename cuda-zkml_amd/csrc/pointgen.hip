@@ -180,14 +180,22 @@ int g2_generator_mul(zk_context* ctx, const void* d_scalars, size_t n, void* d_o
 
 extern "C" {
 
-int zk_g1_generator_mul(zk_context* ctx, const void* d_scalars, size_t n, void* d_out, void* stream) {
+static int zk_g1_generator_mul_impl(zk_context* ctx, const void* d_scalars, size_t n, void* d_out, void* stream) {
   if (!ctx) return ZK_ERR_INVALID;
   return zk::g1_generator_mul(ctx, d_scalars, n, d_out, ctx->s(stream));
 }
 
-int zk_g2_generator_mul(zk_context* ctx, const void* d_scalars, size_t n, void* d_out, void* stream) {
+int zk_g1_generator_mul(zk_context* ctx, const void* d_scalars, size_t n, void* d_out, void* stream) {
+  return zk::guard(ctx, [&] { return zk_g1_generator_mul_impl(ctx, d_scalars, n, d_out, stream); });
+}
+
+static int zk_g2_generator_mul_impl(zk_context* ctx, const void* d_scalars, size_t n, void* d_out, void* stream) {
   if (!ctx) return ZK_ERR_INVALID;
   return zk::g2_generator_mul(ctx, d_scalars, n, d_out, ctx->s(stream));
+}
+
+int zk_g2_generator_mul(zk_context* ctx, const void* d_scalars, size_t n, void* d_out, void* stream) {
+  return zk::guard(ctx, [&] { return zk_g2_generator_mul_impl(ctx, d_scalars, n, d_out, stream); });
 }
 
 }  // extern "C"

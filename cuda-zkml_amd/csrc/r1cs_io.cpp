@@ -19,6 +19,7 @@
 #include <random>
 #include <vector>
 
+#include "abi_guard.hpp"
 #include "../../include/zkml_gpu.h"
 #include "host_bn254.hpp"
 
@@ -207,8 +208,8 @@ void random_fr(std::mt19937_64& rng, uint64_t out[4]) {
 
 extern "C" {
 
-int zk_iden3_r1cs_info(const char* path, int* num_constraints, int* num_variables, int* num_public,
-                       int* num_private, size_t* nA, size_t* nB, size_t* nC) {
+static int zk_iden3_r1cs_info_impl(const char* path, int* num_constraints, int* num_variables, int* num_public,
+                                   int* num_private, size_t* nA, size_t* nB, size_t* nC) {
   if (!path || !num_constraints || !num_variables || !num_public || !num_private || !nA || !nB || !nC)
     return ZK_ERR_INVALID;
   std::vector<uint8_t> f;
@@ -231,7 +232,14 @@ int zk_iden3_r1cs_info(const char* path, int* num_constraints, int* num_variable
   return ZK_OK;
 }
 
-int zk_iden3_r1cs_read(const char* path, zk_sparse_entry* A, zk_sparse_entry* B, zk_sparse_entry* C) {
+int zk_iden3_r1cs_info(const char* path, int* num_constraints, int* num_variables, int* num_public,
+                       int* num_private, size_t* nA, size_t* nB, size_t* nC) {
+  return zkh::abi_guard([&] {
+    return zk_iden3_r1cs_info_impl(path, num_constraints, num_variables, num_public, num_private, nA, nB, nC);
+  });
+}
+
+static int zk_iden3_r1cs_read_impl(const char* path, zk_sparse_entry* A, zk_sparse_entry* B, zk_sparse_entry* C) {
   if (!path) return ZK_ERR_INVALID;
   std::vector<uint8_t> f;
   if (!read_file(path, f)) return ZK_ERR_IO;
@@ -248,9 +256,13 @@ int zk_iden3_r1cs_read(const char* path, zk_sparse_entry* A, zk_sparse_entry* B,
   return r1cs_constraints(s, h, out, cnt);
 }
 
-int zk_iden3_r1cs_write(const char* path, int num_constraints, int num_variables, int num_public, int num_private,
-                        const zk_sparse_entry* A, size_t nA, const zk_sparse_entry* B, size_t nB,
-                        const zk_sparse_entry* C, size_t nC) {
+int zk_iden3_r1cs_read(const char* path, zk_sparse_entry* A, zk_sparse_entry* B, zk_sparse_entry* C) {
+  return zkh::abi_guard([&] { return zk_iden3_r1cs_read_impl(path, A, B, C); });
+}
+
+static int zk_iden3_r1cs_write_impl(const char* path, int num_constraints, int num_variables, int num_public,
+                                    int num_private, const zk_sparse_entry* A, size_t nA, const zk_sparse_entry* B,
+                                    size_t nB, const zk_sparse_entry* C, size_t nC) {
   if (!path || num_constraints < 0 || num_variables <= 0 || num_public < 0 || num_private < 0 ||
       (nA && !A) || (nB && !B) || (nC && !C))
     return ZK_ERR_INVALID;
@@ -297,7 +309,15 @@ int zk_iden3_r1cs_write(const char* path, int num_constraints, int num_variables
   return write_file(path, out) ? ZK_OK : ZK_ERR_IO;
 }
 
-int zk_wtns_info(const char* path, size_t* m) {
+int zk_iden3_r1cs_write(const char* path, int num_constraints, int num_variables, int num_public, int num_private,
+                        const zk_sparse_entry* A, size_t nA, const zk_sparse_entry* B, size_t nB,
+                        const zk_sparse_entry* C, size_t nC) {
+  return zkh::abi_guard([&] {
+    return zk_iden3_r1cs_write_impl(path, num_constraints, num_variables, num_public, num_private, A, nA, B, nB, C, nC);
+  });
+}
+
+static int zk_wtns_info_impl(const char* path, size_t* m) {
   if (!path || !m) return ZK_ERR_INVALID;
   std::vector<uint8_t> f;
   if (!read_file(path, f)) return ZK_ERR_IO;
@@ -314,7 +334,11 @@ int zk_wtns_info(const char* path, size_t* m) {
   return ZK_OK;
 }
 
-int zk_wtns_read(const char* path, void* w_mont, size_t m) {
+int zk_wtns_info(const char* path, size_t* m) {
+  return zkh::abi_guard([&] { return zk_wtns_info_impl(path, m); });
+}
+
+static int zk_wtns_read_impl(const char* path, void* w_mont, size_t m) {
   size_t n = 0;
   int st = zk_wtns_info(path, &n);
   if (st != ZK_OK) return st;
@@ -329,7 +353,11 @@ int zk_wtns_read(const char* path, void* w_mont, size_t m) {
   return ZK_OK;
 }
 
-int zk_wtns_write(const char* path, const void* w_mont, size_t m) {
+int zk_wtns_read(const char* path, void* w_mont, size_t m) {
+  return zkh::abi_guard([&] { return zk_wtns_read_impl(path, w_mont, m); });
+}
+
+static int zk_wtns_write_impl(const char* path, const void* w_mont, size_t m) {
   if (!path || (m && !w_mont) || m > 0xffffffffu) return ZK_ERR_INVALID;
   const uint64_t* w = (const uint64_t*)w_mont;
   std::vector<uint8_t> hdr, vals, out;
@@ -345,8 +373,13 @@ int zk_wtns_write(const char* path, const void* w_mont, size_t m) {
   return write_file(path, out) ? ZK_OK : ZK_ERR_IO;
 }
 
-int zk_synthetic_r1cs(int num_constraints, int num_public, int num_inputs, uint64_t seed, zk_sparse_entry* A,
-                      size_t* nA, zk_sparse_entry* B, size_t* nB, zk_sparse_entry* C, size_t* nC, void* w_mont) {
+int zk_wtns_write(const char* path, const void* w_mont, size_t m) {
+  return zkh::abi_guard([&] { return zk_wtns_write_impl(path, w_mont, m); });
+}
+
+static int zk_synthetic_r1cs_impl(int num_constraints, int num_public, int num_inputs, uint64_t seed,
+                                  zk_sparse_entry* A, size_t* nA, zk_sparse_entry* B, size_t* nB, zk_sparse_entry* C,
+                                  size_t* nC, void* w_mont) {
   if (num_constraints < 0 || num_public < 0 || num_inputs < 0 || !nA || !nB || !nC || !w_mont ||
       (num_constraints > 0 && (!A || !B || !C)))
     return ZK_ERR_INVALID;
@@ -383,6 +416,13 @@ int zk_synthetic_r1cs(int num_constraints, int num_public, int num_inputs, uint6
   *nB = kb;
   *nC = kc;
   return ZK_OK;
+}
+
+int zk_synthetic_r1cs(int num_constraints, int num_public, int num_inputs, uint64_t seed, zk_sparse_entry* A,
+                      size_t* nA, zk_sparse_entry* B, size_t* nB, zk_sparse_entry* C, size_t* nC, void* w_mont) {
+  return zkh::abi_guard([&] {
+    return zk_synthetic_r1cs_impl(num_constraints, num_public, num_inputs, seed, A, nA, B, nB, C, nC, w_mont);
+  });
 }
 
 }  // extern "C"

@@ -29,6 +29,7 @@
 #include <utility>
 #include <vector>
 
+#include "abi_guard.hpp"
 #include "../../include/zkml_gpu.h"
 #include "host_bn254.hpp"
 #include "poseidon.hpp"
@@ -398,7 +399,7 @@ struct zk_statement {
 
 extern "C" {
 
-int zk_poseidon_permute(uint64_t state[12]) {
+static int zk_poseidon_permute_impl(uint64_t state[12]) {
   if (!state) return ZK_ERR_INVALID;
   Fr s[3];
   for (int i = 0; i < 3; i++) s[i] = fr_std4(state + 4 * i);
@@ -407,13 +408,21 @@ int zk_poseidon_permute(uint64_t state[12]) {
   return ZK_OK;
 }
 
-int zk_poseidon_hash2(const uint64_t a[4], const uint64_t b[4], uint64_t out[4]) {
+int zk_poseidon_permute(uint64_t state[12]) {
+  return zkh::abi_guard([&] { return zk_poseidon_permute_impl(state); });
+}
+
+static int zk_poseidon_hash2_impl(const uint64_t a[4], const uint64_t b[4], uint64_t out[4]) {
   if (!a || !b || !out) return ZK_ERR_INVALID;
   zkh::poseidon_hash2(fr_std4(a), fr_std4(b)).to_std(out);
   return ZK_OK;
 }
 
-int zk_poseidon_commit(const uint64_t* values, size_t n, uint64_t domain, uint64_t out[4]) {
+int zk_poseidon_hash2(const uint64_t a[4], const uint64_t b[4], uint64_t out[4]) {
+  return zkh::abi_guard([&] { return zk_poseidon_hash2_impl(a, b, out); });
+}
+
+static int zk_poseidon_commit_impl(const uint64_t* values, size_t n, uint64_t domain, uint64_t out[4]) {
   if ((n && !values) || !out) return ZK_ERR_INVALID;
   std::vector<Fr> v(n);
   for (size_t i = 0; i < n; i++) v[i] = fr_std4(values + 4 * i);
@@ -421,7 +430,11 @@ int zk_poseidon_commit(const uint64_t* values, size_t n, uint64_t domain, uint64
   return ZK_OK;
 }
 
-int zk_poseidon_constants(uint64_t* round_constants, uint64_t* mds) {
+int zk_poseidon_commit(const uint64_t* values, size_t n, uint64_t domain, uint64_t out[4]) {
+  return zkh::abi_guard([&] { return zk_poseidon_commit_impl(values, n, domain, out); });
+}
+
+static int zk_poseidon_constants_impl(uint64_t* round_constants, uint64_t* mds) {
   const Poseidon& P = Poseidon::get();
   if (round_constants)
     for (int i = 0; i < Poseidon::NRC; i++) P.rc[i].to_std(round_constants + 4 * i);
@@ -431,8 +444,13 @@ int zk_poseidon_constants(uint64_t* round_constants, uint64_t* mds) {
   return ZK_OK;
 }
 
-int zk_statement_v2_build(const zk_layer* layers, int num_layers, const int64_t* inputs, int batch, int n_in,
-                          const zk_statement_options* options, zk_statement** out, char* err, size_t err_cap) {
+int zk_poseidon_constants(uint64_t* round_constants, uint64_t* mds) {
+  return zkh::abi_guard([&] { return zk_poseidon_constants_impl(round_constants, mds); });
+}
+
+static int zk_statement_v2_build_impl(const zk_layer* layers, int num_layers, const int64_t* inputs, int batch,
+                                      int n_in, const zk_statement_options* options, zk_statement** out, char* err,
+                                      size_t err_cap) {
   if (!out || (num_layers > 0 && !layers) || num_layers < 0 || n_in < 0) {
     set_err(err, err_cap, "invalid argument");
     return ZK_ERR_INVALID;
@@ -700,10 +718,17 @@ int zk_statement_v2_build(const zk_layer* layers, int num_layers, const int64_t*
   return ZK_OK;
 }
 
+int zk_statement_v2_build(const zk_layer* layers, int num_layers, const int64_t* inputs, int batch, int n_in,
+                          const zk_statement_options* options, zk_statement** out, char* err, size_t err_cap) {
+  return zkh::abi_guard([&] {
+    return zk_statement_v2_build_impl(layers, num_layers, inputs, batch, n_in, options, out, err, err_cap);
+  });
+}
+
 void zk_statement_destroy(zk_statement* st) { delete st; }
 
-int zk_statement_info(const zk_statement* st, int* num_constraints, int* num_variables, int* num_public,
-                      int* num_private, size_t* nA, size_t* nB, size_t* nC) {
+static int zk_statement_info_impl(const zk_statement* st, int* num_constraints, int* num_variables, int* num_public,
+                                  int* num_private, size_t* nA, size_t* nB, size_t* nC) {
   if (!st) return ZK_ERR_INVALID;
   if (num_constraints) *num_constraints = st->nc;
   if (num_variables) *num_variables = st->nv;
@@ -715,13 +740,24 @@ int zk_statement_info(const zk_statement* st, int* num_constraints, int* num_var
   return ZK_OK;
 }
 
-int zk_statement_layout(const zk_statement* st, int32_t layout[ZK_STATEMENT_LAYOUT_WORDS]) {
+int zk_statement_info(const zk_statement* st, int* num_constraints, int* num_variables, int* num_public,
+                      int* num_private, size_t* nA, size_t* nB, size_t* nC) {
+  return zkh::abi_guard([&] {
+    return zk_statement_info_impl(st, num_constraints, num_variables, num_public, num_private, nA, nB, nC);
+  });
+}
+
+static int zk_statement_layout_impl(const zk_statement* st, int32_t layout[ZK_STATEMENT_LAYOUT_WORDS]) {
   if (!st || !layout) return ZK_ERR_INVALID;
   memcpy(layout, st->layout, sizeof(st->layout));
   return ZK_OK;
 }
 
-int zk_statement_r1cs(const zk_statement* st, zk_sparse_entry* A, zk_sparse_entry* B, zk_sparse_entry* C) {
+int zk_statement_layout(const zk_statement* st, int32_t layout[ZK_STATEMENT_LAYOUT_WORDS]) {
+  return zkh::abi_guard([&] { return zk_statement_layout_impl(st, layout); });
+}
+
+static int zk_statement_r1cs_impl(const zk_statement* st, zk_sparse_entry* A, zk_sparse_entry* B, zk_sparse_entry* C) {
   if (!st || (!st->A.empty() && !A) || (!st->B.empty() && !B) || (!st->C.empty() && !C)) return ZK_ERR_INVALID;
   if (!st->A.empty()) memcpy(A, st->A.data(), st->A.size() * sizeof(zk_sparse_entry));
   if (!st->B.empty()) memcpy(B, st->B.data(), st->B.size() * sizeof(zk_sparse_entry));
@@ -729,21 +765,33 @@ int zk_statement_r1cs(const zk_statement* st, zk_sparse_entry* A, zk_sparse_entr
   return ZK_OK;
 }
 
-int zk_statement_witness(const zk_statement* st, void* w_mont) {
+int zk_statement_r1cs(const zk_statement* st, zk_sparse_entry* A, zk_sparse_entry* B, zk_sparse_entry* C) {
+  return zkh::abi_guard([&] { return zk_statement_r1cs_impl(st, A, B, C); });
+}
+
+static int zk_statement_witness_impl(const zk_statement* st, void* w_mont) {
   if (!st || !w_mont) return ZK_ERR_INVALID;
   memcpy(w_mont, st->w.data(), st->w.size() * 32);
   return ZK_OK;
 }
 
-int zk_statement_scores(const zk_statement* st, int64_t* scores) {
+int zk_statement_witness(const zk_statement* st, void* w_mont) {
+  return zkh::abi_guard([&] { return zk_statement_witness_impl(st, w_mont); });
+}
+
+static int zk_statement_scores_impl(const zk_statement* st, int64_t* scores) {
   if (!st || !scores) return ZK_ERR_INVALID;
   memcpy(scores, st->scores.data(), st->scores.size() * sizeof(int64_t));
   return ZK_OK;
 }
 
+int zk_statement_scores(const zk_statement* st, int64_t* scores) {
+  return zkh::abi_guard([&] { return zk_statement_scores_impl(st, scores); });
+}
+
 // (A w) o (B w) = C w on the host (reference R1CS::verify_witness,
 // src/prover/circuit.cuh:92-124)
-int zk_statement_check(const zk_statement* st) {
+static int zk_statement_check_impl(const zk_statement* st) {
   if (!st) return ZK_ERR_INVALID;
   std::vector<Fr> acc[3];
   const std::vector<zk_sparse_entry>* m[3] = {&st->A, &st->B, &st->C};
@@ -759,7 +807,11 @@ int zk_statement_check(const zk_statement* st) {
   return ZK_OK;
 }
 
-int zk_statement_write(const zk_statement* st, const char* r1cs_path, const char* wtns_path) {
+int zk_statement_check(const zk_statement* st) {
+  return zkh::abi_guard([&] { return zk_statement_check_impl(st); });
+}
+
+static int zk_statement_write_impl(const zk_statement* st, const char* r1cs_path, const char* wtns_path) {
   if (!st) return ZK_ERR_INVALID;
   if (r1cs_path) {
     const int rc = zk_iden3_r1cs_write(r1cs_path, st->nc, st->nv, st->npub, st->npriv, st->A.data(), st->A.size(),
@@ -770,8 +822,13 @@ int zk_statement_write(const zk_statement* st, const char* r1cs_path, const char
   return ZK_OK;
 }
 
+int zk_statement_write(const zk_statement* st, const char* r1cs_path, const char* wtns_path) {
+  return zkh::abi_guard([&] { return zk_statement_write_impl(st, r1cs_path, wtns_path); });
+}
+
 // statement_v2_meta_json (statement_v2.cuh:255-287), same keys and layout
-int zk_statement_meta_json(const zk_statement* st, uint64_t model_tag64, char* buf, size_t cap, size_t* len) {
+static int zk_statement_meta_json_impl(const zk_statement* st, uint64_t model_tag64, char* buf, size_t cap,
+                                       size_t* len) {
   if (!st) return ZK_ERR_INVALID;
   const int32_t* L = st->layout;
   char tag[32];
@@ -811,6 +868,10 @@ int zk_statement_meta_json(const zk_statement* st, uint64_t model_tag64, char* b
     if (o.size() >= cap) return ZK_ERR_SIZE;
   }
   return ZK_OK;
+}
+
+int zk_statement_meta_json(const zk_statement* st, uint64_t model_tag64, char* buf, size_t cap, size_t* len) {
+  return zkh::abi_guard([&] { return zk_statement_meta_json_impl(st, model_tag64, buf, cap, len); });
 }
 
 }  // extern "C"

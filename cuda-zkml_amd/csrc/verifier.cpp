@@ -12,6 +12,7 @@
 #include <string>
 #include <vector>
 
+#include "abi_guard.hpp"
 #include "../../include/zkml_gpu.h"
 #include "pairing_host.hpp"
 
@@ -116,7 +117,7 @@ bool ends_with_json(const char* path) {
 
 extern "C" {
 
-int zk_pairing(const void* p_std, const void* q_std, void* out_std) {
+static int zk_pairing_impl(const void* p_std, const void* q_std, void* out_std) {
   if (!p_std || !q_std || !out_std) return ZK_ERR_INVALID;
   const Fq12 f = pairing(g1_std((const uint8_t*)p_std), g2_std((const uint8_t*)q_std));
   const Fq2* c[6] = {&f.c0.c0, &f.c0.c1, &f.c0.c2, &f.c1.c0, &f.c1.c1, &f.c1.c2};
@@ -128,8 +129,12 @@ int zk_pairing(const void* p_std, const void* q_std, void* out_std) {
   return ZK_OK;
 }
 
-int zk_verify(const void* vk_bytes, size_t vk_len, const void* proof256, const void* publics_std, int npub,
-              int* valid) {
+int zk_pairing(const void* p_std, const void* q_std, void* out_std) {
+  return zkh::abi_guard([&] { return zk_pairing_impl(p_std, q_std, out_std); });
+}
+
+static int zk_verify_impl(const void* vk_bytes, size_t vk_len, const void* proof256, const void* publics_std, int npub,
+                          int* valid) {
   if (!vk_bytes || !proof256 || !valid || npub < 0 || (npub > 0 && !publics_std)) return ZK_ERR_INVALID;
   *valid = 0;
   VerifyingKey vk;
@@ -146,7 +151,12 @@ int zk_verify(const void* vk_bytes, size_t vk_len, const void* proof256, const v
   return ZK_OK;
 }
 
-int zk_verify_files(const char* vk_path, const char* proof_path, const char* publics_path, int* valid) {
+int zk_verify(const void* vk_bytes, size_t vk_len, const void* proof256, const void* publics_std, int npub,
+              int* valid) {
+  return zkh::abi_guard([&] { return zk_verify_impl(vk_bytes, vk_len, proof256, publics_std, npub, valid); });
+}
+
+static int zk_verify_files_impl(const char* vk_path, const char* proof_path, const char* publics_path, int* valid) {
   if (!vk_path || !proof_path || !publics_path || !valid) return ZK_ERR_INVALID;
   *valid = 0;
   std::vector<uint8_t> vkb, prb, pubb;
@@ -169,6 +179,10 @@ int zk_verify_files(const char* vk_path, const char* proof_path, const char* pub
   std::vector<uint8_t> flat(pub.size() * 32);
   for (size_t i = 0; i < pub.size(); i++) memcpy(flat.data() + 32 * i, pub[i].data(), 32);
   return zk_verify(vkb.data(), vkb.size(), prb.data(), flat.data(), (int)pub.size(), valid);
+}
+
+int zk_verify_files(const char* vk_path, const char* proof_path, const char* publics_path, int* valid) {
+  return zkh::abi_guard([&] { return zk_verify_files_impl(vk_path, proof_path, publics_path, valid); });
 }
 
 }  // extern "C"

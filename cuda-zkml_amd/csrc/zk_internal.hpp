@@ -8,6 +8,7 @@
 #include <memory>
 #include <mutex>
 #include <string>
+#include <thread>
 #include <vector>
 
 #include "../../include/zkml_gpu.h"
@@ -98,6 +99,39 @@ struct zk_context {
 };
 
 namespace zk {
+
+// Joins every thread of `v` on join() and when it goes out of scope, so no
+// path out of a function leaves a joinable std::thread behind.
+struct ThreadJoiner {
+  std::vector<std::thread>& v;
+  void join() {
+    for (auto& t : v)
+      if (t.joinable()) t.join();
+  }
+  ~ThreadJoiner() { join(); }
+};
+
+// Body of a C entry point: a C++ exception (a failed host allocation, mostly)
+// becomes a status instead of crossing the C ABI.
+template <class Fn>
+int guard(zk_context* ctx, Fn&& fn) noexcept {
+  int code = ZK_ERR_INVALID;
+  const char* what = "internal error";
+  try {
+    return fn();
+  } catch (const std::bad_alloc&) {
+    code = ZK_ERR_OOM;
+    what = "host allocation failed";
+  } catch (...) {
+  }
+  if (ctx) {
+    try {
+      return ctx->fail(code, what);
+    } catch (...) {
+    }
+  }
+  return code;
+}
 
 // Issue priority of the quotient's kernels (sparse products, NTTs, pointwise
 // step).  In a proof they run beside the G2 MSM's accumulation and the H MSM
