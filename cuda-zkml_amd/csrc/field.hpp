@@ -306,6 +306,21 @@ ZK_HD fe<P> fdbl(const fe<P>& a) {
   return fadd(a, a);
 }
 
+// a + b with carries and no reduction: normalized limbs, value in [0, 4m) for
+// a, b in [0, 2m).
+template <class P>
+ZK_HD fe<P> fadd_wide(const fe<P>& a, const fe<P>& b) {
+  fe<P> s;
+  uint32_t c = 0;
+#pragma unroll
+  for (int i = 0; i < NL; i++) {
+    uint32_t v = a.l[i] + b.l[i] + c;
+    c = v >> 29;
+    s.l[i] = v & LMASK;
+  }
+  return s;
+}
+
 // Limb-wise sum without normalization: limbs < 2^30, value < 4m.  Valid only
 // as a direct input of fmul/fsqr.
 template <class P>

@@ -127,6 +127,13 @@ __device__ __forceinline__ fr tw_get(const TwView& tw, int idx) {
 // stages per LDS round trip (a radix-2^2 step on four rows held in
 // registers), a single radix-2 stage first when log2 R is odd.  tw: w_R^t,
 // t < R/2, in LDS.
+//
+// Butterflies are lazy (Harvey's form): a stage's inputs lie in [0, 4m); the
+// untwiddled operand X is brought below 2m by one conditional subtraction,
+// the twiddled one T is an fmul output (< 2m), and the stage writes X + T and
+// X - T + 2m, both in [0, 4m) with normalized limbs.  The first stage's
+// inputs are below 2m (canonical loads or fmul outputs) and need no
+// subtraction.  Results leave in [0, 4m).
 __device__ __forceinline__ void tile_dit(uint32_t* s, const TwView& tw, int logR, int T) {
   const int R = 1 << logR;
   int st = 0;
@@ -135,8 +142,8 @@ __device__ __forceinline__ void tile_dit(uint32_t* s, const TwView& tw, int logR
       const int c = b % T, g = b / T;
       const int i0 = (2 * g) * T + c, i1 = i0 + T;
       const fr x0 = lds_get(s, i0), x1 = lds_get(s, i1);
-      lds_put(s, i0, fadd(x0, x1));
-      lds_put(s, i1, fsub(x0, x1));
+      lds_put(s, i0, fadd_wide(x0, x1));
+      lds_put(s, i1, fsub_lazy(x0, x1));
     }
     __syncthreads();
     st = 1;
@@ -150,18 +157,23 @@ __device__ __forceinline__ void tile_dit(uint32_t* s, const TwView& tw, int logR
       const int j0 = ((q >> st) << (st + 2)) + k;
       const int i0 = j0 * T + c, i1 = i0 + h * T, i2 = i1 + h * T, i3 = i2 + h * T;
       fr x0 = lds_get(s, i0), x1 = lds_get(s, i1), x2 = lds_get(s, i2), x3 = lds_get(s, i3);
-      if (k != 0) {
-        const fr w2 = tw_get(tw, 2 * k * tq);  // w_{2h}^k
-        x1 = fmul(x1, w2);
-        x3 = fmul(x3, w2);
+      fr t1 = x1, t3 = x3;  // h == 1: the first stage, inputs below 2m, twiddle 1
+      if (h > 1) {
+        const fr w2 = tw_get(tw, 2 * k * tq);  // w_{2h}^k (w^0 is the table's one)
+        t1 = fmul(x1, w2);
+        t3 = fmul(x3, w2);
+        x0 = fcsub(x0, FrP::MOD2);
+        x2 = fcsub(x2, FrP::MOD2);
       }
-      const fr y0 = fadd(x0, x1), y1 = fsub(x0, x1), y2 = fadd(x2, x3), y3 = fsub(x2, x3);
-      const fr z2 = k != 0 ? fmul(y2, tw_get(tw, k * tq)) : y2;  // w_{4h}^k
-      const fr z3 = fmul(y3, tw_get(tw, (k + h) * tq));           // w_{4h}^(k+h)
-      lds_put(s, i0, fadd(y0, z2));
-      lds_put(s, i2, fsub(y0, z2));
-      lds_put(s, i1, fadd(y1, z3));
-      lds_put(s, i3, fsub(y1, z3));
+      const fr y0 = fadd_wide(x0, t1), y1 = fsub_lazy(x0, t1);
+      const fr y2 = fadd_wide(x2, t3), y3 = fsub_lazy(x2, t3);
+      const fr z2 = h > 1 ? fmul(y2, tw_get(tw, k * tq)) : fcsub(y2, FrP::MOD2);  // w_{4h}^k
+      const fr z3 = fmul(y3, tw_get(tw, (k + h) * tq));                           // w_{4h}^(k+h)
+      const fr u0 = fcsub(y0, FrP::MOD2), u1 = fcsub(y1, FrP::MOD2);
+      lds_put(s, i0, fadd_wide(u0, z2));
+      lds_put(s, i2, fsub_lazy(u0, z2));
+      lds_put(s, i1, fadd_wide(u1, z3));
+      lds_put(s, i3, fsub_lazy(u1, z3));
     }
     __syncthreads();
   }
@@ -211,6 +223,7 @@ __global__ __launch_bounds__(NTT_THREADS) void k_ntt_pass_mid(uint4* __restrict_
     const size_t rel = (size_t)k * a.S + m0 + c;
     fr x = lds_get(s, k * T + c);
     if (k != 0 && (m0 + c) != 0) x = fmul(x, load_table(twp, twp_count, rel));
+    else x = fcsub(x, FrP::MOD2);
     store_elem(dst, ubase + rel, x);
   }
 }
@@ -253,6 +266,7 @@ __global__ __launch_bounds__(NTT_THREADS) void k_ntt_pass_last(uint4* __restrict
     fr x = lds_get(s, k * T + c);
     if (post) x = fmul(x, load_table(post, a.n, out));
     else if (scale_en) x = fmul(x, scale);
+    else x = fcsub(x, FrP::MOD2);
     store_elem(dst, out, x);
   }
 }

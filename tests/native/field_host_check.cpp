@@ -39,6 +39,8 @@ int fh_op(int op, const uint32_t* a, const uint32_t* b, const uint32_t* c, const
     case 11: r = fneg_lazy4<FqP>(A); break;
     case 12: r = fe_zero<FqP>(); r.l[0] = fis_zero<FqP>(A) ? 1u : 0u; break;
     case 13: r = fe_zero<FqP>(); r.l[0] = fis_zero4<FqP>(A) ? 1u : 0u; break;
+    case 14: r = fadd_wide(A, B); break;
+    case 15: r = fcsub(A, FqP::MOD2); break;
     case 8: {  // four products: a*b + c*d + a*d + c*b
       const fq x[4] = {A, C, A, C}, y[4] = {B, D, D, B};
       r = fmul_sum<FqP, 4>(x, y);
@@ -47,6 +49,23 @@ int fh_op(int op, const uint32_t* a, const uint32_t* b, const uint32_t* c, const
     default: return -1;
   }
   st(out, r);
+  return 0;
+}
+
+// The NTT butterfly's Fr operations (the same templates over the scalar
+// field): 0 fmul, 1 fadd_wide, 2 fcsub(a, 2r), 3 fsub_lazy (a + 2r - b).
+int fh_fr_op(int op, const uint32_t* a, const uint32_t* b, uint32_t* out) {
+  fr A, B, r;
+  memcpy(A.l, a, sizeof(A.l));
+  memcpy(B.l, b, sizeof(B.l));
+  switch (op) {
+    case 0: r = fmul(A, B); break;
+    case 1: r = fadd_wide(A, B); break;
+    case 2: r = fcsub(A, FrP::MOD2); break;
+    case 3: r = fsub_lazy(A, B); break;
+    default: return -1;
+  }
+  memcpy(out, r.l, sizeof(r.l));
   return 0;
 }
 

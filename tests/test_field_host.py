@@ -10,6 +10,8 @@ limb, carry or range assumption fails here before any kernel runs:
   fsub_lazy / fneg_lazy   exact a - b + 2q and 2q - a (and the 4q forms)
   fsub3, fis_zero(4)      a - b - 2c into [0, 2q); zero tests over [0, 2q) / [0, 4q)
   fadd / fsub / fmul_sub  congruence and the [0, 2q) output range
+  fadd_wide / fcsub       exact a + b below 4q; a - 2q when a >= 2q
+  NTT lazy butterfly      over Fr: X, Y in [0, 4r) give X' +- Y*w in [0, 4r)
   XYZZ madd/add/dbl/mdbl  G1 and G2 against affine formulas, with coordinates
                           given in non-canonical [q, 2q) representatives and
                           random Z, plus the doubling / inverse / infinity cases
@@ -38,6 +40,7 @@ def fh(tmp_path_factory):
     lib = ctypes.CDLL(str(so))
     lib.fh_op.restype = ctypes.c_int
     lib.fh_xyzz.restype = ctypes.c_int
+    lib.fh_fr_op.restype = ctypes.c_int
     return lib
 
 
@@ -125,6 +128,46 @@ def test_fused_sub_lazy4_zero_tests(fh):
         assert op(fh, 12, a) == (1 if a % Q == 0 else 0)
     for a in [0, Q, 2 * Q, 3 * Q, 1, 2 * Q + 1, 3 * Q - 1, 4 * Q - 1] + [rng.randrange(4 * Q) for _ in range(50)]:
         assert op(fh, 13, a) == (1 if a % Q == 0 else 0)
+
+
+def test_wide_add_and_conditional_subtract(fh):
+    rng = random.Random(11)
+    for a in samples(rng, 2 * Q):
+        for b in samples(rng, 2 * Q, 4):
+            assert op(fh, 14, a, b) == a + b  # exact, below 4q
+    for a in samples(rng, 4 * Q, 60) + [2 * Q, 2 * Q - 1, 2 * Q + 1, 4 * Q - 1]:
+        assert op(fh, 15, a) == (a - 2 * Q if a >= 2 * Q else a)
+
+
+def fr_op(fh, code, a, b=0):
+    out = U32x9()
+    assert fh.fh_fr_op(code, U32x9(*to_l(a)), U32x9(*to_l(b)), out) == 0
+    ws = list(out)
+    assert all(w < 1 << 29 for w in ws), "limb not normalized"
+    return from_l(ws)
+
+
+def test_ntt_lazy_butterfly_bounds(fh):
+    """The NTT's lazy radix-2 step: inputs X, Y in [0, 4r), a canonical
+    twiddle w; T = Y*w (Montgomery), X' = X mod 2r, outputs X' + T and
+    X' - T + 2r must stay in [0, 4r) and be congruent to X +- Y*w/R'."""
+    rng = random.Random(12)
+    r = ORDER
+    rinv = pow(RP, -1, r)
+    edge = [0, 1, r - 1, r, 2 * r - 1, 2 * r, 3 * r, 4 * r - 1]
+    xs = edge + [rng.randrange(4 * r) for _ in range(40)]
+    ws = [0, 1, r - 1] + [rng.randrange(r) for _ in range(8)]
+    for x in xs:
+        for y in xs[:12]:
+            w = rng.choice(ws)
+            t = fr_op(fh, 0, y, w)
+            assert t < 2 * r and t % r == y * w * rinv % r
+            xc = fr_op(fh, 2, x)
+            assert xc == (x - 2 * r if x >= 2 * r else x)
+            s, d = fr_op(fh, 1, xc, t), fr_op(fh, 3, xc, t)
+            assert s == xc + t and s < 4 * r
+            assert d == xc + 2 * r - t and 0 < d < 4 * r
+            assert (s - x - y * w * rinv) % r == 0 and (d - x + y * w * rinv) % r == 0
 
 
 def test_add_sub_mulsub(fh):
