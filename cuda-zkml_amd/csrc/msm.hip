@@ -33,6 +33,7 @@
 #include <stdlib.h>
 
 #include <algorithm>
+#include <numeric>
 #include <thread>
 #include <vector>
 
@@ -520,6 +521,13 @@ struct BaseSets {
 // Chunk ch covers sorted positions [ch*L0, ch*L0 + L0) of window
 // ch / chunks_per_window; positions past the window's entry count are empty.
 // blockIdx.y selects the base set; its buckets start at set * nbuckets.
+//
+// Waves are scattered over the chunk space: wave v of the grid takes the 64
+// chunks of chunk-wave (v * wave_mul) mod nwaves (wave_mul coprime to
+// nwaves, so every chunk is taken once).  With skewed scalars most entries
+// sit in a few windows (small witness values fill the low ones); in chunk
+// order those windows' waves would land on a fraction of the CUs, scattered
+// they spread over all of them.
 template <class F>
 __global__ __launch_bounds__(256) void k_msm_accumulate(const uint2* __restrict__ sorted, BaseSets sets,
                                                         const uint32_t* __restrict__ start,
@@ -527,9 +535,12 @@ __global__ __launch_bounds__(256) void k_msm_accumulate(const uint2* __restrict_
                                                         const uint32_t* __restrict__ wstat, uint32_t nchunks,
                                                         uint32_t chunks_per_window, uint32_t n_pad, uint32_t L0,
                                                         size_t nbuckets, xyzz<F>* __restrict__ buckets,
-                                                        ChunkSlots<F> all_slots) {
+                                                        ChunkSlots<F> all_slots, uint32_t nwaves,
+                                                        uint32_t wave_mul) {
   msm_accumulate_priority<F>();
-  const uint32_t ch = blockIdx.x * blockDim.x + threadIdx.x;
+  const uint32_t tid = blockIdx.x * blockDim.x + threadIdx.x;
+  if ((tid >> 6) >= nwaves) return;
+  const uint32_t ch = (uint32_t)((uint64_t)(tid >> 6) * wave_mul % nwaves) * 64 + (tid & 63);
   if (ch >= nchunks) return;
   const uint32_t set = blockIdx.y;
   const uint4* __restrict__ recs = sets.recs[set];
@@ -840,6 +851,16 @@ void msm_workspace_free(MsmWorkspace* ws) {
   delete ws;
 }
 
+// Multiplier of the accumulation's wave scatter: coprime to nwaves (so
+// v -> v * m mod nwaves is a permutation) and near nwaves / golden ratio, so
+// that consecutive waves land far apart in the chunk space.
+static uint32_t wave_scatter(uint32_t nwaves) {
+  if (nwaves <= 2) return 1;
+  uint32_t m = (uint32_t)(nwaves * 0.6180339887) | 1u;
+  while (std::gcd(m, nwaves) != 1) m += 2;
+  return m % nwaves;
+}
+
 // Window size by input size (index: ceil(log2 n)), from measurements on
 // gfx950 with uniform scalars.  Below ~2^19 points the accumulation and the
 // bucket reduction are latency-bound, so fewer buckets pay off well beyond
@@ -1028,8 +1049,9 @@ static int msm_run_sets(zk_context* ctx, MsmWorkspace& ws, const BaseSets& sets,
   ChunkSlots<F> slots{(uint32_t*)ws.hkey.p, (uint32_t*)ws.tkey.p, (xyzz<F>*)ws.hpt.p, (xyzz<F>*)ws.tpt.p};
   const uint32_t gx = cdiv(nchunks, 256);
   const uint32_t gxl = cdiv((size_t)nchunks * Lanes<F>::N, 256);  // combine: Lanes<F>::N lanes per chunk
+  const uint32_t nwaves = cdiv(nchunks, 64);
   ZK_LAUNCH(ctx, st, "msm_accumulate", k_msm_accumulate<F>, dim3(gx, nsets), dim3(256), 0, sorted, sets, start, end,
-            wstat, nchunks, cpw, n_pad, L0, nbuckets, buckets, slots);
+            wstat, nchunks, cpw, n_pad, L0, nbuckets, buckets, slots, nwaves, wave_scatter(nwaves));
   // the largest bucket decides the depth of the chunk-combine tree; its
   // read-back overlaps the accumulation
   ZK_HIP(ctx, hipEventSynchronize(ws.stat_ready));
