@@ -967,24 +967,10 @@ static int msm_run_sets(zk_context* ctx, MsmWorkspace& ws, const BaseSets& sets,
   const int W = (MSM_BITS + c - 1) / c;
   const uint32_t B = 1u << (c - 1);  // buckets per window
   const size_t nbuckets = (size_t)W * B;
-  // entries per accumulation thread, by the entry count W*n: short chunks
-  // give small MSMs enough threads (a thread's chunk is a serial chain of
-  // additions), long chunks keep the chunk-combine tree of large ones shallow.
-  // Measured on MI355X over 2^10 .. 2^20 points, G1 and G2, uniform and
-  // witness-like scalars.
-  // Beside other kernels (see msm_recs_ws) a G1 chunk below the longest is
-  // one step shorter (measured in the 2^16 proof: 1.97 -> 1.87 ms; the 2^22
-  // proof's MSMs keep the longest chunks, shorter ones cost it 2 ms).
-  const size_t entries = (size_t)W * n;
-  const uint32_t L0_alone = entries >= ((size_t)1 << 23)   ? MSM_L0
-                            : entries >= ((size_t)1 << 20) ? MSM_L0 / 2
-                            : entries >= ((size_t)1 << 18) ? MSM_L0 / 4
-                                                           : MSM_L0 / 8;
-  const uint32_t L0 =
-      beside && !G2 && L0_alone < (uint32_t)MSM_L0 ? std::max<uint32_t>(L0_alone / 2, MSM_L0 / 8) : L0_alone;
-  const uint32_t n_pad = (uint32_t)((n + L0 - 1) / L0 * L0);
-  const uint32_t cpw = n_pad / L0;  // chunks per window
-  const uint32_t nchunks = cpw * (uint32_t)W;
+  // window regions of the sorted list are padded to the longest chunk, so
+  // every chunk length divides them (the length is chosen after the sort's
+  // counts are known)
+  const uint32_t n_pad = (uint32_t)((n + MSM_L0 - 1) / MSM_L0 * MSM_L0);
   // slices per window: about 256 blocks, each slice at least B points
   uint32_t S = (uint32_t)std::max<size_t>(1, std::min<size_t>({(size_t)cdiv(256, W), (size_t)64, n / B}));
   const uint32_t slice = (uint32_t)cdiv(n, S);
@@ -1000,10 +986,6 @@ static int msm_run_sets(zk_context* ctx, MsmWorkspace& ws, const BaseSets& sets,
   ZK_TRY(ctx->ensure(ws.end, nbuckets * 4));
   ZK_TRY(ctx->ensure(ws.wstat, (size_t)W * 8));
   ZK_TRY(ctx->ensure(ws.buckets, nsets * nbuckets * sizeof(xyzz<F>)));
-  ZK_TRY(ctx->ensure(ws.hkey, (size_t)nsets * nchunks * 4));
-  ZK_TRY(ctx->ensure(ws.tkey, (size_t)nsets * nchunks * 4));
-  ZK_TRY(ctx->ensure(ws.hpt, (size_t)nsets * nchunks * sizeof(xyzz<F>)));
-  ZK_TRY(ctx->ensure(ws.tpt, (size_t)nsets * nchunks * sizeof(xyzz<F>)));
   if (!ws.h_stat) ZK_HIP(ctx, hipHostMalloc((void**)&ws.h_stat, 2 * 32 * 4, hipHostMallocDefault));
   if (!ws.stat_ready) ZK_HIP(ctx, hipEventCreateWithFlags(&ws.stat_ready, hipEventDisableTiming));
 
@@ -1046,17 +1028,48 @@ static int msm_run_sets(zk_context* ctx, MsmWorkspace& ws, const BaseSets& sets,
               sorted);
   }
 
+  // The windows' entry counts and largest buckets come back while the scatter
+  // and placement run.  Entries per accumulation thread, by the entry count
+  // (G1: zero digits are no entries, so skewed scalars, such as a witness of
+  // small values, count for less than W*n): short chunks give small MSMs
+  // enough threads (a thread's chunk is a serial chain of additions), long
+  // chunks keep the chunk-combine tree of large ones shallow.  Measured on
+  // MI355X over 2^10 .. 2^20 points, G1 and G2, uniform and witness-like
+  // scalars.  Beside other kernels (see msm_recs_ws) a G1 chunk below the
+  // longest is one step shorter (measured in the 2^16 proof: 1.97 -> 1.87 ms;
+  // the 2^22 proof's MSMs keep the longest chunks, shorter ones cost it 2 ms).
+  ZK_HIP(ctx, hipEventSynchronize(ws.stat_ready));
+  size_t entries = 0;
+  uint32_t maxrun = 1;
+  for (int w = 0; w < W; w++) {
+    entries += ws.h_stat[2 * w];
+    maxrun = std::max(maxrun, ws.h_stat[2 * w + 1]);
+  }
+  entries += entries / 32;  // uniform scalars' few zero digits keep their chunk length
+  // a G2 chunk combine costs about 3x a G1 one: shorter G2 chunks for skewed
+  // scalars lost more there than they gained (2^16 witness-like G2 MSM 1.30 ->
+  // 1.35 ms), so G2 keeps the length of W*n entries
+  if (G2) entries = (size_t)W * n;
+  const uint32_t L0_alone = entries >= ((size_t)1 << 23)   ? MSM_L0
+                            : entries >= ((size_t)1 << 20) ? MSM_L0 / 2
+                            : entries >= ((size_t)1 << 18) ? MSM_L0 / 4
+                                                           : MSM_L0 / 8;
+  const uint32_t L0 =
+      beside && !G2 && L0_alone < (uint32_t)MSM_L0 ? std::max<uint32_t>(L0_alone / 2, MSM_L0 / 8) : L0_alone;
+  const uint32_t cpw = n_pad / L0;  // chunks per window
+  const uint32_t nchunks = cpw * (uint32_t)W;
+  ZK_TRY(ctx->ensure(ws.hkey, (size_t)nsets * nchunks * 4));
+  ZK_TRY(ctx->ensure(ws.tkey, (size_t)nsets * nchunks * 4));
+  ZK_TRY(ctx->ensure(ws.hpt, (size_t)nsets * nchunks * sizeof(xyzz<F>)));
+  ZK_TRY(ctx->ensure(ws.tpt, (size_t)nsets * nchunks * sizeof(xyzz<F>)));
+
   ChunkSlots<F> slots{(uint32_t*)ws.hkey.p, (uint32_t*)ws.tkey.p, (xyzz<F>*)ws.hpt.p, (xyzz<F>*)ws.tpt.p};
   const uint32_t gx = cdiv(nchunks, 256);
   const uint32_t gxl = cdiv((size_t)nchunks * Lanes<F>::N, 256);  // combine: Lanes<F>::N lanes per chunk
   const uint32_t nwaves = cdiv(nchunks, 64);
   ZK_LAUNCH(ctx, st, "msm_accumulate", k_msm_accumulate<F>, dim3(gx, nsets), dim3(256), 0, sorted, sets, start, end,
             wstat, nchunks, cpw, n_pad, L0, nbuckets, buckets, slots, nwaves, wave_scatter(nwaves));
-  // the largest bucket decides the depth of the chunk-combine tree; its
-  // read-back overlaps the accumulation
-  ZK_HIP(ctx, hipEventSynchronize(ws.stat_ready));
-  uint32_t maxrun = 1;
-  for (int w = 0; w < W; w++) maxrun = std::max(maxrun, ws.h_stat[2 * w + 1]);
+  // the largest bucket decides the depth of the chunk-combine tree
   const uint32_t max_span = (maxrun + L0 - 2) / L0 + 1;  // chunks spanned by the largest bucket
   if (max_span <= MSM_SERIAL_SPAN + 1) {
     ZK_LAUNCH(ctx, st, "msm_combine", k_msm_combine_serial<F>, dim3(gxl, nsets), dim3(256), 0, slots, end, nchunks,
