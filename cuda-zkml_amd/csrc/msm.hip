@@ -52,7 +52,7 @@ constexpr int SORT_U = 8;          // loads in flight per thread in the sort pas
 constexpr int SCAN_T = 128;        // buckets per column-scan block (<= the smallest B)
 constexpr int MSM_NCB = 256;       // coarse bins per window of the two-pass placement
 constexpr int MSM_BPC_MAX = 128;   // buckets per coarse bin at B = 2^15
-constexpr int PLACE_T = 256;       // threads of a placement block
+constexpr int PLACE_T = 1024;      // threads of a placement block
 constexpr uint32_t MSM_SERIAL_SPAN = 8;  // longest serial chunk-partial chain of the one-launch combine
 // Bits covered by the windows.  After the optional negation s <= (r-1)/2 <
 // 2^253, and signed digits need one more bit for the final carry.
@@ -483,12 +483,32 @@ __global__ __launch_bounds__(PLACE_T) void k_msm_place(const uint2* __restrict__
       const uint32_t p = p0 + u * PLACE_T;
       e[u] = p < hi ? tmp[p] : make_uint2(KEY_INVALID, 0u);
     }
+    // When every active lane of a wave holds the same bucket, the wave takes
+    // its positions with one atomic (order inside a bucket is free: its
+    // points are summed).  A hot bucket (the carry digit of small witness
+    // values can hold ~40% of all points) would otherwise serialize the CU's
+    // LDS on one counter.  All eight atomics are issued before any result is
+    // read, so their round trips overlap.
+    uint32_t pos[SORT_U], rank[SORT_U];
+    bool agg[SORT_U];
 #pragma unroll
     for (int u = 0; u < SORT_U; u++) {
-      if (e[u].x != KEY_INVALID) {
-        const uint32_t pos = atomicAdd(&cur[e[u].x - k0], 1u);
-        out[pos] = e[u];
+      const uint32_t key = e[u].x;
+      const uint32_t lead = __builtin_amdgcn_readfirstlane(key);
+      const uint64_t same = __ballot(key == lead);
+      agg[u] = same == __ballot(1) && lead != KEY_INVALID;
+      rank[u] = __builtin_amdgcn_mbcnt_hi((uint32_t)(same >> 32), __builtin_amdgcn_mbcnt_lo((uint32_t)same, 0u));
+      pos[u] = 0;
+      if (agg[u]) {
+        if (rank[u] == 0) pos[u] = atomicAdd(&cur[lead - k0], (uint32_t)__popcll(same));
+      } else if (key != KEY_INVALID) {
+        pos[u] = atomicAdd(&cur[key - k0], 1u);
       }
+    }
+#pragma unroll
+    for (int u = 0; u < SORT_U; u++) {
+      if (agg[u]) pos[u] = __builtin_amdgcn_readfirstlane(pos[u]) + rank[u];
+      if (e[u].x != KEY_INVALID) out[pos[u]] = e[u];
     }
   }
 }
