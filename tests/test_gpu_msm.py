@@ -165,10 +165,13 @@ def test_msm_g1_edge_cases(ctx):
     assert np.array_equal(got, oracle_msm(pts, sc))
 
 
-def test_msm_g1_all_equal_scalars(ctx):
-    """Every scalar equal: one bucket per window holds all n points."""
+@pytest.mark.parametrize("log_n", [14, 20])
+def test_msm_g1_all_equal_scalars(ctx, log_n):
+    """Every scalar equal: one bucket per window holds all n points (at 2^20
+    every placement wave holds a single bucket, and the chunk-combine tree
+    spans 2^14 chunks)."""
     rng = np.random.default_rng(8)
-    n = 1 << 14
+    n = 1 << log_n
     ks = from_std_arr(rand_std(n, rng))
     s = 0x1234567890ABCDEF1234567890ABCDEF
     km = to_mont(std_words(ks))
