@@ -8,9 +8,13 @@ Pins:
     R1CS and toxic-waste seed;
   * 256-byte proofs byte-identical to the oracle's restatement of prove
     (groth16.cu:655-920) for the same key, witness and blinding seed;
-  * every proof accepted by the reference's own verifier (pairing code
-    compiled from the reference sources into oracle/_ref), a wrong public
-    input rejected, an unsatisfying witness refused;
+  * every key point and proof element equal to s * G for the scalar the
+    Groth16 equations give for the reference's seeds (closed forms of
+    tests/groth16_closed_form.py, no reference code involved);
+  * every proof accepted by the product's verifier (itself pinned by the
+    reference's T4 golden proofs) and, where oracle/_ref is built, by the
+    reference's own verifier code; a wrong public input rejected, an
+    unsatisfying witness refused;
   * the reference's own T4 proving keys load with the reference checks.
 """
 import os
@@ -84,16 +88,38 @@ def test_setup_and_prove_match_oracle_and_verify(ctx, tmp_path, kind):
     assert rc == 0
     assert proof == proof_o
     assert t["total"] > 0
+    pf = tmp_path / "proof.bin"
+    pf.write_bytes(proof)
+    pub = tmp_path / "pub.bin"
+    write_public(pub, circ.public())
+    import zkml_amd
+    assert zkml_amd.verify_files(str(vk_g), str(pf), str(pub))
     if ref_available():
-        pf = tmp_path / "proof.bin"
-        pf.write_bytes(proof)
-        pub = tmp_path / "pub.bin"
-        write_public(pub, circ.public())
         assert ref().ref_verify_files(str(vk_g).encode(), str(pf).encode(), str(pub).encode()) == 1
         bad = list(circ.public())
         bad[-1] = (bad[-1] + 1) % Z.R
         write_public(pub, bad)
         assert ref().ref_verify_files(str(vk_g).encode(), str(pf).encode(), str(pub).encode()) == 0
+
+
+@pytest.mark.parametrize("kind,seeds", [("mul", (SETUP_SEED, PROVE_SEED)), ("r50", (SETUP_SEED, PROVE_SEED)),
+                                        ("r50", (7, 11))])
+def test_keys_and_proof_equal_closed_form(ctx, tmp_path, kind, seeds):
+    """zk_setup / zk_prove against the scalar-domain closed forms: toxic waste
+    and blinding from std::mt19937_64 (groth16.cu:48-58, 462-472, 712-715),
+    the QAP over the domain {w^j} (groth16.cu:97-189), C = L + H + sA + rB1."""
+    import groth16_closed_form as CF
+    circ = mul_circuit(7, 9) if kind == "mul" else random_r1cs(50, npub=3, seed=5)
+    setup_seed, prove_seed = seeds
+    r = gpu_r1cs(ctx, circ)
+    ctx.setup(r, setup_seed, tmp_path / "pk.bin", tmp_path / "vk.bin")
+    tw = CF.toxic_waste(setup_seed)
+    parsed = CF.parse_zkmlpk3(str(tmp_path / "pk.bin"))
+    assert CF.check_keys(circ, parsed, (tmp_path / "vk.bin").read_bytes(), tw) == []
+    pk = ctx.load_pk(tmp_path / "pk.bin")
+    proof, _ = ctx.prove(pk, r, circ.witness_words(), circ.npub, prove_seed)
+    rr, ss = CF.blinding(prove_seed)
+    assert CF.check_proof(circ, proof, tw, rr, ss) == []
 
 
 def test_prove_rejects_bad_witness_and_sizes(ctx, tmp_path):

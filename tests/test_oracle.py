@@ -26,6 +26,7 @@ import pytest
 
 import zkpy as Z
 from bindings import OracleR1CS, oracle, ptr, ref, ref_available, words
+from groth16_closed_form import parse_zkmlpk3
 from r1cs_gen import mul_circuit, random_r1cs
 
 GOLD = os.path.join(os.path.dirname(os.path.abspath(__file__)), "golden")
@@ -403,37 +404,6 @@ def test_t4_tampered_proof_rejected(tmp_path):
     bad = tmp_path / "bad.proof.bin"
     bad.write_bytes(bytes(data))
     assert ref().ref_verify_files(vk.encode(), str(bad).encode(), pub.encode()) == 0
-
-
-def parse_zkmlpk3(path):
-    """Independent Python parser of the ZKMLPK3 layout (groth16.cu:1104-1188)."""
-    d = open(path, "rb").read()
-    assert d[:7] == b"ZKMLPK3"
-    ver, n, m, npub = struct.unpack_from("<Iiii", d, 8)
-    off = 24
-    def g1():
-        nonlocal off
-        inf = d[off]
-        x = int.from_bytes(d[off + 1:off + 33], "little")
-        y = int.from_bytes(d[off + 33:off + 65], "little")
-        off += 65
-        return None if inf else (x, y)
-    def g2():
-        nonlocal off
-        inf = d[off]
-        v = [int.from_bytes(d[off + 1 + 32 * i:off + 33 + 32 * i], "little") for i in range(4)]
-        off += 129
-        return None if inf else ((v[0], v[1]), (v[2], v[3]))
-    def vec(f):
-        nonlocal off
-        (k,) = struct.unpack_from("<i", d, off)
-        off += 4
-        return [f() for _ in range(k)]
-    hdr = dict(ver=ver, n=n, m=m, npub=npub)
-    fixed = [g1(), g1(), g1(), g2(), g2(), g2()]
-    vecs = [vec(g1), vec(g2), vec(g1), vec(g1), vec(g2), vec(g1), vec(g1)]
-    assert off == len(d)
-    return hdr, fixed, vecs
 
 
 def test_t4_pk_parse_matches_independent_parser():

@@ -1,0 +1,351 @@
+"""Pins of the product's statement builder (zk_statement_v2_build) that need
+no reference code: the reference repository's published figures and its own
+soundness checks, plus closed forms of the gadgets' sizes.
+
+* Published counts (reference README.md:43-44): the public-model statement of
+  the host test (variant A, tests/host/test_statement_v2.cpp:96-127) has
+  8,082 constraints; the private one (variant B, :129-182) 62,692
+  constraints and 62,779 variables.  Public layouts: A = outputs (2 x 4) +
+  tag + context + inputs (2 x 36) = 82 (:105-106), B = tag + C_model +
+  C_input (2) + route (2 x 2) = 8 (:144).
+* Every variable pinned: the single-variable perturbation check of
+  test_statement_v2.cpp:62-89 and tests/test_underconstrained.py:36-60
+  (w_i + 1 and w_i - 1 each break some row, for every i >= 1; every wire is
+  used), and random corruption of three internal wires is always rejected.
+* Negative checks of the same test: a changed context breaks A (:120-123), a
+  flipped route flag breaks B (:174-177).
+* Gadget closed forms (gadgets.cuh:160-457, statement_v2.cuh:82-253): rows
+  and variables of bit decomposition (k + 1 rows, k variables), exact ReLU
+  (k + 2, k + 1), rescale (shift + k + 3, shift + k + 2), comparison flag
+  (k + 1, k), select (2, 2), fixed and private linear / conv layers, and the
+  in-circuit Poseidon permutation (3 rows per S-box, 8 full and 57 partial
+  rounds, plus one row per state linear combination that grows past 8 terms)
+  -- summed over a statement and compared with the builder's sizes for a
+  sweep of models and options, including both published variants.
+"""
+import random
+
+import numpy as np
+import pytest
+
+import statement_models as sm
+import zkml_amd as z
+
+R = z.R_INT
+RINV = pow(1 << 256, -1, R)
+RF, RP = 8, 57
+
+
+# ------------------------------------------------------------------ closed forms
+def poseidon_permutation(state, fresh):
+    """Rows and variables of one in-circuit permutation (gadgets.cuh:370-401)
+    for a state of three linear combinations given as sets of variable ids.
+    Returns (rows, state after); `fresh` counts the new variables."""
+    rows = 0
+    st = [set(s) for s in state]
+    for r in range(RF + RP):
+        st = [s | {0} for s in st]          # round constant on the constant wire
+        full = r < RF // 2 or r >= RF // 2 + RP
+        for i in (range(3) if full else (0,)):
+            fresh(3)                          # x^2, x^4, x^5
+            st[i] = {fresh.last}
+            rows += 3
+        u = st[0] | st[1] | st[2]             # MDS: every entry nonzero
+        st = [set(u), set(u), set(u)]
+        for i in range(3):
+            if len(st[i]) > 8:                # materialise the long combination
+                fresh(1)
+                st[i] = {fresh.last}
+                rows += 1
+    return rows, st
+
+
+class Fresh:
+    def __init__(self):
+        self.next, self.count, self.last = 1 << 40, 0, None
+
+    def __call__(self, k):
+        for _ in range(k):
+            self.last = self.next
+            self.next += 1
+        self.count += k
+
+
+def poseidon_commit_cost(nvals):
+    """(rows, vars) of add_poseidon_commit over nvals wires with a preset
+    output (gadgets.cuh:431-447): ceil(max(n, 1) / 2) permutations absorbing
+    two wires each, then one linear row binding the output."""
+    fresh = Fresh()
+    ids = list(range(1, nvals + 1))
+    st = [{0}, set(), set()]
+    n = 2 if nvals == 0 else nvals + nvals % 2
+    rows = 0
+    for i in range(0, n, 2):
+        if i < nvals:
+            st[1] = st[1] | {ids[i]}
+        if i + 1 < nvals:
+            st[2] = st[2] | {ids[i + 1]}
+        pr, st = poseidon_permutation(st, fresh)
+        rows += pr
+    return rows + 1, fresh.count
+
+
+def conv_taps(conv):
+    ci, h, w, co, kh, kw, stride, pad = conv
+    oh, ow = (h + 2 * pad - kh) // stride + 1, (w + 2 * pad - kw) // stride + 1
+    taps = 0
+    for oy in range(oh):
+        for ox in range(ow):
+            for ky in range(kh):
+                for kx in range(kw):
+                    iy, ix = oy * stride + ky - pad, ox * stride + kx - pad
+                    if 0 <= iy < h and 0 <= ix < w:
+                        taps += ci
+    return co * taps, co * oh * ow
+
+
+def statement_size(layers, B, n_in, context=False, private_input=False, private_model=False,
+                   private_outputs=False, route=False, compare_bits=48):
+    """(constraints, variables, public) of build_statement_v2 from the gadget costs."""
+    circ = [d for d in layers if d["type"] != z.SOFTMAX_APPROX]
+    n_out = conv_taps(circ[-1]["conv"])[1] if circ[-1]["type"] == z.CONV2D else circ[-1]["out_size"]
+    pub = (0 if private_outputs else B * n_out) + 1 + int(context) + int(private_model)
+    pub += B if private_input else B * n_in
+    pub += 2 * B if route else 0
+    rows, nv = 1, 1 + pub                         # model-tag binding row; w[0] and the public block
+    if context:
+        rows, nv = rows + 1, nv + 1
+    if private_model:
+        nw = sum(len(d["weights"]) + len(d["bias"]) for d in circ if "weights" in d)
+        cr, cv = poseidon_commit_cost(nw)
+        rows, nv = rows + cr, nv + nw + cv
+    if private_input:
+        cr, cv = poseidon_commit_cost(n_in + 1)
+        rows, nv = rows + B * cr, nv + B * (n_in + 1 + cv)
+    K = compare_bits
+    per_r = per_v = 0
+    for d in circ:
+        t = d["type"]
+        if t == z.LINEAR:
+            o, i = d["out_size"], d["in_size"]
+            per_r, per_v = (per_r + o * i + o, per_v + o * i + o) if private_model else (per_r + o, per_v + o)
+        elif t == z.CONV2D:
+            taps, outs = conv_taps(d["conv"])
+            per_r, per_v = (per_r + taps + outs, per_v + taps + outs) if private_model else (per_r + outs,
+                                                                                           per_v + outs)
+        elif t == z.RELU_EXACT:
+            k, s = d["bits"], d["shift"]
+            er, ev = k + 2, k + 1                 # signed range (k + 1 rows) + y = s * z
+            if s > 0:
+                er, ev = er + s + k + 3, ev + s + k + 2
+            per_r, per_v = per_r + d["in_size"] * er, per_v + d["in_size"] * ev
+        elif t == z.RELU_APPROX:
+            per_r, per_v = per_r + 3 * d["in_size"], per_v + 3 * d["in_size"]
+    if not private_outputs:
+        per_r += n_out
+    if route:
+        geq_r, geq_v, sel = K + 1, K, 2
+        per_r += 2 * geq_r + 3 * sel + (n_out - 2) * (2 * geq_r + 4 * sel) + 2
+        per_v += 2 * geq_v + 3 * sel + (n_out - 2) * (2 * geq_v + 4 * sel)
+    return rows + B * per_r, nv + B * per_v, pub
+
+
+# ------------------------------------------------------------------ the published variants
+def variant_a():
+    layers, xs = sm.tiny_cnn()
+    st = z.statement_v2(layers, xs, model_tag=0xC0FFEE, context=0x0123456789ABCDEF0123456789ABCDEF)
+    return layers, xs, st
+
+
+def variant_b():
+    layers, xs = sm.tiny_cnn()
+    return layers, xs, sm.config4()
+
+
+@pytest.fixture(scope="module")
+def stmt_a():
+    return variant_a()
+
+
+@pytest.fixture(scope="module")
+def stmt_b():
+    return variant_b()
+
+
+def test_variant_a_published_size(stmt_a):
+    layers, xs, st = stmt_a
+    assert st.nc == 8082
+    assert st.npub == 2 * 4 + 1 + 1 + 2 * 36
+    assert (st.nc, st.nv, st.npub) == statement_size(layers, 2, 36, context=True)
+    assert st.check()
+
+
+def test_variant_b_published_size(stmt_b):
+    layers, xs, st = stmt_b
+    assert (st.nc, st.nv) == (62692, 62779)
+    assert st.npub == 1 + 1 + 2 + 4
+    assert (st.nc, st.nv, st.npub) == statement_size(layers, 2, 36, private_input=True, private_model=True,
+                                                     private_outputs=True, route=True)
+    assert st.check()
+
+
+def test_poseidon_permutation_cost():
+    """243 rows of S-boxes; the materialisations depend only on the state
+    sizes: the published variant B implies 270 rows per permutation on
+    average over its 194 permutations."""
+    fresh = Fresh()
+    rows, st = poseidon_permutation([{0}, {1}, {2}], fresh)
+    assert rows >= 243 and rows == fresh.count
+    r312, _ = poseidon_commit_cost(312)          # variant B's weights and biases
+    r37, _ = poseidon_commit_cost(37)            # one sample and its blinding
+    assert r312 - 1 + 2 * (r37 - 1) == 194 * 270
+
+
+# ------------------------------------------------------------------ gadget sweep
+def _random_model(rng):
+    layers, n_in = [], None
+    kind = rng.choice(["mlp", "cnn", "approx"])
+    if kind == "cnn":
+        c, h, w = 1, rng.randint(3, 6), rng.randint(3, 6)
+        co, k, pad = rng.randint(1, 3), rng.choice([1, 2, 3]), rng.randint(0, 1)
+        conv = (c, h, w, co, k, k, 1, pad)
+        oh, ow = h + 2 * pad - k + 1, w + 2 * pad - k + 1
+        wts = [rng.randint(-3, 3) for _ in range(co * c * k * k)]
+        layers.append(z.layer_conv2d(c, h, w, co, k, k, 1, pad, wts, [rng.randint(-5, 5) for _ in range(co)]))
+        n_in, cur = c * h * w, co * oh * ow
+    else:
+        n_in = rng.randint(2, 8)
+        cur = rng.randint(2, 6)
+        layers.append(z.layer_linear(n_in, cur, [rng.randint(-9, 9) for _ in range(n_in * cur)],
+                                     [rng.randint(-9, 9) for _ in range(cur)]))
+    if kind == "approx":
+        layers.append(z.layer_relu_approx(cur))
+    else:
+        layers.append(z.layer_relu_exact(cur, rng.randint(12, 20), rng.randint(0, 3)))
+    n_out = rng.randint(2, 5)
+    layers.append(z.layer_linear(cur, n_out, [rng.randint(-9, 9) for _ in range(cur * n_out)],
+                                 [rng.randint(-9, 9) for _ in range(n_out)]))
+    layers.append(z.layer_softmax(n_out))
+    return layers, n_in
+
+
+@pytest.mark.parametrize("seed", range(12))
+def test_statement_sizes_equal_gadget_closed_forms(seed):
+    rng = random.Random(seed)
+    layers, n_in = _random_model(rng)
+    B = rng.randint(1, 3)
+    xs = [[rng.randint(0, 4) for _ in range(n_in)] for _ in range(B)]
+    route = rng.random() < 0.5
+    opts = dict(context=0x1234 if rng.random() < 0.5 else None, private_input=rng.random() < 0.4,
+                private_model=rng.random() < 0.4, route_threshold=1 if route else None)
+    opts["private_outputs"] = route and rng.random() < 0.5
+    if opts["private_input"]:
+        opts["input_blinding"] = [rng.randrange(1, 1 << 60) for _ in range(B)]
+    st = z.statement_v2(layers, xs, **opts)
+    want = statement_size(layers, B, n_in, context=opts["context"] is not None,
+                          private_input=opts["private_input"], private_model=opts["private_model"],
+                          private_outputs=opts["private_outputs"], route=route)
+    assert (st.nc, st.nv, st.npub) == want
+    assert st.check()
+
+
+# ------------------------------------------------------------------ soundness checks
+def _std_system(st):
+    """Rows as {var: coeff} dicts per matrix and the witness, standard form."""
+    w = [int(sum(int(v) << (64 * k) for k, v in enumerate(row))) * RINV % R for row in st.w]
+    rows = [[{}, {}, {}] for _ in range(st.nc)]
+    for mat, M in enumerate((st.A, st.B, st.C)):
+        for e in M:
+            c = int(sum(int(v) << (64 * k) for k, v in enumerate(e["value"]))) * RINV % R
+            d = rows[int(e["row"])][mat]
+            d[int(e["col"])] = (d.get(int(e["col"]), 0) + c) % R
+    return rows, w
+
+
+def _pinned_report(st, corruptions=200, seed=1):
+    rows, w = _std_system(st)
+    ev = [[sum(c * w[v] for v, c in d.items()) % R for d in row] for row in rows]
+    assert all((a * b - c) % R == 0 for a, b, c in ev)
+    hits = {}
+    for k, row in enumerate(rows):
+        for mat, d in enumerate(row):
+            for v, c in d.items():
+                hits.setdefault(v, []).append((k, mat, c))
+    unused = [i for i in range(1, len(w)) if i not in hits]
+    unpinned = []
+    for i in range(1, len(w)):
+        for delta in (1, R - 1):
+            touched = {}
+            for k, mat, c in hits.get(i, []):
+                touched.setdefault(k, list(ev[k]))
+                touched[k][mat] = (touched[k][mat] + c * delta) % R
+            if all((a * b - c) % R == 0 for a, b, c in touched.values()):
+                unpinned.append(i)
+                break
+    # random corruption of three internal wires: only rows touching them change
+    rng = random.Random(seed)
+    internal = list(range(1 + st.npub, len(w)))
+    accepted = 0
+    for _ in range(corruptions):
+        w2 = dict((i, rng.randrange(R)) for i in rng.sample(internal, 3))
+        ks = {k for i in w2 for k, _, _ in hits.get(i, [])}
+        ok = True
+        for k in ks:
+            a, b, c = (sum(cf * w2.get(v, w[v]) for v, cf in d.items()) % R for d in rows[k])
+            if (a * b - c) % R:
+                ok = False
+                break
+        accepted += ok
+    return unused, unpinned, accepted
+
+
+def test_variant_a_every_variable_pinned(stmt_a):
+    unused, unpinned, accepted = _pinned_report(stmt_a[2])
+    assert unused == [] and unpinned == [] and accepted == 0
+
+
+@pytest.mark.slow
+def test_variant_b_every_variable_pinned(stmt_b):
+    unused, unpinned, accepted = _pinned_report(stmt_b[2])
+    assert unused == [] and unpinned == [] and accepted == 0
+
+
+def test_perturbation_check_flags_a_free_wire():
+    """The checker itself (test_underconstrained.py:88-97): x * y = z plus a
+    wire that appears in no row."""
+    class S:
+        pass
+    st = S()
+    st.nc, st.npub = 1, 1
+    one = 1 << 256
+    def fr(v):
+        m = v * one % R
+        return [(m >> (64 * k)) & (2**64 - 1) for k in range(4)]
+    st.w = np.array([fr(v) for v in (1, 3, 5, 15, 42)], dtype=np.uint64)
+    mk = lambda r, c: np.array([(r, c, fr(1))], dtype=z.SPARSE_DTYPE)
+    st.A, st.B, st.C = mk(0, 1), mk(0, 2), mk(0, 3)
+    unused, unpinned, _ = _pinned_report(st, corruptions=0)
+    assert unused == [4] and 4 in unpinned and 2 not in unpinned and 3 not in unpinned
+
+
+def _bump(st, idx, fn):
+    """Witness with w[idx] replaced by fn(w[idx]) (standard form), Montgomery words."""
+    w = st.w.copy()
+    v = int(sum(int(x) << (64 * k) for k, x in enumerate(w[idx]))) * RINV % R
+    m = fn(v) % R * (1 << 256) % R
+    w[idx] = [(m >> (64 * k)) & (2**64 - 1) for k in range(4)]
+    return w
+
+
+def _satisfied(st, w):
+    rows, _ = _std_system(st)
+    wi = [int(sum(int(v) << (64 * k) for k, v in enumerate(row))) * RINV % R for row in w]
+    return all((sum(c * wi[v] for v, c in a.items()) * sum(c * wi[v] for v, c in b.items())
+                - sum(c * wi[v] for v, c in cc.items())) % R == 0 for a, b, cc in rows)
+
+
+def test_changed_context_and_route_flag_are_rejected(stmt_a, stmt_b):
+    st = stmt_a[2]
+    assert not _satisfied(st, _bump(st, 1 + st.layout["context_index"], lambda v: v + 1))
+    st = stmt_b[2]
+    assert not _satisfied(st, _bump(st, 1 + st.layout["route_start"], lambda v: 1 - v))
