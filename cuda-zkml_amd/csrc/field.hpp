@@ -47,6 +47,8 @@ struct FqP {
                                        0x0b6d0302u, 0x029b8504u, 0x197098d0u, 0x00c19139u};
   static constexpr uint32_t MOD6[9] = {0x12edefaau, 0x061a4448u, 0x0aafd3dau, 0x10fed0e5u, 0x012318d0u,
                                        0x11238484u, 0x03e94786u, 0x1628e538u, 0x012259d6u};
+  static constexpr uint32_t MOD8[9] = {0x03e7ea38u, 0x082305b6u, 0x03951a78u, 0x16a91687u, 0x0c2ecbc0u,
+                                       0x16da0605u, 0x05370a08u, 0x12e131a0u, 0x01832273u};
   static constexpr uint32_t INV = 0x04866389u;  // -q^-1 mod 2^29
   static constexpr uint32_t ONE[9] = {0x157ccc21u, 0x141c2758u, 0x185230d3u, 0x014c0419u, 0x0aa36fb9u,
                                       0x1d4240ceu, 0x11d54c07u, 0x052ac7a8u, 0x000dc836u};  // 2^261 mod q
@@ -71,6 +73,8 @@ struct FrP {
                                        0x0b6d0302u, 0x029b8504u, 0x197098d0u, 0x00c19139u};
   static constexpr uint32_t MOD6[9] = {0x00000006u, 0x1a5e0bbdu, 0x1628d9e5u, 0x0ee365b4u, 0x0122ef13u,
                                        0x11238484u, 0x03e94786u, 0x1628e538u, 0x012259d6u};
+  static constexpr uint32_t MOD8[9] = {0x00000008u, 0x187d64fcu, 0x12e12287u, 0x1e84879bu, 0x0c2e9419u,
+                                       0x16da0605u, 0x05370a08u, 0x12e131a0u, 0x01832273u};
   static constexpr uint32_t INV = 0x0fffffffu;  // -r^-1 mod 2^29
   static constexpr uint32_t ONE[9] = {0x0fffff57u, 0x1ea70ab4u, 0x052c068bu, 0x17504f49u, 0x0aa8075bu,
                                       0x1d4240ceu, 0x11d54c07u, 0x052ac7a8u, 0x000dc836u};  // 2^261 mod r
@@ -112,8 +116,9 @@ ZK_HD fe<P> fe_one() {
 }
 
 // Montgomery product a*b*2^-261 mod m, column (product-scanning) order with the
-// reduction interleaved per column.  Inputs: limbs < 2^30, values < 8m.
-// Output: limbs < 2^29, value < 2m.
+// reduction interleaved per column.  Inputs: limbs < 2^30.  Output: limbs
+// < 2^29, value < a*b/2^261 + m, so below 2m for values < 8m, and also when
+// one operand is below m and the other anywhere below 2^261.
 template <class P>
 ZK_HD fe<P> fmul(const fe<P>& a, const fe<P>& b) {
   uint32_t q[NL];
@@ -433,6 +438,42 @@ ZK_HD fe<P> fneg_lazy4(const fe<P>& a) {
     d.l[i] = (uint32_t)v & LMASK;
   }
   return d;
+}
+
+// a - b + KM*m with carries (KM in {2, 4, 8}): for b < KM*m the value is
+// a - b + KM*m > 0 with normalized limbs (valid while below 2^261).
+template <int KM, class P>
+ZK_HD fe<P> fsub_off(const fe<P>& a, const fe<P>& b) {
+  static_assert(KM == 2 || KM == 4 || KM == 8, "offset multiple");
+  const uint32_t(&K)[NL] = KM == 2 ? P::MOD2 : KM == 4 ? P::MOD4 : P::MOD8;
+  fe<P> d;
+  int32_t c = 0;
+#pragma unroll
+  for (int i = 0; i < NL; i++) {
+    int32_t v = (int32_t)a.l[i] + (int32_t)K[i] - (int32_t)b.l[i] + c;
+    c = v >> 29;
+    d.l[i] = (uint32_t)v & LMASK;
+  }
+  return d;
+}
+
+// Canonical value of x (normalized limbs, any value below 2^261).  Both
+// moduli have top limb M8 = 0x30644e; q = (l8 * floor(2^40 / (M8 + 1))) >> 40
+// never exceeds floor(x / m) and falls short of it by at most 2, so
+// x - q m < 3m and two conditional subtractions finish.
+template <class P>
+ZK_HD fe<P> freduce(const fe<P>& x) {
+  static_assert(P::MOD[NL - 1] == 0x0030644eu, "quotient estimate assumes the BN254 top limb");
+  const uint32_t q = (uint32_t)(((uint64_t)x.l[NL - 1] * 346695ull) >> 40);
+  fe<P> r;
+  int64_t c = 0;
+#pragma unroll
+  for (int i = 0; i < NL; i++) {
+    const int64_t t = (int64_t)x.l[i] - (int64_t)q * (int64_t)P::MOD[i] + c;
+    r.l[i] = (uint32_t)t & LMASK;
+    c = t >> 29;
+  }
+  return fcsub(fcsub(r, P::MOD2), P::MOD);
 }
 
 template <class P>

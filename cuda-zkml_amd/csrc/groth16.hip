@@ -241,14 +241,11 @@ int quotient_run(zk_context* ctx, const zk_r1cs* c, const void* d_w, void* d_h, 
   Fr zinv;
   const uint64_t g = coset_shift(c->log_n, zinv);
   if (!g) return ctx->fail(ZK_ERR_INVALID, "no valid coset shift");
+  // 3 iNTT -> coefficients; 3 coset NTT -> evaluations on g*H
+  // (groth16.cu:321-363); (A B - C) / Z and the coset iNTT h_i = iNTT(H)_i g^-i
+  // (groth16.cu:366-383), the pointwise step inside the last transform
   uint4* abc = (uint4*)d_abc;
-  // 3 iNTT -> coefficients; 3 coset NTT -> evaluations on g*H (groth16.cu:321-363)
-  ZK_TRY(ntt_run(ctx, abc, abc, c->log_n, 1, 3, 0, st));
-  ZK_TRY(ntt_run(ctx, abc, abc, c->log_n, 0, 3, g, st));
-  ZK_TRY(quotient_pointwise(ctx, d_h, abc, abc + 2 * n, abc + 4 * n, n, zinv.v, st));
-  // coset iNTT: h_i = iNTT(H)_i g^-i (groth16.cu:372-383)
-  ZK_TRY(ntt_run(ctx, d_h, d_h, c->log_n, 1, 1, g, st));
-  return ZK_OK;
+  return quotient_ntts(ctx, d_h, abc, abc + 6 * n, c->log_n, g, zinv.v, st);
 }
 
 // ------------------------------------------------------------------ ZKMLPK3
@@ -516,7 +513,7 @@ static int zk_quotient_h_impl(zk_context* ctx, const zk_r1cs* c, const void* d_w
                               void* stream) {
   if (!ctx || !c || !d_witness || !d_h) return ZK_ERR_INVALID;
   if (m != (size_t)c->nv) return ctx->fail(ZK_ERR_MISMATCH, "quotient: witness length != num_variables");
-  ZK_TRY(ctx->ensure(ctx->scratch_b, c->n * 32 * 3));
+  ZK_TRY(ctx->ensure(ctx->scratch_b, c->n * 32 * 6));  // A | B | C and the transforms' work space
   return quotient_run(ctx, c, d_witness, d_h, ctx->scratch_b.p, ctx->s(stream), false, nullptr);
 }
 
@@ -627,7 +624,7 @@ static int zk_prove_impl(zk_context* ctx, const zk_pk* pk, const zk_r1cs* c, con
   if (num_public != pk->npub) return ctx->fail(ZK_ERR_MISMATCH, "witness public count != proving key");
   if ((size_t)(1 + pk->npub) > m) return ctx->fail(ZK_ERR_MISMATCH, "public inputs exceed witness");
   const size_t n = c->n;
-  ZK_TRY(ctx->ensure(ctx->scratch_b, n * 32 * 3));
+  ZK_TRY(ctx->ensure(ctx->scratch_b, n * 32 * 6));  // A | B | C and the transforms' work space
   ZK_TRY(ctx->ensure(ctx->scratch_c, n * 32 + m * 32 + 64));
   // Streams: the context stream (witness upload, quotient, then the H MSM),
   // one for the G2 MSM and one for the G1 MSMs over the witness (A, B1 and

@@ -6,19 +6,34 @@
 // four-step (Bailey) decomposition n = R_0 * ... * R_{P-1} with P <= 3 passes
 // over HBM and R_p <= 256:
 //
-//   digits of the input index (most significant first) n_0 .. n_{P-1};
-//   pass p < P-1: DFT of size R_p over digit n_p for every setting of the
-//     other digits, result k_p written back in place, then multiplied by
-//     w_{R_p S_p}^(k_p * m) with m the index formed by the lower digits
-//     (S_p = R_{p+1} * ... * R_{P-1});
-//   pass P-1: DFT over the last digit and a digit-reversed store so that the
+//   digits of the input index (most significant first) i_0 .. i_{P-1};
+//   pass p < P-1: DFT of size R_p over digit i_p for every setting of the
+//     other digits, result k_p written back to the same positions, then
+//     multiplied by w_{R_p S_p}^(k_p * m) with m the index formed by the lower
+//     digits (S_p = R_{p+1} * ... * R_{P-1});
+//   pass P-1: DFT over the last digit and a digit-reversed store, so that the
 //     output index is k_0 + R_0 k_1 + R_0 R_1 k_2 (natural order).
 //
-// Every pass works on a tile of 1024 elements (R rows x 1024/R columns) in
-// LDS: the 1024/R columns are adjacent in HBM, so each row of the tile is a
-// contiguous segment of >= 128 bytes.  The sub-DFT is radix-2 DIT on the
-// bit-reversed rows, with w_R^t from a small table.  Field elements live in
-// LDS as nine 29-bit limb planes (conflict-free for consecutive lanes).
+// A pass works on tiles of R rows (the DFT's length) x T columns (T
+// neighbouring transforms, adjacent in HBM for the first passes).  Each
+// thread owns 2^KMAX elements of a column and runs the DFT as radix-2^KMAX
+// decimation-in-time steps held in registers:
+//   * the first step reads its elements straight from HBM at bit-reversed
+//     rows (so no bit-reversal pass exists) and its twiddles are the same for
+//     every thread (w_2, w_4, w_8 powers, several of them 1);
+//   * the steps in between exchange elements through LDS (nine 29-bit limb
+//     planes, rows XOR-swizzled against bank conflicts) with per-thread
+//     twiddles w_R^e from an LDS copy of the pass's table;
+//   * the last step writes its outputs straight to HBM, multiplied by the
+//     inter-pass twiddle (or the coset / 1/n factor of the last pass).
+//
+// Butterflies are lazy: u + w v and u - w v + 2m with carries normalised but
+// no modular reduction, so a value grows by at most 2m per stage (w v is a
+// Montgomery product, below 2m).  After the eight stages of a pass it is
+// below 26m, far inside the 2^261 range of nine 29-bit limbs; the pass's
+// output multiply brings it back below 2m, and the last pass reduces to the
+// canonical range.  The inverse transform's 1/n rides in the first
+// inter-pass table, so it costs no multiply.
 //
 // Radix bookkeeping: the NTT is linear, so the kernels run directly on the
 // 256-bit words of the reference's Montgomery form (repack only); twiddles and
@@ -26,13 +41,14 @@
 // multiplies the stored integers by the intended field constant.
 #include <string.h>
 
+#include <utility>
+
 #include "zk_internal.hpp"
 
 namespace zk {
 
-constexpr int NTT_TILE = 1024;
-constexpr int NTT_THREADS = 256;
 constexpr int NTT_MAX_LOG = 24;
+constexpr int NTT_MAX_LOGR = 8;
 
 // SoA table of internal-form field elements: limb l of entry i at l*count+i.
 struct FrTable {
@@ -40,21 +56,19 @@ struct FrTable {
   size_t count = 0;
 };
 
-struct NttDir {
-  FrTable twr[3];  // w_{R_p}^t, t < R_p/2
-  FrTable twp[2];  // w_{R_p S_p}^(k*m) at k*S_p + m, for passes p < P-1
-};
-
 struct NttPlan {
   int log_n = 0, P = 0;
   int logR[3] = {0, 0, 0};
-  NttDir dir[2];            // [0] forward, [1] inverse
-  uint32_t ninv[NL];        // n^-1 in internal form
+  FrTable twr[3][2];  // [pass][direction]: w_{R_p}^e, e < R_p / 2
+  FrTable twp[2][2];  // [pass < P-1][direction]: w_{R_p S_p}^(k m); the inverse pass-0 table carries 1/n
+  uint32_t ninv[NL];  // n^-1 in internal form
 };
 
+// Per (log_n, g): g^i (forward coset pre-multiply), g^-i / n^[P == 1]
+// (inverse coset post-multiply) and g^i / n^[P == 1] (an inverse transform
+// whose output goes on to a coset transform).
 struct CosetTables {
-  FrTable fwd;  // g^i
-  FrTable inv;  // n^-1 g^-i
+  FrTable pre, post_inv, post_fold;
 };
 
 __device__ __forceinline__ fr load_table(const uint32_t* __restrict__ t, size_t count, size_t i) {
@@ -76,208 +90,333 @@ __device__ __forceinline__ fr load_elem(const uint4* __restrict__ p, size_t i) {
   return repack_in<FrP>(w);
 }
 
-__device__ __forceinline__ void store_elem(uint4* __restrict__ p, size_t i, const fr& x) {
+// Pack nine limbs of a value below 2^256 into eight words (no reduction).
+__device__ __forceinline__ void store_elem_raw(uint4* __restrict__ p, size_t i, const fr& x) {
   uint32_t w[8];
-  repack_out(x, w);
+#pragma unroll
+  for (int j = 0; j < 8; j++) {
+    const int bit = 32 * j;
+    const int k = bit / 29;
+    const int sh = bit % 29;
+    uint64_t v = x.l[k];
+    if (k + 1 < NL) v |= (uint64_t)x.l[k + 1] << 29;
+    if (k + 2 < NL && sh > 26) v |= (uint64_t)x.l[k + 2] << 58;
+    w[j] = (uint32_t)(v >> sh);
+  }
   p[2 * i] = make_uint4(w[0], w[1], w[2], w[3]);
   p[2 * i + 1] = make_uint4(w[4], w[5], w[6], w[7]);
 }
 
-__device__ __forceinline__ fr lds_get(const uint32_t* s, int idx) {
-  fr x;
-#pragma unroll
-  for (int l = 0; l < NL; l++) x.l[l] = s[l * NTT_TILE + idx];
-  return x;
-}
+__device__ __forceinline__ uint32_t bitrev(uint32_t x, int bits) { return bits ? __brev(x) >> (32 - bits) : 0; }
 
-__device__ __forceinline__ void lds_put(uint32_t* s, int idx, const fr& x) {
-#pragma unroll
-  for (int l = 0; l < NL; l++) s[l * NTT_TILE + idx] = x.l[l];
-}
+// ------------------------------------------------------------------ pass kernel
+enum { PRE_NONE = 0, PRE_TABLE = 1, PRE_QUOTIENT = 2 };
+enum { POST_NONE = 0, POST_SCALE = 1, POST_TABLE = 2 };
 
-__device__ __forceinline__ uint32_t bitrev(uint32_t x, int bits) { return __brev(x) >> (32 - bits); }
-
-// Twiddles w_R^t, t < R/2: staged in LDS (plane-major) when R/2 <= NTT_TWL
-// so the stage loop reads no global memory; the single-pass transforms of
-// 2^9 and 2^10 points read the table in place.
-constexpr int NTT_TWL = 128;
-struct TwView {
-  const uint32_t* p;
-  int stride;  // words between planes
+struct PassGeo {
+  uint32_t logR, logT;  // DFT length and tile columns
+  uint32_t logS;        // middle pass: stride of this digit
+  uint32_t logR0, logS0, logS1, logNR;  // last pass: first-digit count and stride, middle-digit stride, log(n/R)
+  uint64_t n;
 };
 
-__device__ __forceinline__ TwView stage_twiddles(uint32_t* tw, const uint32_t* __restrict__ twr, int half) {
-  if (half > NTT_TWL) return TwView{twr, half};
-  for (int e = threadIdx.x; e < half; e += NTT_THREADS) {
-#pragma unroll
-    for (int l = 0; l < NL; l++) tw[l * NTT_TWL + e] = twr[(size_t)l * half + e];
-  }
-  return TwView{tw, NTT_TWL};
+struct PassIO {
+  const uint4* src;
+  uint4* dst;
+  const uint32_t* twr;   // w_R^e, e < R/2 (R/2 entries)
+  const uint32_t* twp;   // middle pass: inter-pass table, R * S entries
+  const uint32_t* pre;   // PRE_TABLE: n entries by input position
+  const uint32_t* post;  // POST_TABLE: n entries by output position
+  int pre_mode, post_mode;
+  fr scale;              // POST_SCALE
+  fr kc, zk;             // PRE_QUOTIENT: h = (a b - c kc) zk
+};
+
+// LDS word of (row p, column c) in a plane: rows swizzled so that the 32/T
+// rows a half-wave touches at once (T < 32) fall in different banks.
+__device__ __forceinline__ uint32_t lds_ix(uint32_t p, uint32_t c, uint32_t logT, uint32_t smask) {
+  return ((p ^ ((p >> 3) & smask)) << logT) + c;
 }
 
-__device__ __forceinline__ fr tw_get(const TwView& tw, int idx) {
+__device__ __forceinline__ fr lds_get(const uint32_t* s, uint32_t E, uint32_t ix) {
   fr x;
 #pragma unroll
-  for (int l = 0; l < NL; l++) x.l[l] = tw.p[l * tw.stride + idx];
+  for (int l = 0; l < NL; l++) x.l[l] = s[l * E + ix];
   return x;
 }
 
-// In-LDS DIT over the rows of a (R x T) tile stored row-major (index j*T + c);
-// rows were stored bit-reversed, results come out natural.  Two radix-2
-// stages per LDS round trip (a radix-2^2 step on four rows held in
-// registers), a single radix-2 stage first when log2 R is odd.  tw: w_R^t,
-// t < R/2, in LDS.
-//
-// Butterflies are lazy (Harvey's form): a stage's inputs lie in [0, 4m); the
-// untwiddled operand X is brought below 2m by one conditional subtraction,
-// the twiddled one T is an fmul output (< 2m), and the stage writes X + T and
-// X - T + 2m, both in [0, 4m) with normalized limbs.  The first stage's
-// inputs are below 2m (canonical loads or fmul outputs) and need no
-// subtraction.  Results leave in [0, 4m).
-__device__ __forceinline__ void tile_dit(uint32_t* s, const TwView& tw, int logR, int T) {
-  const int R = 1 << logR;
-  int st = 0;
-  if (logR & 1) {  // stage 0: twiddle 1, pairs (2g, 2g + 1)
-    for (int b = threadIdx.x; b < (R >> 1) * T; b += NTT_THREADS) {
-      const int c = b % T, g = b / T;
-      const int i0 = (2 * g) * T + c, i1 = i0 + T;
-      const fr x0 = lds_get(s, i0), x1 = lds_get(s, i1);
-      lds_put(s, i0, fadd_wide(x0, x1));
-      lds_put(s, i1, fsub_lazy(x0, x1));
-    }
-    __syncthreads();
-    st = 1;
-  }
-  for (; st < logR; st += 2) {
-    const int h = 1 << st;
-    const int tq = R >> (st + 2);  // twiddle stride of w_{4h} in the w_R table
-    for (int b = threadIdx.x; b < (R >> 2) * T; b += NTT_THREADS) {
-      const int c = b % T, q = b / T;
-      const int k = q & (h - 1);
-      const int j0 = ((q >> st) << (st + 2)) + k;
-      const int i0 = j0 * T + c, i1 = i0 + h * T, i2 = i1 + h * T, i3 = i2 + h * T;
-      fr x0 = lds_get(s, i0), x1 = lds_get(s, i1), x2 = lds_get(s, i2), x3 = lds_get(s, i3);
-      fr t1 = x1, t3 = x3;  // h == 1: the first stage, inputs below 2m, twiddle 1
-      if (h > 1) {
-        const fr w2 = tw_get(tw, 2 * k * tq);  // w_{2h}^k (w^0 is the table's one)
-        t1 = fmul(x1, w2);
-        t3 = fmul(x3, w2);
-        x0 = fcsub(x0, FrP::MOD2);
-        x2 = fcsub(x2, FrP::MOD2);
+__device__ __forceinline__ void lds_put(uint32_t* s, uint32_t E, uint32_t ix, const fr& x) {
+#pragma unroll
+  for (int l = 0; l < NL; l++) s[l * E + ix] = x.l[l];
+}
+
+__device__ __forceinline__ fr tw_get(const uint32_t* tw, uint32_t half, uint32_t e) {
+  fr x;
+#pragma unroll
+  for (int l = 0; l < NL; l++) x.l[l] = tw[l * half + e];
+  return x;
+}
+
+// f(integral_constant<int, I>) for I = 0 .. N-1, expanded at compile time so
+// that every register-array index inside is a constant.
+template <class F, int... I>
+__device__ __forceinline__ void unroll_seq(F&& f, std::integer_sequence<int, I...>) {
+  (f(std::integral_constant<int, I>{}), ...);
+}
+template <int N, class F>
+__device__ __forceinline__ void unroll(F&& f) {
+  unroll_seq(f, std::make_integer_sequence<int, N>{});
+}
+
+// One lazy DIT butterfly with a twiddle: (u + w v, u - w v + 2m).
+__device__ __forceinline__ void bfly(fr& u, fr& v, const fr& w) {
+  const fr t = fmul(v, w);
+  v = fsub_off<2>(u, t);
+  u = fadd_wide(u, t);
+}
+
+// Index of the p-th pair's lower element at sub-stage i (bit i clear).
+template <int I, int P>
+constexpr int pair_lo() {
+  return ((P >> I) << (I + 1)) | (P & ((1 << I) - 1));
+}
+
+// First step of a tile: K radix-2 stages (h = 1 .. 2^(K-1)) whose twiddles
+// w_{2^(i+1)}^(t mod 2^i) are the same for every group; index 0 is 1 and is
+// skipped (the subtraction then adds the bound of its operand: inputs below
+// 2m give at most 2^(i+2) m after sub-stage i).
+template <int K>
+__device__ __forceinline__ void first_step(fr (&x)[1 << K], const uint32_t* tw, uint32_t half, uint32_t logR) {
+  unroll<K>([&](auto I) {
+    constexpr int i = decltype(I)::value, hi = 1 << i;
+    unroll<(1 << K) / 2>([&](auto Pp) {
+      constexpr int t = pair_lo<i, decltype(Pp)::value>();
+      constexpr int lo = t & (hi - 1);
+      if constexpr (lo == 0) {
+        const fr u = x[t], v = x[t + hi];
+        x[t] = fadd_wide(u, v);
+        x[t + hi] = fsub_off<(i == 0 ? 2 : i == 1 ? 4 : 8)>(u, v);
+      } else {
+        bfly(x[t], x[t + hi], tw_get(tw, half, (uint32_t)lo << (logR - 1 - i)));
       }
-      const fr y0 = fadd_wide(x0, t1), y1 = fsub_lazy(x0, t1);
-      const fr y2 = fadd_wide(x2, t3), y3 = fsub_lazy(x2, t3);
-      const fr z2 = h > 1 ? fmul(y2, tw_get(tw, k * tq)) : fcsub(y2, FrP::MOD2);  // w_{4h}^k
-      const fr z3 = fmul(y3, tw_get(tw, (k + h) * tq));                           // w_{4h}^(k+h)
-      const fr u0 = fcsub(y0, FrP::MOD2), u1 = fcsub(y1, FrP::MOD2);
-      lds_put(s, i0, fadd_wide(u0, z2));
-      lds_put(s, i2, fsub_lazy(u0, z2));
-      lds_put(s, i1, fadd_wide(u1, z3));
-      lds_put(s, i3, fsub_lazy(u1, z3));
-    }
-    __syncthreads();
-  }
+    });
+  });
 }
 
-struct PassArgs {
-  int logR;          // this pass's radix
-  int T;             // tile columns = NTT_TILE / R
-  uint32_t S;        // stride of this digit
-  uint64_t n;        // transform size
-  // last pass only
-  uint32_t R0, S0;   // first-digit count and stride
-  uint32_t R1, S1;   // middle-digit count and stride (P == 3), else R1 = 1
+// A step of K stages starting at stage s (h = 2^s) on the group
+// {j0 + t h : t < 2^K}, jl = j0 mod h: sub-stage i pairs t, t + 2^i with
+// twiddle w_{2 h 2^i}^(jl + (t mod 2^i) h) = w_R^((jl + (t mod 2^i) h) << (logR-1-s-i)).
+template <int K>
+__device__ __forceinline__ void mid_step(fr (&x)[1 << K], const uint32_t* tw, uint32_t half, uint32_t logR,
+                                         uint32_t s, uint32_t jl) {
+  unroll<K>([&](auto I) {
+    constexpr int i = decltype(I)::value, hi = 1 << i;
+    unroll<(1 << K) / 2>([&](auto Pp) {
+      constexpr int t = pair_lo<i, decltype(Pp)::value>();
+      const uint32_t e = (jl + ((uint32_t)(t & (hi - 1)) << s)) << (logR - 1 - s - i);
+      bfly(x[t], x[t + hi], tw_get(tw, half, e));
+    });
+  });
+}
+// Tile origin of a pass: middle passes read and write (row r, column c) at
+// base + (r << logS) + c, base = u R S + m0 (m0 = the tile's first column);
+// the last pass reads (k0s + c) S0 + v S1 + r and writes output index
+// (k0s + c) + v R0 + k n / R.
+struct TileOrigin {
+  size_t base;
+  uint32_t m0, k0s, v;
 };
 
-// Pass p < P-1: in-place (position-preserving) sub-DFTs with the inter-pass
-// twiddle applied on the way out.  pre: optional g^pos table for a forward
-// coset transform (first pass only).
-__global__ __launch_bounds__(NTT_THREADS) void k_ntt_pass_mid(uint4* __restrict__ dst, const uint4* __restrict__ src,
-                                                               PassArgs a, const uint32_t* __restrict__ twr,
-                                                               const uint32_t* __restrict__ twp,
-                                                               const uint32_t* __restrict__ pre) {
-  quotient_priority();
-  __shared__ uint32_t s[NL * NTT_TILE];
-  __shared__ uint32_t tws[NL * NTT_TWL];
-  const int R = 1 << a.logR, T = a.T;
-  const size_t boff = (size_t)blockIdx.y * a.n;
-  src += 2 * boff;
-  dst += 2 * boff;
-  const TwView tw = stage_twiddles(tws, twr, R >> 1);
-  const uint32_t tiles_per_u = a.S / T;
-  const size_t u = blockIdx.x / tiles_per_u;
-  const uint32_t m0 = (blockIdx.x % tiles_per_u) * T;
-  const size_t ubase = u * (size_t)R * a.S;
-  for (int e = threadIdx.x; e < NTT_TILE; e += NTT_THREADS) {
-    const int c = e % T, j = e / T;
-    const size_t pos = ubase + (size_t)j * a.S + m0 + c;
-    fr x = load_elem(src, pos);
-    if (pre) x = fmul(x, load_table(pre, a.n, pos));
-    lds_put(s, bitrev(j, a.logR) * T + c, x);
+template <bool LAST>
+__device__ __forceinline__ size_t in_pos(const PassGeo& g, const TileOrigin& o, uint32_t r, uint32_t c) {
+  if (LAST) return ((size_t)(o.k0s + c) << g.logS0) + o.base + r;
+  return o.base + ((size_t)r << g.logS) + c;
+}
+
+// (a b - c kc) zk: the quotient's pointwise step on the three transforms'
+// values at position pos (a, b, c canonical; result below 2m).
+__device__ __forceinline__ fr quotient_in(const PassGeo& g, const PassIO& io, const uint4* src, size_t pos) {
+  const fr a = load_elem(src, pos), b = load_elem(src + 2 * g.n, pos), c = load_elem(src + 4 * g.n, pos);
+  return fmul(fsub(fmul(a, b), fmul(c, io.kc)), io.zk);
+}
+
+// Last step of a pass, output row (digit) k of column c: the pass's
+// multiply and its HBM position.  Middle passes multiply by the inter-pass
+// twiddle (result below 2m < 2^256, stored as is); the last pass multiplies
+// by its post table or constant and canonicalises, or reduces the lazy
+// value when there is no multiply.
+template <bool LAST>
+__device__ __forceinline__ fr finish(const PassGeo& g, const PassIO& io, const TileOrigin& o, uint32_t k, uint32_t c,
+                                     const fr& x, size_t& pos) {
+  if (!LAST) {
+    const size_t rel = ((size_t)k << g.logS) + o.m0 + c;
+    pos = o.base + ((size_t)k << g.logS) + c;
+    return fmul(x, load_table(io.twp, (size_t)1 << (g.logR + g.logS), rel));
   }
-  __syncthreads();
-  tile_dit(s, tw, a.logR, T);
-  const size_t twp_count = (size_t)R * a.S;
-  for (int e = threadIdx.x; e < NTT_TILE; e += NTT_THREADS) {
-    const int c = e % T, k = e / T;
-    const size_t rel = (size_t)k * a.S + m0 + c;
-    fr x = lds_get(s, k * T + c);
-    if (k != 0 && (m0 + c) != 0) x = fmul(x, load_table(twp, twp_count, rel));
-    else x = fcsub(x, FrP::MOD2);
-    store_elem(dst, ubase + rel, x);
+  pos = (size_t)(o.k0s + c) + ((size_t)o.v << g.logR0) + ((size_t)k << g.logNR);
+  if (io.post_mode == POST_NONE) return freduce(x);
+  const fr m = io.post_mode == POST_TABLE ? load_table(io.post, g.n, pos) : io.scale;
+  return fcanon(fmul(x, m));
+}
+
+// Everything a step of a tile needs.
+struct TileCtx {
+  uint32_t* s;           // LDS planes
+  const uint32_t* tw;    // LDS twiddles w_R^e
+  uint32_t E, half, logR, logT, smask, cmask, tid, nthr;
+};
+
+// First step of K stages: each group (q, c) loads rows bitrev(q) +
+// bitrev(t) R / 2^K (t < 2^K), optionally pre-multiplied, and leaves the DIT
+// positions (q << K) + t in LDS.
+template <int K, int EPT, bool LAST>
+__device__ __forceinline__ void tile_first(const TileCtx& tc, const PassGeo& g, const PassIO& io, const uint4* src,
+                                           const TileOrigin& o) {
+  for (uint32_t gi = 0; gi < (uint32_t)(EPT >> K); gi++) {
+    const uint32_t grp = tc.tid + gi * tc.nthr;
+    const uint32_t q = grp >> tc.logT, c = grp & tc.cmask;
+    const uint32_t rq = bitrev(q, tc.logR - K);
+    fr x[1 << K];
+    auto row = [&](int t) { return in_pos<LAST>(g, o, rq + (bitrev(t, K) << (tc.logR - K)), c); };
+    if (io.pre_mode == PRE_QUOTIENT) {
+      unroll<(1 << K)>([&](auto T) { x[T] = quotient_in(g, io, src, row(T)); });
+    } else {
+      unroll<(1 << K)>([&](auto T) { x[T] = load_elem(src, row(T)); });
+      if (io.pre_mode == PRE_TABLE)
+        unroll<(1 << K)>([&](auto T) { x[T] = fmul(x[T], load_table(io.pre, g.n, row(T))); });
+    }
+    first_step<K>(x, tc.tw, tc.half, tc.logR);
+    unroll<(1 << K)>([&](auto T) { lds_put(tc.s, tc.E, lds_ix((q << K) + T, c, tc.logT, tc.smask), x[T]); });
   }
 }
 
-// Last pass: sub-DFT over the last (contiguous) digit for T consecutive
-// values of the first digit, digit-reversed store to natural order.
-// post: optional per-output-index table (coset iNTT) or, when post is null
-// and scale_en is set, the constant `scale` (iNTT 1/n).
-__global__ __launch_bounds__(NTT_THREADS) void k_ntt_pass_last(uint4* __restrict__ dst, const uint4* __restrict__ src,
-                                                                PassArgs a, const uint32_t* __restrict__ twr,
-                                                                const uint32_t* __restrict__ pre,
-                                                                const uint32_t* __restrict__ post, fr scale,
-                                                                int scale_en) {
-  quotient_priority();
-  __shared__ uint32_t s[NL * NTT_TILE];
-  __shared__ uint32_t tws[NL * NTT_TWL];
-  const int R = 1 << a.logR, T = a.T;
-  const int E = R * T;
-  const size_t boff = (size_t)blockIdx.y * a.n;
-  src += 2 * boff;
-  dst += 2 * boff;
-  const TwView tw = stage_twiddles(tws, twr, R >> 1);
-  const uint32_t tiles_per_v = a.R0 / T;
-  const uint32_t v = blockIdx.x / tiles_per_v;     // middle digit k_1 (P == 3) or 0
-  const uint32_t k0s = (blockIdx.x % tiles_per_v) * T;
-  const size_t vpos = (size_t)v * a.S1;
-  for (int e = threadIdx.x; e < E; e += NTT_THREADS) {
-    const int c = e / R, j = e % R;
-    const size_t pos = (size_t)(k0s + c) * a.S0 + vpos + j;
-    fr x = load_elem(src, pos);
-    if (pre) x = fmul(x, load_table(pre, a.n, pos));
-    lds_put(s, bitrev(j, a.logR) * T + c, x);
-  }
-  __syncthreads();
-  tile_dit(s, tw, a.logR, T);
-  const size_t kstride = (size_t)a.R0 * a.R1;  // = n / R
-  for (int e = threadIdx.x; e < E; e += NTT_THREADS) {
-    const int c = e % T, k = e / T;
-    const size_t out = (size_t)(k0s + c) + (size_t)a.R0 * v + kstride * k;
-    fr x = lds_get(s, k * T + c);
-    if (post) x = fmul(x, load_table(post, a.n, out));
-    else if (scale_en) x = fmul(x, scale);
-    else x = fcsub(x, FrP::MOD2);
-    store_elem(dst, out, x);
+// A later step of K stages starting at stage s: group (q, c) holds rows
+// j0 + t 2^s; results back to LDS (OUT = false) or out of the pass (OUT =
+// true).  The groups of a step are disjoint, so each thread reads and
+// writes back its own rows and only the barrier between steps is needed.
+template <int K, int EPT, bool LAST, bool OUT>
+__device__ __forceinline__ void tile_step(const TileCtx& tc, const PassGeo& g, const PassIO& io, uint4* dst,
+                                          const TileOrigin& o, uint32_t s) {
+  const uint32_t h = 1u << s;
+  for (uint32_t gi = 0; gi < (uint32_t)(EPT >> K); gi++) {
+    const uint32_t grp = tc.tid + gi * tc.nthr;
+    const uint32_t q = grp >> tc.logT, c = grp & tc.cmask;
+    const uint32_t jl = q & (h - 1);
+    const uint32_t j0 = ((q >> s) << (s + K)) | jl;
+    fr x[1 << K];
+    unroll<(1 << K)>([&](auto T) { x[T] = lds_get(tc.s, tc.E, lds_ix(j0 + ((uint32_t)T << s), c, tc.logT, tc.smask)); });
+    mid_step<K>(x, tc.tw, tc.half, tc.logR, s, jl);
+    if constexpr (OUT) {
+      unroll<(1 << K)>([&](auto T) {
+        size_t pos;
+        const fr y = finish<LAST>(g, io, o, j0 + ((uint32_t)T << s), c, x[T], pos);
+        store_elem_raw(dst, pos, y);
+      });
+    } else {
+      unroll<(1 << K)>([&](auto T) { lds_put(tc.s, tc.E, lds_ix(j0 + ((uint32_t)T << s), c, tc.logT, tc.smask), x[T]); });
+    }
   }
 }
 
-// table[e] = base^(e_hi * e_lo) with (e_hi, e_lo) = (e / cols, e % cols) and
-// the exponent reduced mod 2^log_order; base given in internal form.
-__global__ void k_fill_pow_table(uint32_t* __restrict__ t, size_t count, uint32_t cols, fr base, int log_order,
+// All rows of a tile from LDS straight out (a single-step DFT).
+template <int EPT, bool LAST>
+__device__ __forceinline__ void tile_copy_out(const TileCtx& tc, const PassGeo& g, const PassIO& io, uint4* dst,
+                                              const TileOrigin& o) {
+  for (uint32_t e = tc.tid; e < tc.E; e += tc.nthr) {
+    const uint32_t q = e >> tc.logT, c = e & tc.cmask;
+    size_t pos;
+    const fr y = finish<LAST>(g, io, o, q, c, lds_get(tc.s, tc.E, lds_ix(q, c, tc.logT, tc.smask)), pos);
+    store_elem_raw(dst, pos, y);
+  }
+}
+
+// One pass over tiles of R = 2^logR rows and T = 2^logT columns; block =
+// T*R / 2^min(KMAX, logR) threads; grid = (tiles, batch).  Dynamic LDS: nine
+// planes of T*R words plus nine planes of R/2 twiddles.  Inputs below 2m
+// (canonical words, or the previous pass's outputs).  The DFT runs in steps
+// of KMAX stages, the remainder in the last step.
+template <int KMAX, bool LAST>
+__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(KMAX == 3 ? 2 : 3)))
+void k_ntt_pass(PassGeo g, PassIO io) {
+  quotient_priority();
+  extern __shared__ uint32_t smem[];
+  constexpr int EPT = 1 << KMAX;
+  TileCtx tc;
+  tc.logR = g.logR;
+  tc.logT = g.logT;
+  tc.E = 1u << (g.logR + g.logT);
+  tc.half = 1u << (g.logR - 1);
+  tc.smask = tc.logT >= 5 ? 0u : (tc.logT >= 3 ? (32u >> tc.logT) - 1u : 7u);
+  tc.cmask = (1u << tc.logT) - 1;
+  tc.s = smem;
+  tc.tw = smem + NL * tc.E;
+  tc.tid = threadIdx.x;
+  tc.nthr = blockDim.x;
+
+  const size_t boff = (size_t)blockIdx.y * g.n;
+  const uint4* src = io.src + 2 * boff;
+  uint4* dst = io.dst + 2 * boff;
+
+  TileOrigin o{};
+  if (!LAST) {
+    const uint32_t lt = g.logS - tc.logT;  // tiles per block of R*S elements (log)
+    const size_t u = blockIdx.x >> lt;
+    o.m0 = (blockIdx.x & ((1u << lt) - 1)) << tc.logT;
+    o.base = (u << (g.logR + g.logS)) + o.m0;
+  } else {
+    const uint32_t lt = g.logR0 - tc.logT;
+    o.v = blockIdx.x >> lt;
+    o.k0s = (blockIdx.x & ((1u << lt) - 1)) << tc.logT;
+    o.base = (size_t)o.v << g.logS1;
+  }
+
+  uint32_t* twl = smem + NL * tc.E;
+  for (uint32_t e = tc.tid; e < tc.half; e += tc.nthr) {
+#pragma unroll
+    for (int l = 0; l < NL; l++) twl[l * tc.half + e] = io.twr[l * tc.half + e];
+  }
+  __syncthreads();
+
+  const uint32_t nsteps = (g.logR + KMAX - 1) / KMAX;
+  const uint32_t klast = g.logR - KMAX * (nsteps - 1);
+  if (nsteps == 1) {
+    // a single step (R <= 2^KMAX): the whole DFT in the first step, then out
+    switch (klast) {
+      case 1: tile_first<1, EPT, LAST>(tc, g, io, src, o); break;
+      case 2: if constexpr (KMAX >= 2) tile_first<2, EPT, LAST>(tc, g, io, src, o); break;
+      case 3: if constexpr (KMAX >= 3) tile_first<3, EPT, LAST>(tc, g, io, src, o); break;
+      default: break;
+    }
+    __syncthreads();
+    tile_copy_out<EPT, LAST>(tc, g, io, dst, o);
+    return;
+  }
+  tile_first<KMAX, EPT, LAST>(tc, g, io, src, o);
+  uint32_t stage = KMAX;
+  for (uint32_t st = 1; st + 1 < nsteps; st++) {
+    __syncthreads();
+    tile_step<KMAX, EPT, LAST, false>(tc, g, io, dst, o, stage);
+    stage += KMAX;
+  }
+  __syncthreads();
+  switch (klast) {
+    case 1: tile_step<1, EPT, LAST, true>(tc, g, io, dst, o, stage); break;
+    case 2: if constexpr (KMAX >= 2) tile_step<2, EPT, LAST, true>(tc, g, io, dst, o, stage); break;
+    case 3: if constexpr (KMAX >= 3) tile_step<3, EPT, LAST, true>(tc, g, io, dst, o, stage); break;
+    default: break;
+  }
+}
+
+// ------------------------------------------------------------------ tables
+// table[e] = base^(e_hi * e_lo) * mul with (e_hi, e_lo) = (e >> log_cols, e mod
+// 2^log_cols), the exponent reduced mod 2^log_order; base and mul in internal
+// form.  log_cols = 0 gives base^e (e_lo = 0 would give base^0: handled by
+// the linear variant below).
+__global__ void k_fill_pow_table(uint32_t* __restrict__ t, size_t count, uint32_t log_cols, fr base, int log_order,
                                  fr mul) {
   size_t e = blockIdx.x * (size_t)blockDim.x + threadIdx.x;
   if (e >= count) return;
-  uint64_t ex = (uint64_t)(e / cols) * (uint64_t)(e % cols);
+  uint64_t ex = (uint64_t)(e >> log_cols) * (uint64_t)(e & (((size_t)1 << log_cols) - 1));
   if (log_order < 64) ex &= ((uint64_t)1 << log_order) - 1;
   fr r = fe_one<FrP>(), b = base;
   while (ex) {
@@ -289,8 +428,22 @@ __global__ void k_fill_pow_table(uint32_t* __restrict__ t, size_t count, uint32_
   store_table(t, count, e, r);
 }
 
-// h = (a*b - c) * zinv on the reference's Montgomery words.  With raw words
-// A = a 2^256, fmul(A,B) = ab 2^251, fmul(C, 2^256) = c 2^251 and
+__global__ void k_fill_pow_linear(uint32_t* __restrict__ t, size_t count, fr base, fr mul) {
+  size_t e = blockIdx.x * (size_t)blockDim.x + threadIdx.x;
+  if (e >= count) return;
+  uint64_t ex = e;
+  fr r = fe_one<FrP>(), b = base;
+  while (ex) {
+    if (ex & 1) r = fmul(r, b);
+    b = fsqr(b);
+    ex >>= 1;
+  }
+  store_table(t, count, e, fmul(r, mul));
+}
+
+// h = (a*b - c) * zinv on the reference's Montgomery words (kept for callers
+// that need H itself; the prover fuses it into the last transform).  With raw
+// words A = a 2^256, fmul(A,B) = ab 2^251, fmul(C, 2^256) = c 2^251 and
 // fmul(., z 2^266) = (ab - c) z 2^256: three multiplies per element.
 __global__ void k_quotient_pointwise(uint4* __restrict__ h, const uint4* __restrict__ A, const uint4* __restrict__ B,
                                      const uint4* __restrict__ C, size_t n, fr kc, fr zk) {
@@ -299,11 +452,10 @@ __global__ void k_quotient_pointwise(uint4* __restrict__ h, const uint4* __restr
   if (i >= n) return;
   fr t = fmul(load_elem(A, i), load_elem(B, i));
   fr u = fmul(load_elem(C, i), kc);
-  store_elem(h, i, fmul(fsub(t, u), zk));
+  store_elem_raw(h, i, fcanon(fmul(fsub(t, u), zk)));
 }
 
 // ------------------------------------------------------------------ host side
-// Host copies of field helpers (the device code is ZK_HD so usable here).
 static fr fr_from_mont256_words(const uint64_t w[4]) {
   uint32_t v[8];
   memcpy(v, w, 32);
@@ -332,45 +484,116 @@ static fr fr_inv_host(const fr& x) {
   return fpow(x, e);
 }
 
-static int alloc_table(zk_context* ctx, FrTable& t, size_t count) {
-  t.count = count;
-  if (hipMalloc(&t.d, count * NL * sizeof(uint32_t)) != hipSuccess) {
-    t.d = nullptr;
-    return ctx->fail(ZK_ERR_OOM, "NTT table allocation failed");
+// n^-1 = ((r+1)/2)^log_n (reference ntt.cu:437-458)
+static fr ninv_int(int log_n) {
+  fr two_inv = fr_inv_host(fr_small(2));
+  fr r = fe_one<FrP>();
+  for (int i = 0; i < log_n; i++) r = fmul(r, two_inv);
+  return fcanon(r);
+}
+
+// Pass layout for 2^log_n points: P passes of at most 2^8 points each.
+struct PassShape {
+  int P;
+  int logR[3];
+};
+
+static PassShape pass_shape(int log_n) {
+  PassShape s{};
+  if (log_n <= NTT_MAX_LOGR) {
+    s.P = 1;
+    s.logR[0] = log_n;
+  } else if (log_n <= 2 * NTT_MAX_LOGR) {
+    s.P = 2;
+    s.logR[0] = (log_n + 1) / 2;
+    s.logR[1] = log_n / 2;
+  } else {
+    s.P = 3;
+    s.logR[0] = (log_n + 2) / 3;
+    s.logR[1] = (log_n + 1) / 3;
+    s.logR[2] = log_n / 3;
   }
-  return ZK_OK;
+  return s;
 }
 
-static void free_table(FrTable& t) {
-  if (t.d) (void)hipFree(t.d);
-  t.d = nullptr;
-}
-
-static int fill_pow(zk_context* ctx, FrTable& t, size_t count, uint32_t cols, const fr& base, int log_order,
-                    const fr& mul, hipStream_t st) {
-  ZK_TRY(alloc_table(ctx, t, count));
-  ZK_LAUNCH(ctx, st, "ntt_twiddle_fill", k_fill_pow_table, dim3(cdiv(count, 256)), dim3(256), 0, t.d, count, cols,
-            base, log_order, mul);
-  return ZK_OK;
-}
-
-__global__ void k_fill_pow_linear(uint32_t* __restrict__ t, size_t count, fr base, fr mul) {
-  size_t e = blockIdx.x * (size_t)blockDim.x + threadIdx.x;
-  if (e >= count) return;
-  uint64_t ex = e;
-  fr r = fe_one<FrP>(), b = base;
-  while (ex) {
-    if (ex & 1) r = fmul(r, b);
-    b = fsqr(b);
-    ex >>= 1;
+// Device words of the tables of one plan (both directions), for a plan
+// placed in caller-provided memory.
+static size_t plan_table_words(const PassShape& sh, int log_n) {
+  size_t w = 0;
+  int below = log_n;
+  for (int q = 0; q < sh.P; q++) {
+    w += 2 * ((size_t)1 << (sh.logR[q] - 1)) * NL;
+    if (q < sh.P - 1) w += 2 * ((size_t)1 << below) * NL;
+    below -= sh.logR[q];
   }
-  store_table(t, count, e, fmul(r, mul));
+  return w;
 }
 
-int fill_linear(zk_context* ctx, FrTable& t, const fr& base, const fr& mul, hipStream_t st) {
+static int launch_fill_linear(zk_context* ctx, const FrTable& t, const fr& base, const fr& mul, hipStream_t st) {
   ZK_LAUNCH(ctx, st, "ntt_twiddle_fill", k_fill_pow_linear, dim3(cdiv(t.count, 256)), dim3(256), 0, t.d, t.count,
             base, mul);
   return ZK_OK;
+}
+
+static int launch_fill_pow(zk_context* ctx, const FrTable& t, uint32_t log_cols, const fr& base, int log_order,
+                           const fr& mul, hipStream_t st) {
+  ZK_LAUNCH(ctx, st, "ntt_twiddle_fill", k_fill_pow_table, dim3(cdiv(t.count, 256)), dim3(256), 0, t.d, t.count,
+            log_cols, base, log_order, mul);
+  return ZK_OK;
+}
+
+// Fill every table of plan p (whose FrTable pointers and counts are set) on
+// stream st.
+static int plan_fill(zk_context* ctx, NttPlan* p, hipStream_t st) {
+  const int log_n = p->log_n;
+  const fr one = fe_one<FrP>();
+  fr ninv;
+  memcpy(ninv.l, p->ninv, sizeof(ninv.l));
+  for (int d = 0; d < 2; d++) {
+    const fr w = omega_int(log_n, d == 1);
+    int below = log_n;  // log of R_q * S_q
+    for (int q = 0; q < p->P; q++) {
+      const int lr = p->logR[q];
+      fr wr = w;  // w_{R_q} = w_n^(n / R_q)
+      for (int i = 0; i < log_n - lr; i++) wr = fsqr(wr);
+      ZK_TRY(launch_fill_linear(ctx, p->twr[q][d], wr, one, st));
+      if (q < p->P - 1) {
+        fr wm = w;  // w_{R_q S_q} = w_n^(n / (R_q S_q)); table over (k, m) in [R_q) x [S_q)
+        for (int i = 0; i < log_n - below; i++) wm = fsqr(wm);
+        const fr mul = (d == 1 && q == 0) ? ninv : one;
+        ZK_TRY(launch_fill_pow(ctx, p->twp[q][d], (uint32_t)(below - lr), wm, below, mul, st));
+      }
+      below -= lr;
+    }
+  }
+  return ZK_OK;
+}
+
+// Carve plan tables out of `words` (device memory of plan_table_words).
+static void plan_place(NttPlan* p, uint32_t* words) {
+  int below = p->log_n;
+  for (int q = 0; q < p->P; q++) {
+    for (int d = 0; d < 2; d++) {
+      p->twr[q][d].count = (size_t)1 << (p->logR[q] - 1);
+      p->twr[q][d].d = words;
+      words += p->twr[q][d].count * NL;
+      if (q < p->P - 1) {
+        p->twp[q][d].count = (size_t)1 << below;
+        p->twp[q][d].d = words;
+        words += p->twp[q][d].count * NL;
+      }
+    }
+    below -= p->logR[q];
+  }
+}
+
+static void plan_init(NttPlan* p, int log_n) {
+  const PassShape sh = pass_shape(log_n);
+  p->log_n = log_n;
+  p->P = sh.P;
+  for (int q = 0; q < 3; q++) p->logR[q] = sh.logR[q];
+  const fr ninv = ninv_int(log_n);
+  memcpy(p->ninv, ninv.l, sizeof(p->ninv));
 }
 
 static int plan_get(zk_context* ctx, int log_n, NttPlan** out, hipStream_t st) {
@@ -379,68 +602,36 @@ static int plan_get(zk_context* ctx, int log_n, NttPlan** out, hipStream_t st) {
     *out = it->second;
     return ZK_OK;
   }
-  NttPlan* p = new NttPlan();
-  p->log_n = log_n;
-  if (log_n <= 10) {
-    p->P = 1;
-    p->logR[0] = log_n;
-  } else if (log_n <= 16) {
-    p->P = 2;
-    p->logR[0] = (log_n + 1) / 2;
-    p->logR[1] = log_n / 2;
-  } else {
-    p->P = 3;
-    p->logR[0] = (log_n + 2) / 3;
-    p->logR[1] = (log_n + 1) / 3;
-    p->logR[2] = log_n / 3;
+  std::unique_ptr<NttPlan> p(new NttPlan());
+  plan_init(p.get(), log_n);
+  const size_t words = plan_table_words(pass_shape(log_n), log_n);
+  void* mem = nullptr;
+  if (hipMalloc(&mem, words * 4) != hipSuccess) return ctx->fail(ZK_ERR_OOM, "NTT table allocation failed");
+  plan_place(p.get(), (uint32_t*)mem);
+  // Tables are filled on the caller's stream and waited for before the plan
+  // is cached, so a later call on any stream finds them complete.
+  int rc = plan_fill(ctx, p.get(), st);
+  if (rc == ZK_OK && hipStreamSynchronize(st) != hipSuccess) rc = ctx->fail(ZK_ERR_HIP, "NTT table fill failed");
+  if (rc != ZK_OK) {
+    (void)hipFree(mem);
+    return rc;
   }
-  const fr one = fe_one<FrP>();
-  for (int d = 0; d < 2; d++) {
-    fr w = omega_int(log_n, d == 1);
-    int below = log_n;  // log of R_p * S_p
-    for (int q = 0; q < p->P; q++) {
-      const int lr = p->logR[q];
-      // w_{R_q} = w_n^(n / R_q)
-      fr wr = w;
-      for (int i = 0; i < log_n - lr; i++) wr = fsqr(wr);
-      const size_t half = (size_t)1 << (lr > 0 ? lr - 1 : 0);
-      ZK_TRY(alloc_table(ctx, p->dir[d].twr[q], half));
-      ZK_TRY(fill_linear(ctx, p->dir[d].twr[q], wr, one, st));
-      if (q < p->P - 1) {
-        // w_{R_q S_q} = w_n^(n / (R_q S_q)), table over (k, m) in [R_q) x [S_q)
-        fr wm = w;
-        for (int i = 0; i < log_n - below; i++) wm = fsqr(wm);
-        const size_t S = (size_t)1 << (below - lr);
-        ZK_TRY(fill_pow(ctx, p->dir[d].twp[q], ((size_t)1 << lr) * S, (uint32_t)S, wm, below, one, st));
-      }
-      below -= lr;
-    }
-  }
-  // n^-1 = ((r+1)/2)^log_n (reference ntt.cu:437-458)
-  fr two_inv = fr_inv_host(fr_small(2));
-  fr ninv = one;
-  for (int i = 0; i < log_n; i++) ninv = fmul(ninv, two_inv);
-  ninv = fcanon(ninv);
-  memcpy(p->ninv, ninv.l, sizeof(p->ninv));
-  ctx->ntt_plans[log_n] = p;
-  *out = p;
+  NttPlan* raw = p.release();
+  ctx->ntt_plans[log_n] = raw;
+  *out = raw;
   return ZK_OK;
 }
 
 void ntt_plans_free(zk_context* ctx) {
   for (auto& kv : ctx->ntt_plans) {
     NttPlan* p = kv.second;
-    for (int d = 0; d < 2; d++) {
-      for (auto& t : p->dir[d].twr) free_table(t);
-      for (auto& t : p->dir[d].twp) free_table(t);
-    }
+    if (p->twr[0][0].d) (void)hipFree(p->twr[0][0].d);  // the plan's one allocation starts there
     delete p;
   }
   ctx->ntt_plans.clear();
   for (auto& kv : ctx->coset_tables) {
     CosetTables* c = (CosetTables*)kv.second;
-    free_table(c->fwd);
-    free_table(c->inv);
+    if (c->pre.d) (void)hipFree(c->pre.d);
     delete c;
   }
   ctx->coset_tables.clear();
@@ -454,19 +645,133 @@ static int coset_get(zk_context* ctx, int log_n, uint64_t g, const NttPlan* plan
     *out = (CosetTables*)it->second;
     return ZK_OK;
   }
-  CosetTables* c = new CosetTables();
   const size_t n = (size_t)1 << log_n;
-  fr gi = fr_small(g);
-  fr ginv = fr_inv_host(gi);
-  fr ninv;
-  memcpy(ninv.l, plan->ninv, sizeof(ninv.l));
-  ctx->coset_tables[key] = c;
-  ZK_TRY(alloc_table(ctx, c->fwd, n));
-  ZK_TRY(alloc_table(ctx, c->inv, n));
-  ZK_TRY(fill_linear(ctx, c->fwd, gi, fe_one<FrP>(), st));   // g^i
-  ZK_TRY(fill_linear(ctx, c->inv, ginv, ninv, st));          // n^-1 g^-i
-  *out = c;
+  std::unique_ptr<CosetTables> c(new CosetTables());
+  void* mem = nullptr;
+  if (hipMalloc(&mem, 3 * n * NL * 4) != hipSuccess) return ctx->fail(ZK_ERR_OOM, "coset table allocation failed");
+  uint32_t* w = (uint32_t*)mem;
+  c->pre = FrTable{w, n};
+  c->post_inv = FrTable{w + n * NL, n};
+  c->post_fold = FrTable{w + 2 * n * NL, n};
+  const fr gi = fr_small(g), ginv = fr_inv_host(gi);
+  fr scale = fe_one<FrP>();
+  if (plan->P == 1) memcpy(scale.l, plan->ninv, sizeof(scale.l));
+  int rc = launch_fill_linear(ctx, c->pre, gi, fe_one<FrP>(), st);            // g^i
+  if (rc == ZK_OK) rc = launch_fill_linear(ctx, c->post_inv, ginv, scale, st);  // g^-i (/ n when P == 1)
+  if (rc == ZK_OK) rc = launch_fill_linear(ctx, c->post_fold, gi, scale, st);   // g^i (/ n when P == 1)
+  if (rc == ZK_OK && hipStreamSynchronize(st) != hipSuccess) rc = ctx->fail(ZK_ERR_HIP, "coset table fill failed");
+  if (rc != ZK_OK) {
+    (void)hipFree(mem);
+    return rc;
+  }
+  CosetTables* raw = c.release();
+  ctx->coset_tables[key] = raw;
+  *out = raw;
   return ZK_OK;
+}
+
+// One transform (or a batch of them) over prepared tables.
+//   src -> dst; mid: n*batch elements for the passes before the last (may be
+//   src when src is writable and differs from dst; never dst);
+//   pre/post modes as in PassIO (PRE_QUOTIENT reads src, src + n, src + 2n).
+struct NttCall {
+  void* dst;
+  const void* src;
+  void* mid;
+  int log_n, inverse, batch;
+  int pre_mode, post_mode;
+  const uint32_t* pre;
+  const uint32_t* post;
+  fr kc, zk;
+  int kmax;  // 2 or 3: elements per thread 4 or 8
+};
+
+// Tiles of 2048 elements take 78 KB of LDS: above the 64 KB a launch may
+// request by default.
+static void ntt_lds_limits() {
+  static std::once_flag once;
+  std::call_once(once, [] {
+    const int bytes = 160 * 1024;
+    (void)hipFuncSetAttribute((const void*)k_ntt_pass<3, true>, hipFuncAttributeMaxDynamicSharedMemorySize, bytes);
+    (void)hipFuncSetAttribute((const void*)k_ntt_pass<3, false>, hipFuncAttributeMaxDynamicSharedMemorySize, bytes);
+    (void)hipFuncSetAttribute((const void*)k_ntt_pass<2, true>, hipFuncAttributeMaxDynamicSharedMemorySize, bytes);
+    (void)hipFuncSetAttribute((const void*)k_ntt_pass<2, false>, hipFuncAttributeMaxDynamicSharedMemorySize, bytes);
+  });
+}
+
+static int ntt_exec(zk_context* ctx, const NttPlan* plan, const NttCall& c, hipStream_t st) {
+  ntt_lds_limits();
+  const int d = c.inverse ? 1 : 0;
+  const int L = c.log_n, P = plan->P;
+  const size_t n = (size_t)1 << L;
+  const int kmax = c.kmax;
+  const int logE = std::min(L, kmax == 3 ? 11 : 10);
+  int logS[3];
+  {
+    int s = L;
+    for (int q = 0; q < P; q++) {
+      s -= plan->logR[q];
+      logS[q] = s;
+    }
+  }
+  for (int q = 0; q < P; q++) {
+    const bool last = q == P - 1;
+    PassGeo g{};
+    g.logR = (uint32_t)plan->logR[q];
+    g.n = n;
+    PassIO io{};
+    io.twr = plan->twr[q][d].d;
+    io.src = (const uint4*)(q == 0 ? c.src : c.mid);
+    io.dst = (uint4*)(last ? c.dst : c.mid);
+    io.pre_mode = q == 0 ? c.pre_mode : PRE_NONE;
+    io.pre = c.pre;
+    io.kc = c.kc;
+    io.zk = c.zk;
+    if (!last) {
+      g.logS = (uint32_t)logS[q];
+      g.logT = (uint32_t)std::min(logE - plan->logR[q], logS[q]);
+      io.twp = plan->twp[q][d].d;
+    } else {
+      g.logR0 = P == 1 ? 0 : (uint32_t)plan->logR[0];
+      g.logS0 = P == 1 ? 0 : (uint32_t)logS[0];
+      g.logS1 = P == 3 ? (uint32_t)logS[1] : 0;
+      g.logNR = (uint32_t)(L - plan->logR[q]);
+      g.logT = P == 1 ? 0 : (uint32_t)std::min(logE - plan->logR[q], (int)g.logR0);
+      io.post_mode = c.post_mode;
+      io.post = c.post;
+      if (c.post_mode == POST_SCALE) memcpy(io.scale.l, plan->ninv, sizeof(io.scale.l));
+    }
+    const uint32_t E = 1u << (g.logR + g.logT);
+    const uint32_t kk = std::min<uint32_t>((uint32_t)kmax, g.logR);
+    const uint32_t threads = std::max<uint32_t>(1, E >> kk);
+    const uint32_t tiles = (uint32_t)(n / E);
+    const size_t lds = (size_t)NL * 4 * (E + (1u << (g.logR - 1)));
+    const dim3 grid(tiles, c.batch), block(threads);
+    if (kmax == 3 && g.logR >= 3) {
+      if (last)
+        ZK_LAUNCH(ctx, st, "ntt_pass", (k_ntt_pass<3, true>), grid, block, lds, g, io);
+      else
+        ZK_LAUNCH(ctx, st, "ntt_pass", (k_ntt_pass<3, false>), grid, block, lds, g, io);
+    } else if (g.logR >= 2) {
+      if (last)
+        ZK_LAUNCH(ctx, st, "ntt_pass", (k_ntt_pass<2, true>), grid, block, lds, g, io);
+      else
+        ZK_LAUNCH(ctx, st, "ntt_pass", (k_ntt_pass<2, false>), grid, block, lds, g, io);
+    } else {
+      if (last)
+        ZK_LAUNCH(ctx, st, "ntt_pass", (k_ntt_pass<1, true>), grid, block, lds, g, io);
+      else
+        ZK_LAUNCH(ctx, st, "ntt_pass", (k_ntt_pass<1, false>), grid, block, lds, g, io);
+    }
+  }
+  return ZK_OK;
+}
+
+// Elements per thread: 8 for large transforms (throughput), 4 below (a
+// thread's elements are a serial chain, so small transforms want more
+// threads).
+static int choose_kmax(int log_n, int batch) {
+  return ((size_t)batch << log_n) >= ((size_t)1 << 19) ? 3 : 2;
 }
 
 int ntt_run(zk_context* ctx, void* d_out, const void* d_in, int log_n, int inverse, int batch, uint64_t coset_g,
@@ -477,76 +782,98 @@ int ntt_run(zk_context* ctx, void* d_out, const void* d_in, int log_n, int inver
   ZK_TRY(plan_get(ctx, log_n, &plan, st));
   CosetTables* cos = nullptr;
   if (coset_g) ZK_TRY(coset_get(ctx, log_n, coset_g, plan, &cos, st));
-  const int d = inverse ? 1 : 0;
   const size_t n = (size_t)1 << log_n;
-  const uint32_t* pre = (cos && !inverse) ? cos->fwd.d : nullptr;
-  const uint32_t* post = (cos && inverse) ? cos->inv.d : nullptr;
-  fr scale;
-  memcpy(scale.l, plan->ninv, sizeof(scale.l));
-  const int scale_en = inverse ? 1 : 0;
-  const int P = plan->P;
-
-  const uint4* src = (const uint4*)d_in;
-  uint4* out = (uint4*)d_out;
-  if (P > 1) ZK_TRY(ctx->ensure(ctx->scratch_a, n * 32 * (size_t)batch));
-  uint4* scr = (uint4*)ctx->scratch_a.p;
-
-  size_t strides[3];
-  {
-    size_t s = n;
-    for (int q = 0; q < P; q++) {
-      s >>= plan->logR[q];
-      strides[q] = s;
+  NttCall c{};
+  c.dst = d_out;
+  c.src = d_in;
+  c.log_n = log_n;
+  c.inverse = inverse;
+  c.batch = batch;
+  c.kmax = choose_kmax(log_n, batch);
+  if (plan->P > 1) {
+    ZK_TRY(ctx->ensure(ctx->scratch_a, n * 32 * (size_t)batch));
+    c.mid = ctx->scratch_a.p;
+  }
+  c.pre_mode = (cos && !inverse) ? PRE_TABLE : PRE_NONE;
+  c.pre = cos ? cos->pre.d : nullptr;
+  if (inverse) {
+    if (cos) {
+      c.post_mode = POST_TABLE;
+      c.post = cos->post_inv.d;
+    } else {
+      c.post_mode = plan->P == 1 ? POST_SCALE : POST_NONE;
     }
   }
-  for (int q = 0; q < P - 1; q++) {
-    PassArgs a{};
-    a.logR = plan->logR[q];
-    a.T = NTT_TILE >> a.logR;
-    a.S = (uint32_t)strides[q];
-    a.n = n;
-    dim3 grid(cdiv(n, NTT_TILE), batch);
-    ZK_LAUNCH(ctx, st, "ntt_pass", k_ntt_pass_mid, grid, dim3(NTT_THREADS), 0, scr, q == 0 ? src : scr, a,
-              plan->dir[d].twr[q].d, plan->dir[d].twp[q].d, q == 0 ? pre : nullptr);
-  }
-  PassArgs a{};
-  a.logR = plan->logR[P - 1];
-  a.n = n;
-  if (P == 1) {
-    a.T = 1;
-    a.R0 = 1;
-    a.S0 = 0;
-    a.R1 = 1;
-    a.S1 = 0;
-  } else {
-    a.T = NTT_TILE >> a.logR;
-    a.R0 = 1u << plan->logR[0];
-    a.S0 = (uint32_t)strides[0];
-    a.R1 = P == 3 ? (1u << plan->logR[1]) : 1;
-    a.S1 = P == 3 ? (uint32_t)strides[1] : 0;
-  }
-  const uint32_t tiles = P == 1 ? 1 : (uint32_t)(n / ((size_t)a.T << a.logR));
-  dim3 grid(tiles, batch);
-  ZK_LAUNCH(ctx, st, "ntt_pass", k_ntt_pass_last, grid, dim3(NTT_THREADS), 0, out, P == 1 ? src : scr, a,
-            plan->dir[d].twr[P - 1].d, P == 1 ? pre : nullptr, post, scale, post ? 0 : scale_en);
-  return ZK_OK;
+  return ntt_exec(ctx, plan, c, st);
 }
 
-int quotient_pointwise(zk_context* ctx, void* d_h, const void* d_a, const void* d_b, const void* d_c, size_t n,
-                       const uint64_t zinv_mont[4], hipStream_t st) {
-  // kc = 2^256 mod r as a raw integer.  With z_mont = z 2^256 (raw words),
-  // zk = z 2^266 = fmul(z_mont, 2^271 raw).
+// (kc, zk) of the pointwise quotient step for (g^n - 1)^-1 given in
+// Montgomery words: kc = 2^256 mod r as a raw integer, zk = z 2^266.
+static void quotient_consts(const uint64_t zinv_mont[4], fr& kc, fr& zk) {
   static const uint32_t K256[8] = {0x4ffffffbu, 0xac96341cu, 0x9f60cd29u, 0x36fc7695u,
                                    0x7879462eu, 0x666ea36fu, 0x9a07df2fu, 0x0e0a77c1u};  // 2^256 mod r
   static const uint32_t K271[8] = {0x2ffd5addu, 0x29ab3316u, 0xf4f5739fu, 0x3b9f942fu,
                                    0x3ca28ff2u, 0x84aad391u, 0xf9a8c5dfu, 0x1ed378c2u};  // 2^271 mod r
-  fr kc = repack_in<FrP>(K256);
+  kc = repack_in<FrP>(K256);
   uint32_t zw[8];
   memcpy(zw, zinv_mont, 32);
-  fr zk = fmul(repack_in<FrP>(zw), repack_in<FrP>(K271));
+  zk = fmul(repack_in<FrP>(zw), repack_in<FrP>(K271));
+}
+
+int quotient_pointwise(zk_context* ctx, void* d_h, const void* d_a, const void* d_b, const void* d_c, size_t n,
+                       const uint64_t zinv_mont[4], hipStream_t st) {
+  fr kc, zk;
+  quotient_consts(zinv_mont, kc, zk);
   ZK_LAUNCH(ctx, st, "quotient_pointwise", k_quotient_pointwise, dim3(cdiv(n, 256)), dim3(256), 0, (uint4*)d_h,
             (const uint4*)d_a, (const uint4*)d_b, (const uint4*)d_c, n, kc, zk);
   return ZK_OK;
+}
+
+// The transforms of the quotient (groth16.cu:321-383) on evaluations
+// abc = A | B | C (3n elements, destroyed; work: 3n more elements):
+//   3 inverse transforms whose outputs are multiplied by g^i (the coset
+//   shift of the next step, with 1/n in the first inter-pass table);
+//   3 forward transforms -> A, B, C on the coset g H;
+//   one inverse transform whose first pass forms (A B - C) / Z from the three
+//   and whose output is multiplied by g^-i -> h.
+int quotient_ntts(zk_context* ctx, void* d_h, void* d_abc, void* d_work, int log_n, uint64_t g,
+                  const uint64_t zinv_mont[4], hipStream_t st) {
+  NttPlan* plan = nullptr;
+  ZK_TRY(plan_get(ctx, log_n, &plan, st));
+  CosetTables* cos = nullptr;
+  ZK_TRY(coset_get(ctx, log_n, g, plan, &cos, st));
+  NttCall c{};
+  c.log_n = log_n;
+  c.batch = 3;
+  c.kmax = choose_kmax(log_n, 3);
+  // coefficients * g^i: X -> Y (X is writable: the passes before the last run in it)
+  c.src = d_abc;
+  c.dst = d_work;
+  c.mid = d_abc;
+  c.inverse = 1;
+  c.post_mode = POST_TABLE;
+  c.post = cos->post_fold.d;
+  ZK_TRY(ntt_exec(ctx, plan, c, st));
+  // coset evaluations: Y -> X
+  c.src = d_work;
+  c.dst = d_abc;
+  c.mid = d_work;
+  c.inverse = 0;
+  c.post_mode = POST_NONE;
+  c.post = nullptr;
+  ZK_TRY(ntt_exec(ctx, plan, c, st));
+  // h: (A B - C) / Z from X, through Y, to d_h
+  quotient_consts(zinv_mont, c.kc, c.zk);
+  c.batch = 1;
+  c.kmax = choose_kmax(log_n, 1);
+  c.src = d_abc;
+  c.dst = d_h;
+  c.mid = d_work;
+  c.inverse = 1;
+  c.pre_mode = PRE_QUOTIENT;
+  c.post_mode = POST_TABLE;
+  c.post = cos->post_inv.d;
+  return ntt_exec(ctx, plan, c, st);
 }
 
 }  // namespace zk

@@ -153,6 +153,11 @@ inline uint32_t cdiv(size_t a, size_t b) { return (uint32_t)((a + b - 1) / b); }
 // ---- NTT (ntt.hip)
 int ntt_run(zk_context* ctx, void* d_out, const void* d_in, int log_n, int inverse, int batch, uint64_t coset_g,
             hipStream_t st);
+// The quotient's transforms (ntt.hip): abc = A | B | C evaluations on the
+// domain (3n elements, destroyed), work: 3n elements; h receives the
+// coefficients of (A B - C) / (x^n - 1) through the coset g H.
+int quotient_ntts(zk_context* ctx, void* d_h, void* d_abc, void* d_work, int log_n, uint64_t g,
+                  const uint64_t zinv_mont[4], hipStream_t st);
 // Pointwise H step: h = (a*b - c) * zinv over n elements (ntt.hip)
 int quotient_pointwise(zk_context* ctx, void* d_h, const void* d_a, const void* d_b, const void* d_c, size_t n,
                        const uint64_t zinv_mont[4], hipStream_t st);

@@ -53,7 +53,8 @@ int fh_op(int op, const uint32_t* a, const uint32_t* b, const uint32_t* c, const
 }
 
 // The NTT butterfly's Fr operations (the same templates over the scalar
-// field): 0 fmul, 1 fadd_wide, 2 fcsub(a, 2r), 3 fsub_lazy (a + 2r - b).
+// field): 0 fmul, 1 fadd_wide, 2 fcsub(a, 2r), 3 fsub_lazy (a + 2r - b),
+// 4 / 5 / 7: a - b + 4r / 8r / 2r, 6 freduce (canonical value).
 int fh_fr_op(int op, const uint32_t* a, const uint32_t* b, uint32_t* out) {
   fr A, B, r;
   memcpy(A.l, a, sizeof(A.l));
@@ -63,6 +64,10 @@ int fh_fr_op(int op, const uint32_t* a, const uint32_t* b, uint32_t* out) {
     case 1: r = fadd_wide(A, B); break;
     case 2: r = fcsub(A, FrP::MOD2); break;
     case 3: r = fsub_lazy(A, B); break;
+    case 4: r = fsub_off<4>(A, B); break;
+    case 5: r = fsub_off<8>(A, B); break;
+    case 6: r = freduce(A); break;
+    case 7: r = fsub_off<2>(A, B); break;
     default: return -1;
   }
   memcpy(out, r.l, sizeof(r.l));

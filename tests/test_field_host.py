@@ -170,6 +170,51 @@ def test_ntt_lazy_butterfly_bounds(fh):
             assert (s - x - y * w * rinv) % r == 0 and (d - x + y * w * rinv) % r == 0
 
 
+def test_ntt_offset_subtract_and_reduce(fh):
+    """The NTT pass's lazy helpers: fsub_off<K>(a, b) = a - b + K r exactly for
+    b < K r (K = 2, 4, 8; a up to 26r), and freduce gives the canonical value
+    of any normalized input below 2^261 (its top-limb quotient estimate may
+    fall 2 short: the two conditional subtractions must absorb that)."""
+    rng = random.Random(21)
+    r = ORDER
+    for code, K in ((7, 2), (4, 4), (5, 8)):
+        for _ in range(60):
+            a = rng.randrange(26 * r)
+            b = rng.choice([0, K * r - 1, rng.randrange(K * r)])
+            assert fr_op(fh, code, a, b) == a - b + K * r
+    edge = [0, 1, r - 1, r, r + 1, 2 * r - 1, 2 * r, 3 * r - 1, 26 * r, (1 << 261) - 1, (1 << 260) + 12345]
+    # values just below and above multiples of r, where the estimate is tight
+    edge += [k * r + d for k in (1, 5, 17, 100, 168) for d in (-1, 0, 1) if 0 <= k * r + d < 1 << 261]
+    for x in edge + [rng.randrange(1 << 261) for _ in range(200)]:
+        assert fr_op(fh, 6, x) == x % r, hex(x)
+
+
+def test_ntt_grow_butterfly_chain(fh):
+    """The pass kernel's arithmetic on one element path: a first radix-8 step
+    with twiddle-free butterflies (offsets 2r, 4r, 8r) and five twiddled
+    stages (u + w v, u - w v + 2r, no reduction) keep normalized limbs and
+    values below 26r, congruent to the exact result; freduce finishes."""
+    rng = random.Random(22)
+    r = ORDER
+    rinv = pow(RP, -1, r)
+    for _ in range(30):
+        u, v = rng.randrange(2 * r), rng.randrange(2 * r)
+        exact_u = u
+        for code, K in ((7, 2), (4, 4), (5, 8)):   # sub-stages 0..2, twiddle 1 (worst-case growth path)
+            u, v = fr_op(fh, 1, u, v), fr_op(fh, code, u, v)
+            assert u < 2 * K * r and v < 2 * K * r
+        exact_u, exact_v = u % r, v % r
+        for _ in range(5):
+            w = rng.randrange(r)
+            t = fr_op(fh, 0, v, w)
+            assert t < 2 * r
+            u, v = fr_op(fh, 1, u, t), fr_op(fh, 7, u, t)
+            tv = exact_v * w * rinv % r
+            exact_u, exact_v = (exact_u + tv) % r, (exact_u - tv) % r
+        assert u < 26 * r and v < 26 * r
+        assert fr_op(fh, 6, u) == exact_u and fr_op(fh, 6, v) == exact_v
+
+
 def test_add_sub_mulsub(fh):
     rng = random.Random(4)
     for a in samples(rng, 2 * Q):
