@@ -62,6 +62,10 @@ int zk_create(int device, zk_context** out) {
   if (hipGetDeviceCount(&count) != hipSuccess || count <= 0) return ZK_ERR_HIP;
   if (device < 0 || device >= count) return ZK_ERR_INVALID;
   if (hipSetDevice(device) != hipSuccess) return ZK_ERR_HIP;
+  // device address of the no-allocation NTT's fixed scratch, once per
+  // device with the device current; a failed lookup is recorded and only
+  // zk_ntt_noalloc reports it
+  (void)ntt_scratch_init(device);
   zk_context* ctx = new zk_context();
   ctx->device = device;
   if (hipStreamCreateWithFlags(&ctx->stream, hipStreamNonBlocking) != hipSuccess) {

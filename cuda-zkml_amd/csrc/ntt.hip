@@ -876,6 +876,87 @@ int quotient_ntts(zk_context* ctx, void* d_h, void* d_abc, void* d_work, int log
   return ntt_exec(ctx, plan, c, st);
 }
 
+// ------------------------------------------------------------------ no-allocation variant
+// zk_ntt_noalloc runs the same kernels with its twiddle tables and its
+// pass-to-pass buffer in `scratch`, a fixed device array of this library:
+// every GPU holds one copy from module load to process end, and every call
+// on that GPU shares it (the tables of the last log_n stay there, so a call
+// of the same size only launches the passes; calls that overlap on one GPU
+// race).  Limits: 2^NTT_NA_MAX_LOG points per transform and
+// 2^NTT_NA_MAX_ELEMS_LOG elements per call.
+constexpr int NTT_NA_MAX_LOG = 16;
+constexpr int NTT_NA_MAX_ELEMS_LOG = 18;
+// tables of the largest plan (log_n = 16: two passes of 2^8, a 2^16-entry
+// inter-pass table per direction) and the pass-to-pass buffer, in words
+constexpr size_t NTT_NA_TABLE_WORDS = 2 * 2 * 128 * NL + 2 * ((size_t)1 << 16) * NL;
+constexpr size_t NTT_NA_MID_WORDS = ((size_t)1 << NTT_NA_MAX_ELEMS_LOG) * 8;
+constexpr size_t NTT_NA_WORDS = NTT_NA_TABLE_WORDS + NTT_NA_MID_WORDS;
+
+static __device__ __align__(256) uint32_t scratch[NTT_NA_WORDS];
+
+constexpr int NTT_NA_DEVICES = 64;
+static std::mutex g_na_mu;
+static uint32_t* g_na_ptr[NTT_NA_DEVICES];   // device address of `scratch` per GPU
+static int g_na_status[NTT_NA_DEVICES];      // 0 not looked up, 1 ok, -1 lookup failed
+static int g_na_log_n[NTT_NA_DEVICES];       // log_n whose tables `scratch` holds (0: none)
+
+// Once per device, with that device current (zk_create): the device address
+// of `scratch`.  The host-side name `scratch` is no device address; kernels
+// and copies get this pointer.
+int ntt_scratch_init(int device) {
+  if (device < 0 || device >= NTT_NA_DEVICES) return ZK_ERR_INVALID;
+  std::lock_guard<std::mutex> lk(g_na_mu);
+  if (g_na_status[device] != 0) return g_na_status[device] > 0 ? ZK_OK : ZK_ERR_HIP;
+  void* p = nullptr;
+  const hipError_t e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+  g_na_status[device] = (e == hipSuccess && p) ? 1 : -1;
+  g_na_ptr[device] = g_na_status[device] > 0 ? (uint32_t*)p : nullptr;
+  return g_na_status[device] > 0 ? ZK_OK : ZK_ERR_HIP;
+}
+
+static_assert(NTT_NA_TABLE_WORDS >= 2 * 2 * 128 * NL, "scratch holds every plan up to 2^16");
+
+int ntt_run_noalloc(zk_context* ctx, void* d_out, const void* d_in, int log_n, int inverse, int batch,
+                    hipStream_t st) {
+  if (!d_out || !d_in || batch < 1) return ctx->fail(ZK_ERR_INVALID, "ntt_noalloc: null buffer or batch < 1");
+  if (log_n < 1 || log_n > NTT_NA_MAX_LOG)
+    return ctx->fail(ZK_ERR_SIZE, "ntt_noalloc: log_n outside [1, 16] (the fixed scratch holds 2^16-point plans)");
+  if (((size_t)batch << log_n) > ((size_t)1 << NTT_NA_MAX_ELEMS_LOG))
+    return ctx->fail(ZK_ERR_SIZE, "ntt_noalloc: batch * 2^log_n above 2^18 elements (the fixed scratch's buffer)");
+  const int dev = ctx->device;
+  uint32_t* base;
+  bool fill;
+  {
+    std::lock_guard<std::mutex> lk(g_na_mu);
+    if (dev < 0 || dev >= NTT_NA_DEVICES || g_na_status[dev] <= 0)
+      return ctx->fail(ZK_ERR_HIP, "ntt_noalloc: scratch address of this device unknown");
+    base = g_na_ptr[dev];
+    fill = g_na_log_n[dev] != log_n;
+    g_na_log_n[dev] = log_n;
+  }
+  NttPlan plan;
+  plan_init(&plan, log_n);
+  plan_place(&plan, base);
+  if (fill) {
+    const int rc = plan_fill(ctx, &plan, st);
+    if (rc != ZK_OK) {
+      std::lock_guard<std::mutex> lk(g_na_mu);
+      g_na_log_n[dev] = 0;
+      return rc;
+    }
+  }
+  NttCall c{};
+  c.dst = d_out;
+  c.src = d_in;
+  c.mid = base + NTT_NA_TABLE_WORDS;
+  c.log_n = log_n;
+  c.inverse = inverse;
+  c.batch = batch;
+  c.kmax = choose_kmax(log_n, batch);
+  if (inverse) c.post_mode = plan.P == 1 ? POST_SCALE : POST_NONE;
+  return ntt_exec(ctx, &plan, c, st);
+}
+
 }  // namespace zk
 
 extern "C" {
@@ -900,6 +981,11 @@ static int zk_coset_ntt_impl(zk_context* ctx, void* d_out, const void* d_in, int
 int zk_coset_ntt(zk_context* ctx, void* d_out, const void* d_in, int log_n, uint64_t g, int inverse, int batch,
                  void* stream) {
   return zk::guard(ctx, [&] { return zk_coset_ntt_impl(ctx, d_out, d_in, log_n, g, inverse, batch, stream); });
+}
+
+int zk_ntt_noalloc(zk_context* ctx, void* d_out, const void* d_in, int log_n, int inverse, int batch, void* stream) {
+  if (!ctx) return ZK_ERR_INVALID;
+  return zk::guard(ctx, [&] { return zk::ntt_run_noalloc(ctx, d_out, d_in, log_n, inverse, batch, ctx->s(stream)); });
 }
 
 }  // extern "C"

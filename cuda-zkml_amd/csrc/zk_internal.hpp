@@ -153,6 +153,11 @@ inline uint32_t cdiv(size_t a, size_t b) { return (uint32_t)((a + b - 1) / b); }
 // ---- NTT (ntt.hip)
 int ntt_run(zk_context* ctx, void* d_out, const void* d_in, int log_n, int inverse, int batch, uint64_t coset_g,
             hipStream_t st);
+// Device address of the no-allocation NTT's fixed scratch on `device`
+// (looked up once per device, with that device current).
+int ntt_scratch_init(int device);
+int ntt_run_noalloc(zk_context* ctx, void* d_out, const void* d_in, int log_n, int inverse, int batch,
+                    hipStream_t st);
 // The quotient's transforms (ntt.hip): abc = A | B | C evaluations on the
 // domain (3n elements, destroyed), work: 3n elements; h receives the
 // coefficients of (A B - C) / (x^n - 1) through the coset g H.

@@ -67,6 +67,7 @@ def lib():
         L.zk_kernel_stats_names.restype = ctypes.c_char_p
         L.zk_kernel_stats_names.argtypes = [vp]
         L.zk_ntt.argtypes = [vp, vp, vp, ctypes.c_int, ctypes.c_int, ctypes.c_int, vp]
+        L.zk_ntt_noalloc.argtypes = [vp, vp, vp, ctypes.c_int, ctypes.c_int, ctypes.c_int, vp]
         L.zk_coset_ntt.argtypes = [vp, vp, vp, ctypes.c_int, ctypes.c_uint64, ctypes.c_int, ctypes.c_int, vp]
         L.zk_msm_g1.argtypes = [vp, vp, vp, ctypes.c_size_t, vp, vp]
         L.zk_msm_g2.argtypes = [vp, vp, vp, ctypes.c_size_t, vp, vp]
@@ -255,6 +256,11 @@ class Context:
     # ---- NTT
     def ntt(self, d_out, d_in, log_n, inverse=False, batch=1):
         self._check(lib().zk_ntt(self.h, vp(d_out.ptr), vp(d_in.ptr), log_n, int(inverse), batch, None), "zk_ntt")
+
+    def ntt_noalloc(self, d_out, d_in, log_n, inverse=False, batch=1):
+        """zk_ntt_noalloc: the same transform with no device allocation."""
+        self._check(lib().zk_ntt_noalloc(self.h, vp(d_out.ptr), vp(d_in.ptr), log_n, int(inverse), batch, None),
+                    "zk_ntt_noalloc")
 
     def coset_ntt(self, d_out, d_in, log_n, g, inverse=False, batch=1):
         self._check(lib().zk_coset_ntt(self.h, vp(d_out.ptr), vp(d_in.ptr), log_n, g, int(inverse), batch, None),

@@ -89,6 +89,18 @@ const char* zk_kernel_stats_names(zk_context* ctx);
  * of n elements each are laid out back to back. */
 int zk_ntt(zk_context* ctx, void* d_out, const void* d_in, int log_n, int inverse, int batch, void* stream);
 
+/* No counterpart in the reference: zk_ntt for callers that cannot allocate
+ * device memory (code under HIP graph capture, tight serving loops, harnesses
+ * that forbid hipMalloc).  Same transform, layouts and stream argument as
+ * zk_ntt, with 1 <= log_n <= 16 and batch * 2^log_n <= 2^18 elements; larger
+ * sizes return ZK_ERR_SIZE.  Allocates nothing: its twiddle tables and
+ * pass-to-pass buffer live in a fixed device array of the library (13 MB per
+ * GPU, held from library load to process end) that every call on a GPU
+ * shares and that keeps the last call's contents (the tables of the last
+ * log_n are reused).  Calls that overlap on one GPU race: order them on one
+ * stream or synchronize between them. */
+int zk_ntt_noalloc(zk_context* ctx, void* d_out, const void* d_in, int log_n, int inverse, int batch, void* stream);
+
 /* Coset NTT as used by Groth16Prover::compute_h (src/prover/groth16.cu:350-383):
  * forward: out = NTT(in[i] * g^i); inverse: out[i] = iNTT(in)[i] * g^-i.
  * g is a small plain integer (the prover uses 5; BASELINE config 2 uses 7). */
