@@ -770,8 +770,14 @@ static int ntt_exec(zk_context* ctx, const NttPlan* plan, const NttCall& c, hipS
 // Elements per thread: 8 for large transforms (throughput), 4 below (a
 // thread's elements are a serial chain, so small transforms want more
 // threads).
+#ifndef ZK_NTT_KMAX_LARGE
+#define ZK_NTT_KMAX_LARGE 3
+#endif
+#ifndef ZK_NTT_LARGE_LOG
+#define ZK_NTT_LARGE_LOG 19
+#endif
 static int choose_kmax(int log_n, int batch) {
-  return ((size_t)batch << log_n) >= ((size_t)1 << 19) ? 3 : 2;
+  return ((size_t)batch << log_n) >= ((size_t)1 << ZK_NTT_LARGE_LOG) ? ZK_NTT_KMAX_LARGE : 2;
 }
 
 int ntt_run(zk_context* ctx, void* d_out, const void* d_in, int log_n, int inverse, int batch, uint64_t coset_g,

@@ -909,6 +909,28 @@ void orc_ntt(uint64_t* data, int log_n, int inverse, int threads) {
   ntt_radix2(a, log_n, inverse != 0, threads);
   memcpy(data, a.data(), n * 32);
 }
+// sum_i a_i b_i mod r for standard-form words (the scalar of a closed-form
+// MSM over points k_i G with scalars s_i), written in standard form.
+void orc_fr_dot_std(const uint64_t* a, const uint64_t* b, size_t n, uint64_t* out) {
+  Fr acc = Fr::zero();
+  for (size_t i = 0; i < n; i++) acc = acc + Fr::from_std(a + 4 * i) * Fr::from_std(b + 4 * i);
+  acc.to_std(out);
+}
+
+// coeff[i] *= g^i (g^-i with inverse): the coset loops of compute_h
+// (groth16.cu:352-358 and 377-383) for a small plain integer g.
+void orc_coset_scale(uint64_t* data, int log_n, uint64_t g, int inverse) {
+  const size_t n = (size_t)1 << log_n;
+  Fr gi = Fr::from_uint(g);
+  if (inverse) gi = gi.inv();
+  Fr gp = Fr::one();
+  for (size_t i = 0; i < n; i++) {
+    Fr x = Fr::raw(data + 4 * i) * gp;
+    memcpy(data + 4 * i, x.v, 32);
+    gp = gp * gi;
+  }
+}
+
 void orc_dft_naive(const uint64_t* in, uint64_t* out, int log_n, int inverse) {
   size_t n = (size_t)1 << log_n;
   std::vector<Fr> a(n), b;

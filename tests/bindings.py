@@ -50,6 +50,8 @@ def oracle():
         lib.orc_g1_gen_batch.argtypes = [vp, ctypes.c_size_t, vp, ctypes.c_int]
         lib.orc_g2_gen_batch.argtypes = [vp, ctypes.c_size_t, vp, ctypes.c_int]
         lib.orc_ntt.argtypes = [vp, ctypes.c_int, ctypes.c_int, ctypes.c_int]
+        lib.orc_coset_scale.argtypes = [vp, ctypes.c_int, ctypes.c_uint64, ctypes.c_int]
+        lib.orc_fr_dot_std.argtypes = [vp, vp, ctypes.c_size_t, vp]
         lib.orc_dft_naive.argtypes = [vp, vp, ctypes.c_int, ctypes.c_int]
         lib.orc_fr_from_u64_array.argtypes = [vp, ctypes.c_size_t, vp]
         lib.orc_fr_batch_from_std.argtypes = [vp, ctypes.c_size_t, vp]

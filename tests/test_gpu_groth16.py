@@ -182,28 +182,57 @@ def test_prove_2_16_matches_oracle(ctx, tmp_path):
         assert ref().ref_verify_files(str(vk_path).encode(), str(pf).encode(), str(pub).encode()) == 1
 
 
+def _oracle_of(A, B, C, nc, nv, npub):
+    mats = [(M["row"], M["col"], np.ascontiguousarray(M["value"])) for M in (A, B, C)]
+    return OracleR1CS(nc, nv, npub, nv - 1 - npub, mats)
+
+
+def test_quotient_h_2_22_matches_oracle(ctx):
+    """zk_quotient_h at BASELINE config 5's 2^22 constraints, bit-exact against
+    the oracle's compute_h (groth16.cu:263-390) on the box's host threads."""
+    import zkml_amd
+    nc, npub = 1 << 22, 4
+    A, B, C, w = zkml_amd.synthetic_r1cs(nc, npub, 16, 23)
+    r = ctx.r1cs(nc, w.shape[0], npub, A, B, C)
+    assert r.log_n == 22
+    dw = ctx.upload(w)
+    dh = ctx.alloc(nc * 32)
+    ctx.quotient_h(r, dw, w.shape[0], dh)
+    got = ctx.d2h(dh, (nc, 4))
+    print("[quotient 2^22] oracle compute_h", flush=True)
+    oc = _oracle_of(A, B, C, nc, w.shape[0], npub)
+    assert np.array_equal(got, oc.compute_h(w, threads=16))
+    assert not got[-1].any()  # h has degree < n - 1
+    r.close()
+
+
 def test_prove_2_22_config5_verifies(ctx, tmp_path):
     """BASELINE config 5 at its full 2^22 constraints (3 nonzeros per A and B
-    row, C the fresh product variable).  The oracle's CPU prove is too slow at
-    this size, so the pins are size-independent: the proof is accepted by the
-    product's verifier and by the reference's own (oracle/_ref), a changed
-    public input is rejected, and a second prove with the same seed gives the
-    same bytes."""
+    row, C the fresh product variable): the proof is byte-identical to the
+    oracle's prove with the same key, witness and seed; it is accepted by the
+    product's verifier (and by the reference's own code in oracle/_ref where
+    built), a changed public input is rejected, and a second prove with the
+    same seed gives the same bytes."""
     import zkml_amd
     nc, npub = 1 << 22, 4
     A, B, C, w = zkml_amd.synthetic_r1cs(nc, npub, 16, 22)
     r = ctx.r1cs(nc, w.shape[0], npub, A, B, C)
-    del A, B, C
     assert r.log_n == 22
     pk_path, vk_path = tmp_path / "pk.bin", tmp_path / "vk.bin"
     print("[prove 2^22] setup", flush=True)
     ctx.setup(r, SETUP_SEED, pk_path, vk_path)
     pk = ctx.load_pk(pk_path)
-    os.remove(pk_path)
     print("[prove 2^22] prove", flush=True)
     proof, _ = ctx.prove(pk, r, w, npub, PROVE_SEED)
     again, _ = ctx.prove(pk, r, w, npub, PROVE_SEED)
     assert proof == again
+    print("[prove 2^22] oracle prove", flush=True)
+    oc = _oracle_of(A, B, C, nc, w.shape[0], npub)
+    del A, B, C
+    rc, proof_o, _ = oc.prove(str(pk_path), w, PROVE_SEED, threads=16)
+    del oc
+    os.remove(pk_path)
+    assert rc == 0 and proof == proof_o
     pub = [Z.from_mont(Z.from_limbs([int(x) for x in w[1 + i]]), Z.R) for i in range(npub)]
     pub_words = np.array([Z.limbs(v) for v in pub], dtype=np.uint64)
     vk = vk_path.read_bytes()

@@ -84,6 +84,15 @@ def closed_form_g1(ks, ss):
     return Z.g1.pmul(Z.G1, sum(k * s for k, s in zip(ks, ss)) % Z.R)
 
 
+def closed_form_scalar(kstd, sstd):
+    """sum k_i s_i mod r for (n, 4) standard-form words (oracle Fr arithmetic,
+    itself pinned against Python big integers)."""
+    out = np.zeros(4, dtype=np.uint64)
+    oracle().orc_fr_dot_std(ptr(np.ascontiguousarray(kstd)), ptr(np.ascontiguousarray(sstd)), kstd.shape[0],
+                            ptr(out))
+    return Z.from_limbs(out)
+
+
 # ------------------------------------------------------------------ fixed base
 @pytest.mark.parametrize("n", [1, 5, 1000])
 def test_g1_generator_mul_matches_oracle(ctx, n):
@@ -181,11 +190,12 @@ def test_msm_g1_all_equal_scalars(ctx, log_n):
     assert Z.g1_from_words(got) == Z.g1.pmul(Z.G1, sum(ks) * s % Z.R)
 
 
-@pytest.mark.parametrize("log_n,dist", [(16, "uniform"), (16, "witness"), (18, "uniform"),
-                                        (20, "uniform"), (20, "witness")])
+@pytest.mark.parametrize("log_n,dist", [(16, "uniform"), (16, "witness"), (18, "uniform"), (18, "witness"),
+                                        (20, "uniform"), (20, "witness"), (22, "uniform"), (22, "witness")])
 def test_msm_g1_closed_form_large(ctx, log_n, dist):
-    """P_i = k_i G1 generated on the GPU (spot-checked
-    against the oracle), MSM checked against (sum k_i s_i) G1."""
+    """BASELINE config 3 at every size it names: P_i = k_i G1 generated on
+    the GPU (spot-checked against the oracle), MSM checked against
+    (sum k_i s_i) G1, for uniform and witness-like scalars."""
     n = 1 << log_n
     rng = np.random.default_rng(log_n * 10 + (dist == "witness"))
     kstd = rand_std(n, rng)
@@ -196,9 +206,9 @@ def test_msm_g1_closed_form_large(ctx, log_n, dist):
     assert np.array_equal(spot, oracle_points(np.ascontiguousarray(km[idx])))
     sstd = witness_like(n, rng) if dist == "witness" else rand_std(n, rng)
     ds = ctx.upload(to_mont(sstd))
+    print(f"[msm g1 2^{log_n} {dist}]", flush=True)
     got = ctx.msm_g1(dp, ds, n)
-    ks, ss = from_std_arr(kstd), from_std_arr(sstd)
-    assert Z.g1_from_words(got) == closed_form_g1(ks, ss)
+    assert Z.g1_from_words(got) == Z.g1.pmul(Z.G1, closed_form_scalar(kstd, sstd))
     # repeat on the same context: workspace reuse gives the same bytes
     again = ctx.msm_g1(dp, ds, n)
     assert np.array_equal(again, got)
@@ -277,16 +287,19 @@ def test_msm_g2_vs_oracle(ctx, n):
     assert np.array_equal(got, oracle_msm(pts, sc, g2=True))
 
 
-def test_msm_g2_closed_form_2_14(ctx):
-    n = 1 << 14
-    rng = np.random.default_rng(99)
+@pytest.mark.parametrize("log_n,dist", [(14, "witness"), (16, "uniform"), (16, "witness"), (22, "uniform")])
+def test_msm_g2_closed_form(ctx, log_n, dist):
+    """G2 MSM over Q_i = k_i G2 against (sum k_i s_i) G2: the proof sizes of
+    configs 4 (2^16) and 5 (2^22)."""
+    n = 1 << log_n
+    rng = np.random.default_rng(99 + log_n)
     kstd = rand_std(n, rng)
     dp = gpu_points(ctx, to_mont(kstd), g2=True)
-    sstd = witness_like(n, rng)
+    sstd = witness_like(n, rng) if dist == "witness" else rand_std(n, rng)
     ds = ctx.upload(to_mont(sstd))
+    print(f"[msm g2 2^{log_n} {dist}]", flush=True)
     got = ctx.msm_g2(dp, ds, n)
-    ks, ss = from_std_arr(kstd), from_std_arr(sstd)
-    assert Z.g2_from_words(got) == Z.g2.pmul(Z.G2, sum(k * s for k, s in zip(ks, ss)) % Z.R)
+    assert Z.g2_from_words(got) == Z.g2.pmul(Z.G2, closed_form_scalar(kstd, sstd))
 
 
 # ------------------------------------------------------------------ host-pointer drop-in
@@ -310,3 +323,27 @@ def test_msm_g1_host_reference_layout(ctx):
     expect = oracle_msm(pts, sc)
     assert np.array_equal(out[:8], expect)
     assert Z.from_mont(Z.from_limbs(out[8:12]), Z.P) == 1
+
+
+def test_msm_g2_host_reference_layout(ctx):
+    """zk_msm_g2_host takes the reference's 136-byte G2Affine structs (x, y in
+    Fp2, bool infinity at byte 128) and returns a 192-byte G2Jacobian
+    (msm.cuh:68); a point flagged infinity is skipped whatever its words."""
+    import zkml_amd
+    n = 200
+    rng = np.random.default_rng(6)
+    km = to_mont(rand_std(n, rng))
+    pts = oracle_points(km, g2=True)
+    recs = np.zeros((n, 17), dtype=np.uint64)  # 136 bytes each
+    recs[:, :16] = pts
+    recs[7, 16] = 1  # bool infinity at byte 128; its coordinates stay a valid point
+    sc = to_mont(rand_std(n, rng))
+    out = np.zeros(24, dtype=np.uint64)
+    L = zkml_amd.lib()
+    assert L.zk_msm_g2_host(ctx.h, ptr(recs), ptr(sc), n, ptr(out)) == 0
+    pts_inf = pts.copy()
+    pts_inf[7] = 0
+    expect = oracle_msm(pts_inf, sc, g2=True)
+    assert np.array_equal(out[:16], expect)
+    # z = 1 in Fq2 (Montgomery): c0 = 1, c1 = 0
+    assert Z.from_mont(Z.from_limbs(out[16:20]), Z.P) == 1 and not out[20:24].any()

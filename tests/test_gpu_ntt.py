@@ -24,30 +24,18 @@ def oracle_ntt(a, log_n, inverse, threads=8):
     return b
 
 
-def oracle_coset(a, log_n, g, inverse):
-    """forward: NTT(a_i g^i); inverse: iNTT(a)_i g^-i, on Montgomery words."""
-    n = 1 << log_n
+def oracle_coset(a, log_n, g, inverse, threads=16):
+    """forward: NTT(a_i g^i); inverse: iNTT(a)_i g^-i, on Montgomery words (the
+    oracle's restatement of compute_h's coset loops, groth16.cu:352-383)."""
     lib = oracle()
-    gm = np.array(Z.fr_words(g), dtype=np.uint64)
+    b = np.ascontiguousarray(a.copy())
     if inverse:
-        gm = np.array(Z.fr_words(pow(g, -1, Z.R)), dtype=np.uint64)
-    powers = np.zeros((n, 4), dtype=np.uint64)
-    cur = np.array(Z.fr_words(1), dtype=np.uint64)
-    for i in range(n):
-        powers[i] = cur
-        nxt = np.zeros(4, dtype=np.uint64)
-        lib.orc_fr_mul(ptr(cur), ptr(gm), ptr(nxt))
-        cur = nxt
-    def pointwise(x):
-        o = np.zeros_like(x)
-        for i in range(n):
-            t = np.zeros(4, dtype=np.uint64)
-            lib.orc_fr_mul(ptr(np.ascontiguousarray(x[i])), ptr(np.ascontiguousarray(powers[i])), ptr(t))
-            o[i] = t
-        return o
-    if inverse:
-        return pointwise(oracle_ntt(a, log_n, True))
-    return oracle_ntt(pointwise(a), log_n, False)
+        lib.orc_ntt(ptr(b), log_n, 1, threads)
+        lib.orc_coset_scale(ptr(b), log_n, g, 1)
+    else:
+        lib.orc_coset_scale(ptr(b), log_n, g, 0)
+        lib.orc_ntt(ptr(b), log_n, 0, threads)
+    return b
 
 
 def rand_words(n, seed):
@@ -99,7 +87,7 @@ def test_ntt_2_22_vs_oracle_and_round_trip(ctx):
     assert np.array_equal(back, a)
 
 
-@pytest.mark.parametrize("log_n,g", [(3, 5), (10, 7), (13, 5), (16, 7)])
+@pytest.mark.parametrize("log_n,g", [(3, 5), (10, 7), (13, 5), (16, 7), (20, 7), (22, 7)])
 def test_coset_ntt_vs_oracle(ctx, log_n, g):
     a = rand_words(1 << log_n, 100 + log_n)
     for inverse in (False, True):

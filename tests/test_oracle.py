@@ -330,6 +330,38 @@ def check_quotient(circ, h_words, seed=0):
     assert lhs == Z.poly_eval(h, tau) * zt % Z.R
 
 
+def test_oracle_dot_product_closed_form():
+    """orc_fr_dot_std: sum a_i b_i mod r in standard form (the closed-form
+    MSM scalar), against Python big integers, edge values included."""
+    rng = random.Random(77)
+    vals_a = [0, 1, Z.R - 1, Z.R - 1] + [rng.randrange(Z.R) for _ in range(996)]
+    vals_b = [Z.R - 1, Z.R - 1, Z.R - 1, 1] + [rng.randrange(Z.R) for _ in range(996)]
+    a = np.array([Z.limbs(v) for v in vals_a], dtype=np.uint64)
+    b = np.array([Z.limbs(v) for v in vals_b], dtype=np.uint64)
+    out = np.zeros(4, dtype=np.uint64)
+    oracle().orc_fr_dot_std(ptr(a), ptr(b), len(vals_a), ptr(out))
+    assert Z.from_limbs(out) == sum(x * y for x, y in zip(vals_a, vals_b)) % Z.R
+
+
+@pytest.mark.parametrize("log_n,g", [(3, 5), (8, 7)])
+def test_oracle_coset_scale_evaluates_on_the_coset(log_n, g):
+    """orc_coset_scale then orc_ntt gives the polynomial at g w^j (Horner),
+    and the inverse order (iNTT, then g^-i) undoes it."""
+    n = 1 << log_n
+    rng = random.Random(log_n)
+    coeffs = [rng.randrange(Z.R) for _ in range(n)]
+    a = np.array([Z.fr_words(c) for c in coeffs], dtype=np.uint64)
+    lib = oracle()
+    b = np.ascontiguousarray(a.copy())
+    lib.orc_coset_scale(ptr(b), log_n, g, 0)
+    lib.orc_ntt(ptr(b), log_n, 0, 2)
+    w = Z.omega(log_n)
+    assert [Z.fr_from_words(r) for r in b] == [Z.poly_eval(coeffs, g * pow(w, j, Z.R) % Z.R) for j in range(n)]
+    lib.orc_ntt(ptr(b), log_n, 1, 2)
+    lib.orc_coset_scale(ptr(b), log_n, g, 1)
+    assert np.array_equal(b, a)
+
+
 @pytest.mark.parametrize("rows", [2, 37, 200])
 def test_compute_h_quotient_identity(rows):
     circ = random_r1cs(rows, seed=rows) if rows > 2 else mul_circuit()
