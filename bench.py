@@ -9,6 +9,10 @@ full Groth16 proves, each checked by the product's verifier:
                         built by the reference's own statement builder and
                         committed under tests/golden/statements
   prove_config1         config 1's quantized MLP statement (domain 2^13)
+  prove_config4_named   config 4's network as written (1x8x8 input, four 3x3
+                        filters, MLP 144 -> 32 -> 10, private model and input
+                        under Poseidon, routing): 707 k constraints, domain
+                        2^20, built by the product's statement builder
   prove_2_16_synthetic  a uniform-witness config-5-shaped R1CS, domain 2^16
   prove_2_22_config5    config 5 at its full 2^22 constraints
 the 2^22 NTT of config 2, the G1 MSM at config 3's other sizes and with its
@@ -280,7 +284,7 @@ def main():
         ntt, ntt_in, ntt_out = ntt_case(ctx, ln, rng)
 
     # ---------------- full prove at 2^16
-    prove = prove_syn = prove22 = prove_c1 = None
+    prove = prove_syn = prove22 = prove_c1 = prove_c4n = None
     work = tempfile.TemporaryDirectory()
     kept = {}  # config 4: statement, PK path and GPU proof, for the CPU prove
     if not args.no_prove:
@@ -341,6 +345,11 @@ def main():
 
         prove = prove_case(fixture("config4"), 41, "prove config 4 (2^16)", keep=True)
         prove_c1 = prove_case(fixture("config1"), 41, "prove config 1 (2^13)")
+        import statement_models
+        st4 = statement_models.config4_named()
+        prove_c4n = prove_case((st4.nc, st4.nv, st4.npub, st4.A, st4.B, st4.C, st4.w), 11,
+                               "prove config 4 as named (2^20)")
+        del st4
         prove_syn = prove_case(synthetic((1 << 16) - 64, 16), 21, "prove 2^16 synthetic")
         prove22 = prove_case(synthetic(1 << 22, 22), 5, "prove 2^22 (config 5)")
 
@@ -425,6 +434,7 @@ def main():
         "prove_2_16": prove,
         "prove_2_16_synthetic": prove_syn,
         "prove_config1": prove_c1,
+        "prove_config4_named": prove_c4n,
         "prove_2_22_config5": prove22,
         "ntt_2_22": ntt,
         "cpu_baseline": cpu,

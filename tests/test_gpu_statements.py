@@ -1,5 +1,7 @@
-"""GPU proofs of the BASELINE config 1 and config 4 statements (built by the
-reference's own statement builder, committed as iden3 fixtures):
+"""GPU proofs of the BASELINE config 1 and config 4 statements (config 1 and
+the reference's variant B built by the reference's own statement builder and
+committed as iden3 fixtures; config 4's network as written built by the
+product's builder):
   * GPU setup, then a prove whose 256 bytes equal the oracle's restatement of
     the reference prover for the same key, witness and seed;
   * the proof verifies under the product's verifier and the reference's;
@@ -64,3 +66,38 @@ def test_prove_statement(ctx, tmp_path, name):
         pp.write_bytes(proof)
         up.write_bytes(np.int32(npub).tobytes() + pub.tobytes())
         assert ref().ref_verify_files(vk_path.encode(), str(pp).encode(), str(up).encode()) == 1
+
+
+def test_prove_config4_named(ctx, tmp_path):
+    """BASELINE config 4's network as written (1x8x8 input, four 3x3 filters,
+    MLP 144 -> 32 -> 10, private model and input under Poseidon, routing):
+    707,395 constraints on a 2^20 domain, built by the product's statement
+    builder (its size pinned by the gadget closed forms); GPU proof
+    byte-identical to the oracle's prove with the same key, and verified."""
+    import zkml_amd
+    import statement_models as sm
+    st = sm.config4_named()
+    r = ctx.r1cs(st.nc, st.nv, st.npub, st.A, st.B, st.C)
+    assert r.log_n == 20
+    pk_path, vk_path = str(tmp_path / "pk.bin"), str(tmp_path / "vk.bin")
+    print("[config4 named] setup", flush=True)
+    ctx.setup(r, 0xDEADBEEF42, pk_path, vk_path)
+    pk = ctx.load_pk(pk_path)
+    ctx.prove(pk, r, st.w, st.npub, 0xCAFEBABE)
+    t0 = time.perf_counter()
+    proof, parts = ctx.prove(pk, r, st.w, st.npub, 0xCAFEBABE)
+    print(f"[config4 named] {st.nc} constraints: prove {(time.perf_counter() - t0) * 1e3:.2f} ms {parts}",
+          flush=True)
+    mats = [(M["row"], M["col"], M["value"].reshape(-1, 4)) for M in (st.A, st.B, st.C)]
+    oc = OracleR1CS(st.nc, st.nv, st.npub, st.npriv, mats)
+    print("[config4 named] oracle prove", flush=True)
+    rc, proof_o, _ = oc.prove(pk_path, st.w, 0xCAFEBABE, threads=16)
+    assert rc == 0 and proof == proof_o
+    pub = publics_std(st.w, st.npub)
+    vk = open(vk_path, "rb").read()
+    assert zkml_amd.verify(vk, proof, pub)
+    bad = pub.copy()
+    bad[0, 0] ^= 1
+    assert not zkml_amd.verify(vk, proof, bad)
+    pk.close()
+    r.close()

@@ -201,6 +201,29 @@ def test_poseidon_permutation_cost():
     assert r312 - 1 + 2 * (r37 - 1) == 194 * 270
 
 
+def test_config4_named_size_and_witness():
+    """BASELINE config 4's network as written (tests/statement_models.py):
+    its size equals the gadget closed forms -- the Poseidon commitment of its
+    5,010 private weights and biases dominates -- and the witness satisfies
+    every row; the scores equal a plain integer evaluation."""
+    layers, xs = sm.cnn_private()
+    st = sm.config4_named()
+    want = statement_size(layers, 1, 64, private_input=True, private_model=True, private_outputs=True, route=True)
+    assert (st.nc, st.nv, st.npub) == want
+    assert st.npub == 1 + 1 + 1 + 2
+    assert 2**19 < st.nc <= 2**20  # domain 2^20
+    assert st.check()
+    x = np.asarray(xs[0], dtype=np.int64).reshape(1, 8, 8)
+    W = layers[0]["weights"].reshape(4, 1, 3, 3)
+    conv = np.array([[[layers[0]["bias"][o] + np.sum(W[o] * x[:, i:i + 3, j:j + 3]) for j in range(6)]
+                      for i in range(6)] for o in range(4)], dtype=np.int64).reshape(-1)
+    h = np.maximum(conv, 0) >> 8
+    h = layers[2]["weights"].reshape(32, 144) @ h + layers[2]["bias"]
+    h = np.maximum(h, 0) >> 8
+    scores = layers[4]["weights"].reshape(10, 32) @ h + layers[4]["bias"]
+    assert list(st.scores[0]) == list(scores)
+
+
 # ------------------------------------------------------------------ gadget sweep
 def _random_model(rng):
     layers, n_in = [], None
