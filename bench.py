@@ -274,6 +274,14 @@ def main():
         ctx.g2_generator_mul(d_k2, n16, dp2)
         msm_more["g2_2_16"] = msm_entry(time_msm(ctx.msm_g2, dp2, ds, n16, 20), n16, g2=True)
         del d_k2, dp2
+        # G2 at config 5's size (the B query of the 2^22 proof)
+        k22 = zkml_amd.random_fr(n22, rng)
+        d_k22 = ctx.upload(k22)
+        dp22 = ctx.alloc(n22 * 128)
+        ctx.g2_generator_mul(d_k22, n22, dp22)
+        ds22 = ctx.upload(zkml_amd.random_fr(n22, rng))
+        msm_more["g2_2_22"] = msm_entry(time_msm(ctx.msm_g2, dp22, ds22, n22, 5), n22, g2=True)
+        del d_k22, dp22, ds22, k22
     for key, v in msm_more.items():
         log(f"[bench] MSM {key}: {v['ms']:.3f} ms, {v['Mpoints_per_s']} Mpoints/s")
 

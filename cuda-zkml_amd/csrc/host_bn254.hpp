@@ -10,6 +10,7 @@
 #pragma once
 #include <stdint.h>
 #include <string.h>
+#include <x86intrin.h>
 
 namespace zkh {
 
@@ -48,14 +49,19 @@ struct F {
   bool is_zero() const { return (v[0] | v[1] | v[2] | v[3]) == 0; }
   bool operator==(const F& o) const { return memcmp(v, o.v, 32) == 0; }
 
-  static inline uint64_t sub4(uint64_t* r, const uint64_t* a, const uint64_t* b) {
-    uint64_t br = 0;
-    for (int i = 0; i < 4; i++) {
-      u128 d = (u128)a[i] - b[i] - br;
-      r[i] = (uint64_t)d;
-      br = (uint64_t)(d >> 127);
-    }
-    return br;
+  // r = t - m when t >= m, else t: a carry chain and a mask select (the
+  // outcome is data dependent, so a branch would mispredict half the time).
+  static inline void csub(uint64_t* r, uint64_t t0, uint64_t t1, uint64_t t2, uint64_t t3) {
+    unsigned long long s0, s1, s2, s3;
+    unsigned char b = _subborrow_u64(0, t0, M::M[0], &s0);
+    b = _subborrow_u64(b, t1, M::M[1], &s1);
+    b = _subborrow_u64(b, t2, M::M[2], &s2);
+    b = _subborrow_u64(b, t3, M::M[3], &s3);
+    const uint64_t keep = 0 - (uint64_t)b;  // all ones when t < m
+    r[0] = (t0 & keep) | (s0 & ~keep);
+    r[1] = (t1 & keep) | (s1 & ~keep);
+    r[2] = (t2 & keep) | (s2 & ~keep);
+    r[3] = (t3 & keep) | (s3 & ~keep);
   }
   // Montgomery product a b 2^-256 mod m, CIOS without the extra carry word:
   // both moduli have a top limb below 2^62, so the running value stays
@@ -89,9 +95,7 @@ struct F {
       t2 = (uint64_t)y;
       t3 = C + A;
     }
-    uint64_t t[4] = {t0, t1, t2, t3}, s[4];
-    if (!sub4(s, t, M::M)) memcpy(r, s, 32);
-    else memcpy(r, t, 32);
+    csub(r, t0, t1, t2, t3);
   }
   F operator*(const F& o) const {
     F r;
@@ -99,28 +103,29 @@ struct F {
     return r;
   }
   F sqr() const { return *this * *this; }
+  // sums stay below 2^256 since 2m < 2^255
   F operator+(const F& o) const {
-    F r, t;
-    u128 c = 0;
-    for (int i = 0; i < 4; i++) {
-      c += (u128)v[i] + o.v[i];
-      r.v[i] = (uint64_t)c;
-      c >>= 64;
-    }
-    if (!sub4(t.v, r.v, M::M)) return t;  // sums stay below 2^256 since 2m < 2^255
+    unsigned long long s0, s1, s2, s3;
+    unsigned char c = _addcarry_u64(0, v[0], o.v[0], &s0);
+    c = _addcarry_u64(c, v[1], o.v[1], &s1);
+    c = _addcarry_u64(c, v[2], o.v[2], &s2);
+    (void)_addcarry_u64(c, v[3], o.v[3], &s3);
+    F r;
+    csub(r.v, s0, s1, s2, s3);
     return r;
   }
   F operator-(const F& o) const {
-    F r;
-    if (sub4(r.v, v, o.v)) {
-      u128 c = 0;
-      for (int i = 0; i < 4; i++) {
-        c += (u128)r.v[i] + M::M[i];
-        r.v[i] = (uint64_t)c;
-        c >>= 64;
-      }
-    }
-    return r;
+    unsigned long long d0, d1, d2, d3, r0, r1, r2, r3;
+    unsigned char b = _subborrow_u64(0, v[0], o.v[0], &d0);
+    b = _subborrow_u64(b, v[1], o.v[1], &d1);
+    b = _subborrow_u64(b, v[2], o.v[2], &d2);
+    b = _subborrow_u64(b, v[3], o.v[3], &d3);
+    const uint64_t mask = 0 - (uint64_t)b;  // add m back after a borrow
+    unsigned char c = _addcarry_u64(0, d0, M::M[0] & mask, &r0);
+    c = _addcarry_u64(c, d1, M::M[1] & mask, &r1);
+    c = _addcarry_u64(c, d2, M::M[2] & mask, &r2);
+    (void)_addcarry_u64(c, d3, M::M[3] & mask, &r3);
+    return F{{r0, r1, r2, r3}};
   }
   F operator-() const { return zero() - *this; }
   F dbl() const { return *this + *this; }

@@ -20,9 +20,10 @@
 //                with mixed XYZZ additions (perfect load balance whatever the
 //                bucket sizes); runs that cross a chunk edge leave a head /
 //                tail partial.
-//  5. combine    log-depth tree over the chunk partials of each bucket that
-//                spans chunks (one level for ordinary buckets, ~log2(size/L0)
-//                levels for hot buckets such as many scalars equal to 1).
+//  5. combine    the chunk partials of each bucket that spans chunks are
+//                folded in groups (one launch for ordinary buckets,
+//                ~log8(size/L0) for hot buckets such as many scalars equal
+//                to 1).
 //  6. reduce     sum_b b*S_b per window: G-bucket segments with running sums
 //                plus (segment offset)*run, then LDS scans and trees per
 //                group of T segments and per window.
@@ -54,6 +55,21 @@ constexpr int MSM_NCB = 256;       // coarse bins per window of the two-pass pla
 constexpr int MSM_BPC_MAX = 128;   // buckets per coarse bin at B = 2^15
 constexpr int PLACE_T = 1024;      // threads of a placement block
 constexpr uint32_t MSM_SERIAL_SPAN = 8;  // longest serial chunk-partial chain of the one-launch combine
+// Partials folded per bucket group by each level of a deeper combine.  A
+// level costs a launch plus S - 1 dependent additions; measured on MI355X
+// (G2 2^16 and G1 witness-like 2^20 MSMs, the 2^16 proof) S = 2 beats 4 and 8.
+#ifndef ZK_MSM_COMBINE_S
+#define ZK_MSM_COMBINE_S 2
+#endif
+constexpr uint32_t MSM_COMBINE_S = ZK_MSM_COMBINE_S;
+// G2 accumulation tuning: chunk length divided by 2^ZK_MSM_G2_L0_SHIFT (down
+// to MSM_L0 / 8), waves per SIMD the register budget is cut to.
+#ifndef ZK_MSM_G2_L0_SHIFT
+#define ZK_MSM_G2_L0_SHIFT 0
+#endif
+#ifndef ZK_MSM_G2_ACC_WAVES
+#define ZK_MSM_G2_ACC_WAVES 3
+#endif
 // Bits covered by the windows.  After the optional negation s <= (r-1)/2 <
 // 2^253, and signed digits need one more bit for the final carry.
 constexpr int MSM_BITS = 254;
@@ -538,18 +554,41 @@ struct BaseSets {
   uint32_t lo[MSM_SETS], hi[MSM_SETS];
 };
 
+// Record load into the accumulation's registers: G1 the whole record, G2
+// this lane's half of a lane pair (x.c0, y.c0 on even lanes, x.c1, y.c1 on
+// odd lanes).  Returns true for the point at infinity (all words zero).
+__device__ __forceinline__ bool load_rec_lanes(const uint4* __restrict__ recs, uint32_t idx, fq& x, fq& y) {
+  return load_rec(recs, idx, x, y);
+}
+__device__ __forceinline__ bool load_rec_lanes(const uint4* __restrict__ recs, uint32_t idx, fq2h& x, fq2h& y) {
+  const uint4* p = recs + (size_t)idx * (Rec<fq2>::WORDS / 4) + (lane_odd() ? 2 : 0);
+  const uint4 a = p[0], b = p[1], c = p[4], d = p[5];
+  const uint32_t wx[8] = {a.x, a.y, a.z, a.w, b.x, b.y, b.z, b.w};
+  const uint32_t wy[8] = {c.x, c.y, c.z, c.w, d.x, d.y, d.z, d.w};
+  uint32_t any = 0;
+#pragma unroll
+  for (int k = 0; k < 8; k++) any |= wx[k] | wy[k];
+  any |= swap_pair(any);
+  x.c = repack_in<FqP>(wx);
+  y.c = repack_in<FqP>(wy);
+  return any == 0;
+}
+
 // Chunk ch covers sorted positions [ch*L0, ch*L0 + L0) of window
 // ch / chunks_per_window; positions past the window's entry count are empty.
-// blockIdx.y selects the base set; its buckets start at set * nbuckets.
+// blockIdx.y selects the base set; its buckets start at set * nbuckets.  A
+// chunk is one lane (G1) or one lane pair (G2, Lanes<F>): split over a pair
+// the G2 accumulator needs half the registers per lane, so that more waves
+// fit on a SIMD to cover the gathers' latency.
 //
-// Waves are scattered over the chunk space: wave v of the grid takes the 64
-// chunks of chunk-wave (v * wave_mul) mod nwaves (wave_mul coprime to
-// nwaves, so every chunk is taken once).  With skewed scalars most entries
+// Waves are scattered over the chunk space: wave v of the grid takes the
+// 64 / Lanes<F>::N chunks of chunk-wave (v * wave_mul) mod nwaves (wave_mul
+// coprime to nwaves, so every chunk is taken once).  With skewed scalars most entries
 // sit in a few windows (small witness values fill the low ones); in chunk
 // order those windows' waves would land on a fraction of the CUs, scattered
 // they spread over all of them.
 template <class F>
-__global__ __launch_bounds__(256) void k_msm_accumulate(const uint2* __restrict__ sorted, BaseSets sets,
+__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(sizeof(F) == sizeof(fq) ? 4 : ZK_MSM_G2_ACC_WAVES))) void k_msm_accumulate(const uint2* __restrict__ sorted, BaseSets sets,
                                                         const uint32_t* __restrict__ start,
                                                         const uint32_t* __restrict__ end,
                                                         const uint32_t* __restrict__ wstat, uint32_t nchunks,
@@ -557,10 +596,13 @@ __global__ __launch_bounds__(256) void k_msm_accumulate(const uint2* __restrict_
                                                         size_t nbuckets, xyzz<F>* __restrict__ buckets,
                                                         ChunkSlots<F> all_slots, uint32_t nwaves,
                                                         uint32_t wave_mul) {
+  typedef Lanes<F> LN;
+  typedef typename LN::R R;
+  constexpr uint32_t PER_WAVE = 64 / LN::N;  // chunks per wave
   msm_accumulate_priority<F>();
   const uint32_t tid = blockIdx.x * blockDim.x + threadIdx.x;
   if ((tid >> 6) >= nwaves) return;
-  const uint32_t ch = (uint32_t)((uint64_t)(tid >> 6) * wave_mul % nwaves) * 64 + (tid & 63);
+  const uint32_t ch = (uint32_t)((uint64_t)(tid >> 6) * wave_mul % nwaves) * PER_WAVE + (tid & 63) / LN::N;
   if (ch >= nchunks) return;
   const uint32_t set = blockIdx.y;
   const uint4* __restrict__ recs = sets.recs[set];
@@ -573,7 +615,7 @@ __global__ __launch_bounds__(256) void k_msm_accumulate(const uint2* __restrict_
   uint32_t hk = KEY_INVALID, tk = KEY_INVALID;
   if (lo < total) {
     const uint32_t hi = min(lo + L0, total);
-    xyzz<F> acc;
+    xyzz<R> acc;
     xyzz_set_inf(acc);
     bool empty = true;  // acc is the point at infinity
     uint32_t cur = sorted[lo].x;
@@ -584,9 +626,9 @@ __global__ __launch_bounds__(256) void k_msm_accumulate(const uint2* __restrict_
         // run `cur` ended inside the chunk
         if (start[cur] < lo) {
           hk = cur;
-          slots.hpt[ch] = acc;
+          LN::store(slots.hpt[ch], acc);
         } else {
-          buckets[cur] = acc;
+          LN::store(buckets[cur], acc);
         }
         cur = key;
         xyzz_set_inf(acc);
@@ -594,8 +636,8 @@ __global__ __launch_bounds__(256) void k_msm_accumulate(const uint2* __restrict_
       }
       const uint32_t v = e.y;
       const uint32_t i = (v & 0x7fffffffu) - ilo;  // wraps below lo
-      F x, y;
-      if (i < ilen && !load_rec(recs, i, x, y)) {
+      R x, y;
+      if (i < ilen && !load_rec_lanes(recs, i, x, y)) {
         if (v >> 31) y = fneg(y);
         if (empty) {
           xyzz_set_affine(acc, x, y);
@@ -608,13 +650,13 @@ __global__ __launch_bounds__(256) void k_msm_accumulate(const uint2* __restrict_
     // last run of the chunk
     const uint32_t rs = start[cur], re = end[cur];
     if (rs >= lo && re <= lo + L0) {
-      buckets[cur] = acc;
+      LN::store(buckets[cur], acc);
     } else if (rs < lo) {
       hk = cur;
-      slots.hpt[ch] = acc;
+      LN::store(slots.hpt[ch], acc);
     } else {
       tk = cur;
-      slots.tpt[ch] = acc;
+      LN::store(slots.tpt[ch], acc);
     }
   }
   slots.hkey[ch] = hk;
@@ -631,42 +673,12 @@ __device__ __forceinline__ uint32_t lane_item() {
   return (blockIdx.x * blockDim.x + threadIdx.x) / Lanes<F>::N;
 }
 
-// One level of the tree over the chunk partials of buckets spanning chunks.
-template <class F>
-__global__ __launch_bounds__(256) void k_msm_combine(ChunkSlots<F> all_slots, const uint32_t* __restrict__ start,
-                                                     const uint32_t* __restrict__ end, uint32_t nchunks,
-                                                     uint32_t L0, uint32_t step) {
-  typedef Lanes<F> LN;
-  msm_priority<F>();
-  const uint32_t ch = lane_item<F>();
-  if (ch >= nchunks) return;
-  const ChunkSlots<F> slots = all_slots.at(blockIdx.y, nchunks);
-  const uint32_t tk = slots.tkey[ch];
-  if (tk != KEY_INVALID) {
-    const uint32_t c1 = (end[tk] - 1) / L0;
-    if (ch + step <= c1) {
-      auto v = LN::load(slots.tpt[ch]);
-      xyzz_add(v, LN::load(slots.hpt[ch + step]));
-      LN::store(slots.tpt[ch], v);
-    }
-  }
-  const uint32_t hk = slots.hkey[ch];
-  if (hk != KEY_INVALID) {
-    const uint32_t c0 = start[hk] / L0, c1 = (end[hk] - 1) / L0;
-    const uint32_t j = ch - c0;
-    if ((j % (2 * step)) == 0 && ch + step <= c1) {
-      auto v = LN::load(slots.hpt[ch]);
-      xyzz_add(v, LN::load(slots.hpt[ch + step]));
-      LN::store(slots.hpt[ch], v);
-    }
-  }
-}
-
-// All levels at once when no bucket spans more than MSM_SERIAL_SPAN + 1
-// chunks: the chunk where a spanning run starts adds the head partials of the
-// following chunks it covers, in order (one launch instead of ceil(log2(span))
-// tree levels plus the final store; each level costs a launch and an EC-add
-// latency).
+// Chunk combine.  The partials of a bucket whose run spans chunks c0 .. c1
+// are the tail partial of c0 and the head partials of c0+1 .. c1.
+//
+// When no bucket spans more than MSM_SERIAL_SPAN + 1 chunks, one launch:
+// the chunk where a spanning run starts adds the head partials of the
+// following chunks it covers, in order, and stores the bucket.
 template <class F>
 __global__ __launch_bounds__(256) void k_msm_combine_serial(ChunkSlots<F> all_slots,
                                                             const uint32_t* __restrict__ end, uint32_t nchunks,
@@ -686,16 +698,38 @@ __global__ __launch_bounds__(256) void k_msm_combine_serial(ChunkSlots<F> all_sl
   LN::store(buckets[tk], acc);
 }
 
+// Longer spans (hot buckets, such as many scalars equal to 1): levels with
+// step = 1, S, S^2, ... (S = MSM_COMBINE_S) fold the partials in groups of
+// S: the chunk at j = ch - c0 with j % (S*step) == 0 adds the partials at
+// j + step, ..., j + (S-1) step that exist.  After the level with S*step >=
+// c1 - c0 + 1 chunk c0 holds the bucket's sum and stores it.  A chunk has at
+// most one active job: a head job needs its bucket to continue past the
+// chunk, and then the chunk's last run is that bucket (no tail).
 template <class F>
-__global__ __launch_bounds__(256) void k_msm_finalize(ChunkSlots<F> all_slots, uint32_t nchunks, size_t nbuckets,
-                                                      xyzz<F>* __restrict__ buckets) {
+__global__ __launch_bounds__(256) void k_msm_combine(ChunkSlots<F> all_slots, const uint32_t* __restrict__ start,
+                                                     const uint32_t* __restrict__ end, uint32_t nchunks,
+                                                     uint32_t L0, uint32_t step, size_t nbuckets,
+                                                     xyzz<F>* __restrict__ buckets) {
+  constexpr uint32_t S = MSM_COMBINE_S;
+  typedef Lanes<F> LN;
   msm_priority<F>();
-  const uint32_t ch = blockIdx.x * blockDim.x + threadIdx.x;  // a plain copy: one lane per point
+  const uint32_t ch = lane_item<F>();
   if (ch >= nchunks) return;
   const ChunkSlots<F> slots = all_slots.at(blockIdx.y, nchunks);
   buckets += blockIdx.y * nbuckets;
-  const uint32_t tk = slots.tkey[ch];
-  if (tk != KEY_INVALID) buckets[tk] = slots.tpt[ch];
+  uint32_t key = slots.tkey[ch];
+  const bool tail = key != KEY_INVALID;
+  if (!tail) {
+    key = slots.hkey[ch];
+    if (key == KEY_INVALID) return;
+  }
+  const uint32_t c0 = start[key] / L0, c1 = (end[key] - 1) / L0;
+  if ((ch - c0) % (S * step) != 0 || ch + step > c1) return;  // nothing to fold here
+  xyzz<F>* self = tail ? &slots.tpt[ch] : &slots.hpt[ch];
+  auto acc = LN::load(*self);
+  for (uint32_t m = 1; m < S && ch + m * step <= c1; m++) xyzz_add(acc, LN::load(slots.hpt[ch + m * step]));
+  if (tail && c1 - c0 + 1 <= S * step) self = &buckets[key];
+  LN::store(*self, acc);
 }
 
 // ------------------------------------------------------------------ bucket reduction
@@ -1074,8 +1108,9 @@ static int msm_run_sets(zk_context* ctx, MsmWorkspace& ws, const BaseSets& sets,
                             : entries >= ((size_t)1 << 20) ? MSM_L0 / 2
                             : entries >= ((size_t)1 << 18) ? MSM_L0 / 4
                                                            : MSM_L0 / 8;
-  const uint32_t L0 =
-      beside && !G2 && L0_alone < (uint32_t)MSM_L0 ? std::max<uint32_t>(L0_alone / 2, MSM_L0 / 8) : L0_alone;
+  const uint32_t L0 = G2 ? std::max<uint32_t>(L0_alone >> ZK_MSM_G2_L0_SHIFT, MSM_L0 / 8)
+                     : beside && L0_alone < (uint32_t)MSM_L0 ? std::max<uint32_t>(L0_alone / 2, MSM_L0 / 8)
+                                                              : L0_alone;
   const uint32_t cpw = n_pad / L0;  // chunks per window
   const uint32_t nchunks = cpw * (uint32_t)W;
   ZK_TRY(ctx->ensure(ws.hkey, (size_t)nsets * nchunks * 4));
@@ -1084,22 +1119,21 @@ static int msm_run_sets(zk_context* ctx, MsmWorkspace& ws, const BaseSets& sets,
   ZK_TRY(ctx->ensure(ws.tpt, (size_t)nsets * nchunks * sizeof(xyzz<F>)));
 
   ChunkSlots<F> slots{(uint32_t*)ws.hkey.p, (uint32_t*)ws.tkey.p, (xyzz<F>*)ws.hpt.p, (xyzz<F>*)ws.tpt.p};
-  const uint32_t gx = cdiv(nchunks, 256);
   const uint32_t gxl = cdiv((size_t)nchunks * Lanes<F>::N, 256);  // combine: Lanes<F>::N lanes per chunk
-  const uint32_t nwaves = cdiv(nchunks, 64);
-  ZK_LAUNCH(ctx, st, "msm_accumulate", k_msm_accumulate<F>, dim3(gx, nsets), dim3(256), 0, sorted, sets, start, end,
+  const uint32_t nwaves = cdiv((size_t)nchunks * Lanes<F>::N, 64);
+  ZK_LAUNCH(ctx, st, "msm_accumulate", k_msm_accumulate<F>, dim3(gxl, nsets), dim3(256), 0, sorted, sets, start, end,
             wstat, nchunks, cpw, n_pad, L0, nbuckets, buckets, slots, nwaves, wave_scatter(nwaves));
-  // the largest bucket decides the depth of the chunk-combine tree
+  // The largest bucket decides the combine: one serial launch for spans up to
+  // MSM_SERIAL_SPAN + 1 chunks, else levels folding MSM_COMBINE_S partials.
   const uint32_t max_span = (maxrun + L0 - 2) / L0 + 1;  // chunks spanned by the largest bucket
   if (max_span <= MSM_SERIAL_SPAN + 1) {
-    ZK_LAUNCH(ctx, st, "msm_combine", k_msm_combine_serial<F>, dim3(gxl, nsets), dim3(256), 0, slots, end, nchunks,
-              L0, nbuckets, buckets);
+    if (max_span > 1)
+      ZK_LAUNCH(ctx, st, "msm_combine", k_msm_combine_serial<F>, dim3(gxl, nsets), dim3(256), 0, slots, end,
+                nchunks, L0, nbuckets, buckets);
   } else {
-    for (uint32_t step = 1; step < max_span; step <<= 1)
+    for (uint64_t step = 1; step < max_span; step *= MSM_COMBINE_S)
       ZK_LAUNCH(ctx, st, "msm_combine", k_msm_combine<F>, dim3(gxl, nsets), dim3(256), 0, slots, start, end, nchunks,
-                L0, step);
-    ZK_LAUNCH(ctx, st, "msm_combine", k_msm_finalize<F>, dim3(gx, nsets), dim3(256), 0, slots, nchunks, nbuckets,
-              buckets);
+                L0, (uint32_t)step, nbuckets, buckets);
   }
 
   // bucket reduction: level 1 (T threads x G buckets per group), level 2 per window
