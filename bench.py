@@ -134,6 +134,8 @@ def main():
     ap.add_argument("--no-prove", action="store_true")
     ap.add_argument("--msm-only", action="store_true",
                     help="only the 2^20 G1 MSM steps (the run the rocprofv3 counter summaries profile)")
+    ap.add_argument("--ntt-only", action="store_true",
+                    help="only the forward NTT of 2^22 elements (config 2; the run the NTT counter summaries profile)")
     ap.add_argument("--copy-calibration", type=int, default=0, metavar="MIB",
                     help="only run a plain device copy of MIB MiB (torch's copy kernel), the reference for "
                          "scaling rocprofv3 FETCH_SIZE / WRITE_SIZE readings to bytes")
@@ -170,6 +172,10 @@ def main():
     import zkml_amd
     ctx = zkml_amd.Context(0)
     rng = np.random.default_rng(20260601)
+    if args.ntt_only:
+        ntt, _, _ = ntt_case(ctx, 22, rng)
+        print(json.dumps({"ntt_2_22": ntt}), flush=True)
+        return
     n = 1 << args.log_n
 
     # ---------------- MSM 2^20 (the step)
