@@ -121,3 +121,170 @@ struct Lanes<fq2> {
 };
 
 }  // namespace zk
+
+namespace zk {
+
+// ------------------------------------------------------------------ split point operations
+// One point operation of a latency-bound chain dealt to two lane groups
+// ("roles"): G1 to a lane pair (E = fq, role = lane bit 0), G2 to two lane
+// pairs (E = fq2h, role = lane bit 1, each pair holding the two Fq2 halves).
+// Both roles hold the whole point.  The formulas' independent products are
+// split between the roles, each role computing one of them with operands it
+// selects by its role, and the results are exchanged through DPP lane swaps:
+// an addition's chain of 12 multiplications, 2 squarings and one two-product
+// sum becomes about 7.5 multiplications deep.  The roles branch together
+// (every branch tests values both hold).  Worth it where a chain runs alone
+// on its SIMD; beside other waves the extra selects and swaps cost issue
+// slots.
+template <class E>
+struct split {
+  E v;
+};
+
+template <class E>
+struct SplitRole;
+template <>
+struct SplitRole<fq> {
+  static constexpr uint32_t BIT = 1;
+  static constexpr int DPP = 0xB1;  // quad_perm [1, 0, 3, 2]: the other lane of the pair
+};
+template <>
+struct SplitRole<fq2h> {
+  static constexpr uint32_t BIT = 2;
+  static constexpr int DPP = 0x4E;  // quad_perm [2, 3, 0, 1]: the same half in the other pair
+};
+
+template <class E>
+__device__ __forceinline__ bool split_role1() {
+  return (threadIdx.x & SplitRole<E>::BIT) != 0;
+}
+
+template <int CTRL>
+__device__ __forceinline__ fq dpp_fq(const fq& a) {
+  fq r;
+#pragma unroll
+  for (int i = 0; i < NL; i++) r.l[i] = (uint32_t)__builtin_amdgcn_mov_dpp((int)a.l[i], CTRL, 0xF, 0xF, false);
+  return r;
+}
+__device__ __forceinline__ fq other_role(const fq& a) { return dpp_fq<SplitRole<fq>::DPP>(a); }
+__device__ __forceinline__ fq2h other_role(const fq2h& a) { return fq2h{dpp_fq<SplitRole<fq2h>::DPP>(a.c)}; }
+__device__ __forceinline__ fq pick(bool c, const fq& a, const fq& b) { return fsel(c, a, b); }
+__device__ __forceinline__ fq2h pick(bool c, const fq2h& a, const fq2h& b) { return fq2h{fsel(c, a.c, b.c)}; }
+
+template <class E>
+__device__ __forceinline__ void fset_zero(split<E>& a) {
+  fset_zero(a.v);
+}
+template <class E>
+__device__ __forceinline__ void fset_one(split<E>& a) {
+  fset_one(a.v);
+}
+template <class E>
+__device__ __forceinline__ bool fis_zero(const split<E>& a) {
+  return fis_zero(a.v);
+}
+template <class E>
+__device__ __forceinline__ split<E> fneg(const split<E>& a) {
+  return split<E>{fneg(a.v)};
+}
+
+// p = 2p (dbl-2008-s-1): V = U^2 | X^2, then W = U V | S = X V, then M^2 |
+// V ZZ, then W ZZZ | Y3 = M (S - X3) - W Y.
+template <class E>
+__device__ __forceinline__ void xyzz_dbl(xyzz<split<E>>& p) {
+  if (fis_zero(p.zz.v)) return;
+  const bool r1 = split_role1<E>();
+  const E U = fdbl(p.y.v);
+  const E a = fsqr(pick(r1, p.x.v, U));  // V | X^2
+  const E ao = other_role(a);
+  const E V = pick(r1, ao, a), X2 = pick(r1, a, ao);
+  const E b = fmul(pick(r1, p.x.v, U), V);  // W | S
+  const E bo = other_role(b);
+  const E W = pick(r1, bo, b), S = pick(r1, b, bo);
+  const E M = fadd(fdbl(X2), X2);
+  const E c = fmul(pick(r1, V, M), pick(r1, p.zz.v, M));  // M^2 | ZZ3 = V ZZ
+  const E co = other_role(c);
+  const E MM = pick(r1, co, c), ZZ3 = pick(r1, c, co);
+  E zero;
+  fset_zero(zero);
+  const E X3 = fsub3(MM, zero, S);
+  // W ZZZ - 0 | M (S - X3) - W Y
+  const E d = fmul_sub(pick(r1, M, W), pick(r1, fsub_m(S, X3), p.zzz.v), pick(r1, W, zero), pick(r1, p.y.v, zero));
+  const E dd = other_role(d);
+  p.x.v = X3;
+  p.y.v = pick(r1, d, dd);
+  p.zz.v = ZZ3;
+  p.zzz.v = pick(r1, dd, d);
+}
+
+// p += q (add-2008-s): U1 | U2, S1 | S2, ZZ1 ZZ2 | ZZZ1 ZZZ2; then PP | RR;
+// then PPP | Q and ZZ3 on both; then ZZZ3 | Y3.
+template <class E>
+__device__ __forceinline__ void xyzz_add(xyzz<split<E>>& p, const xyzz<split<E>>& q) {
+  if (fis_zero(q.zz.v)) return;
+  if (fis_zero(p.zz.v)) {
+    p = q;
+    return;
+  }
+  const bool r1 = split_role1<E>();
+  const E a = fmul(pick(r1, q.x.v, p.x.v), pick(r1, p.zz.v, q.zz.v));     // U1 = X1 ZZ2 | U2 = X2 ZZ1
+  const E b = fmul(pick(r1, q.y.v, p.y.v), pick(r1, p.zzz.v, q.zzz.v));   // S1 = Y1 ZZZ2 | S2 = Y2 ZZZ1
+  const E c = fmul(pick(r1, p.zzz.v, p.zz.v), pick(r1, q.zzz.v, q.zz.v)); // ZZ1 ZZ2 | ZZZ1 ZZZ2
+  const E ao = other_role(a), bo = other_role(b), co = other_role(c);
+  const E U1 = pick(r1, ao, a), U2 = pick(r1, a, ao);
+  const E S1 = pick(r1, bo, b), S2 = pick(r1, b, bo);
+  const E ZZ12 = pick(r1, co, c), ZZZ12 = pick(r1, c, co);
+  const E P = fsub(U2, U1);
+  const E R = fsub_m(S2, S1);  // lazy, (0, 4m)
+  if (fis_zero(P)) {
+    if (fis_zero4(R)) xyzz_dbl(p);
+    else xyzz_set_inf(p);
+    return;
+  }
+  const E t = fsqr(pick(r1, R, P));  // PP | RR
+  const E to = other_role(t);
+  const E PP = pick(r1, to, t), RR = pick(r1, t, to);
+  const E v = fmul(pick(r1, U1, P), PP);  // PPP | Q
+  const E ZZ3 = fmul(ZZ12, PP);
+  const E vo = other_role(v);
+  const E PPP = pick(r1, vo, v), Q = pick(r1, v, vo);
+  const E X3 = fsub3(RR, PPP, Q);
+  E zero;
+  fset_zero(zero);
+  // ZZZ12 PPP - 0 | R (Q - X3) - S1 PPP
+  const E d = fmul_sub(pick(r1, R, ZZZ12), pick(r1, fsub_m(Q, X3), PPP), pick(r1, S1, zero), pick(r1, PPP, zero));
+  const E dd = other_role(d);
+  p.x.v = X3;
+  p.y.v = pick(r1, d, dd);
+  p.zz.v = ZZ3;
+  p.zzz.v = pick(r1, dd, d);
+}
+
+// Register forms of the latency-bound kernels with the operations split
+// over two roles: a G1 point on a lane pair, a G2 point on four lanes.  Only
+// role 0 stores (both hold the same point).
+template <class F>
+struct SplitLanes;
+template <>
+struct SplitLanes<fq> {
+  typedef split<fq> R;
+  static constexpr int N = 2;
+  __device__ static xyzz<R> load(const xyzz<fq>& p) { return xyzz<R>{R{p.x}, R{p.y}, R{p.zz}, R{p.zzz}}; }
+  __device__ static void store(xyzz<fq>& p, const xyzz<R>& v) {
+    if (!split_role1<fq>()) p = xyzz<fq>{v.x.v, v.y.v, v.zz.v, v.zzz.v};
+  }
+};
+template <>
+struct SplitLanes<fq2> {
+  typedef split<fq2h> R;
+  static constexpr int N = 4;
+  __device__ static xyzz<R> load(const xyzz<fq2>& p) {
+    const xyzz<fq2h> h = load_half(p);
+    return xyzz<R>{R{h.x}, R{h.y}, R{h.zz}, R{h.zzz}};
+  }
+  __device__ static void store(xyzz<fq2>& p, const xyzz<R>& v) {
+    if (!split_role1<fq2h>()) store_half(p, xyzz<fq2h>{v.x.v, v.y.v, v.zz.v, v.zzz.v});
+  }
+};
+
+}  // namespace zk

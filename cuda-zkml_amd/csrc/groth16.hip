@@ -684,7 +684,8 @@ static int zk_prove_impl(zk_context* ctx, const zk_pk* pk, const zk_r1cs* c, con
   auto run_b2 = [&] {
     hipStream_t js = ctx->job_stream[S_G2];
     record(4 + 2 * JOB_B2, js, rc_b2);
-    if (rc_b2 == ZK_OK && nb2) rc_b2 = msm_recs_ws(ctx, ctx->job_ws[JOB_B2], true, pk->B2, d_w, nb2, b2_msm, js);
+    if (rc_b2 == ZK_OK && nb2)
+      rc_b2 = msm_recs_ws(ctx, ctx->job_ws[JOB_B2], true, pk->B2, d_w, nb2, b2_msm, js, /*beside=*/true);
     record(5 + 2 * JOB_B2, js, rc_b2);
   };
   auto run_g1 = [&] {

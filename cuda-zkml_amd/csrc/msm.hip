@@ -664,13 +664,14 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(sizeof(F) =
 }
 
 // The chunk combine and the bucket reduction are chains of dependent point
-// additions run by comparatively few threads.  They work on Lanes<F>: one
-// lane per point for G1, a lane pair per point for G2 (see curve_split.hpp),
-// so a G2 chain runs about twice as fast.  `item` is the pair index; both
-// lanes of a pair always take the same branches.
-template <class F>
+// additions run by comparatively few threads.  They are templated on the
+// lane layout LN (curve_split.hpp): Lanes<F> (one lane per G1 point, a lane
+// pair per G2 point) or SplitLanes<F> (each point operation dealt to two
+// lane groups: 2 lanes per G1 point, 4 per G2 point).  `item` is the point's
+// index; all lanes of an item always take the same branches.
+template <class LN>
 __device__ __forceinline__ uint32_t lane_item() {
-  return (blockIdx.x * blockDim.x + threadIdx.x) / Lanes<F>::N;
+  return (blockIdx.x * blockDim.x + threadIdx.x) / LN::N;
 }
 
 // Chunk combine.  The partials of a bucket whose run spans chunks c0 .. c1
@@ -679,14 +680,13 @@ __device__ __forceinline__ uint32_t lane_item() {
 // When no bucket spans more than MSM_SERIAL_SPAN + 1 chunks, one launch:
 // the chunk where a spanning run starts adds the head partials of the
 // following chunks it covers, in order, and stores the bucket.
-template <class F>
+template <class F, class LN>
 __global__ __launch_bounds__(256) void k_msm_combine_serial(ChunkSlots<F> all_slots,
                                                             const uint32_t* __restrict__ end, uint32_t nchunks,
                                                             uint32_t L0, size_t nbuckets,
                                                             xyzz<F>* __restrict__ buckets) {
-  typedef Lanes<F> LN;
   msm_priority<F>();
-  const uint32_t ch = lane_item<F>();
+  const uint32_t ch = lane_item<LN>();
   if (ch >= nchunks) return;
   const ChunkSlots<F> slots = all_slots.at(blockIdx.y, nchunks);
   buckets += blockIdx.y * nbuckets;
@@ -705,15 +705,14 @@ __global__ __launch_bounds__(256) void k_msm_combine_serial(ChunkSlots<F> all_sl
 // c1 - c0 + 1 chunk c0 holds the bucket's sum and stores it.  A chunk has at
 // most one active job: a head job needs its bucket to continue past the
 // chunk, and then the chunk's last run is that bucket (no tail).
-template <class F>
+template <class F, class LN>
 __global__ __launch_bounds__(256) void k_msm_combine(ChunkSlots<F> all_slots, const uint32_t* __restrict__ start,
                                                      const uint32_t* __restrict__ end, uint32_t nchunks,
                                                      uint32_t L0, uint32_t step, size_t nbuckets,
                                                      xyzz<F>* __restrict__ buckets) {
   constexpr uint32_t S = MSM_COMBINE_S;
-  typedef Lanes<F> LN;
   msm_priority<F>();
-  const uint32_t ch = lane_item<F>();
+  const uint32_t ch = lane_item<LN>();
   if (ch >= nchunks) return;
   const ChunkSlots<F> slots = all_slots.at(blockIdx.y, nchunks);
   buckets += blockIdx.y * nbuckets;
@@ -745,13 +744,12 @@ __global__ __launch_bounds__(256) void k_msm_combine(ChunkSlots<F> all_slots, co
 // per group: P_k (that sum) and RUN_k = SR_0.
 // Level 2 (k_msm_reduce2) weights group k by K and k + 1 - K, so its chain
 // holds log2 K doublings where contiguous groups would need log2(T G).
-// "Thread" t is a lane pair for G2 (Lanes<F>); T = blockDim.x / Lanes<F>::N.
+// "Thread" t is an item of the lane layout LN; T = blockDim.x / LN::N.
 
 // Inclusive suffix scan over the T values held by the items of a workgroup;
 // returns this item's sum_{u >= t} v_u.
-template <class F, class R>
+template <class F, class LN, class R>
 __device__ __forceinline__ xyzz<R> wg_suffix_scan(xyzz<R> v, xyzz<F>* sh, int T) {
-  typedef Lanes<F> LN;
   const int t = threadIdx.x / LN::N;
   LN::store(sh[t], v);
   __syncthreads();
@@ -770,9 +768,8 @@ __device__ __forceinline__ xyzz<R> wg_suffix_scan(xyzz<R> v, xyzz<F>* sh, int T)
 }
 
 // Sum of the T values of a workgroup (T a power of two), valid in item 0.
-template <class F, class R>
+template <class F, class LN, class R>
 __device__ __forceinline__ xyzz<R> wg_sum(xyzz<R> v, xyzz<F>* sh, int T) {
-  typedef Lanes<F> LN;
   const int t = threadIdx.x / LN::N;
   __syncthreads();
   LN::store(sh[t], v);
@@ -791,14 +788,12 @@ __device__ __forceinline__ xyzz<R> wg_sum(xyzz<R> v, xyzz<F>* sh, int T) {
 // each (G = 2^log2g).  Windows of several base sets follow each other (W_set
 // windows per set); the sorted-list bounds start/end are those of the window
 // within its set.
-template <class F, int TMAX>
-__global__ __launch_bounds__(TMAX * Lanes<F>::N) void k_msm_reduce1(const xyzz<F>* __restrict__ buckets,
-                                                                    const uint32_t* __restrict__ start,
-                                                                    const uint32_t* __restrict__ end, uint32_t B1,
-                                                                    uint32_t K, uint32_t W_set, int log2g,
-                                                                    xyzz<F>* __restrict__ P,
-                                                                    xyzz<F>* __restrict__ RUN) {
-  typedef Lanes<F> LN;
+template <class F, int TMAX, class LN>
+__global__ __launch_bounds__(TMAX * LN::N) void k_msm_reduce1(const xyzz<F>* __restrict__ buckets,
+                                                              const uint32_t* __restrict__ start,
+                                                              const uint32_t* __restrict__ end, uint32_t B1,
+                                                              uint32_t K, uint32_t W_set, int log2g,
+                                                              xyzz<F>* __restrict__ P, xyzz<F>* __restrict__ RUN) {
   typedef typename LN::R R;
   msm_priority<F>();
   __shared__ xyzz<F> sh[TMAX];
@@ -817,14 +812,14 @@ __global__ __launch_bounds__(TMAX * Lanes<F>::N) void k_msm_reduce1(const xyzz<F
     if (end[sb + off] > start[sb + off]) xyzz_add(run, LN::load(buckets[kb + off]));
     xyzz_add(acc, run);
   }
-  xyzz<R> sr = wg_suffix_scan<F, R>(run, sh, T);
+  xyzz<R> sr = wg_suffix_scan<F, LN, R>(run, sh, T);
   if (t >= 1) {
     for (int d = 0; d < log2g; d++) xyzz_dbl(sr);
     xyzz_add(acc, sr);
   } else {
     LN::store(RUN[blockIdx.x], sr);  // item 0 holds the group total
   }
-  xyzz<R> tot = wg_sum<F, R>(acc, sh, T);
+  xyzz<R> tot = wg_sum<F, LN, R>(acc, sh, T);
   if (t == 0) LN::store(P[blockIdx.x], tot);
 }
 
@@ -847,10 +842,9 @@ __device__ __forceinline__ xyzz<R> shfl_down_pt(const xyzz<R>& p, int lanes) {
 //                   = sum_k [SR_k + K (P_k - RUN_k)],  SR_k = sum_{k' >= k} RUN_k'.
 // Wave 1 forms K (P_k - RUN_k) (log2 K doublings) while wave 0 forms the
 // suffix sums with lane shuffles; wave 0 then adds them and sums the items.
-template <class F>
+template <class F, class LN>
 __global__ __launch_bounds__(128) void k_msm_reduce2(const xyzz<F>* __restrict__ P, const xyzz<F>* __restrict__ RUN,
                                                      uint32_t K, int log2k, xyzz<F>* __restrict__ out) {
-  typedef Lanes<F> LN;
   typedef typename LN::R R;
   msm_priority<F>();
   __shared__ xyzz<F> ku[64];
@@ -1119,29 +1113,58 @@ static int msm_run_sets(zk_context* ctx, MsmWorkspace& ws, const BaseSets& sets,
   ZK_TRY(ctx->ensure(ws.tpt, (size_t)nsets * nchunks * sizeof(xyzz<F>)));
 
   ChunkSlots<F> slots{(uint32_t*)ws.hkey.p, (uint32_t*)ws.tkey.p, (xyzz<F>*)ws.hpt.p, (xyzz<F>*)ws.tpt.p};
-  const uint32_t gxl = cdiv((size_t)nchunks * Lanes<F>::N, 256);  // combine: Lanes<F>::N lanes per chunk
+  const uint32_t gxl = cdiv((size_t)nchunks * Lanes<F>::N, 256);  // accumulation: Lanes<F>::N lanes per chunk
   const uint32_t nwaves = cdiv((size_t)nchunks * Lanes<F>::N, 64);
   ZK_LAUNCH(ctx, st, "msm_accumulate", k_msm_accumulate<F>, dim3(gxl, nsets), dim3(256), 0, sorted, sets, start, end,
             wstat, nchunks, cpw, n_pad, L0, nbuckets, buckets, slots, nwaves, wave_scatter(nwaves));
+  // The chunk combine and the bucket reduction are chains of dependent
+  // additions.  Few of their waves are busy at once (the combine's active
+  // chunks are the spanning runs), so they deal each point operation to two
+  // lane groups (SplitLanes) wherever the plain layout would leave SIMDs idle.
+  // Alone on the GPU a G2 MSM's combine stays on lane pairs (split over four
+  // lanes its sparse chains shared SIMDs: G2 2^16 0.12 -> 0.15 ms); beside
+  // other MSMs, where the SIMDs are shared anyway, it splits (proofs of 2^13
+  // and 2^16 constraints 3-5% shorter).
+  typedef SplitLanes<F> SL;
+  const bool split_combine = !G2 || beside;
+  const uint32_t gxs = cdiv((size_t)nchunks * (split_combine ? SL::N : Lanes<F>::N), 256);
   // The largest bucket decides the combine: one serial launch for spans up to
   // MSM_SERIAL_SPAN + 1 chunks, else levels folding MSM_COMBINE_S partials.
   const uint32_t max_span = (maxrun + L0 - 2) / L0 + 1;  // chunks spanned by the largest bucket
   if (max_span <= MSM_SERIAL_SPAN + 1) {
-    if (max_span > 1)
-      ZK_LAUNCH(ctx, st, "msm_combine", k_msm_combine_serial<F>, dim3(gxl, nsets), dim3(256), 0, slots, end,
+    if (max_span > 1 && split_combine)
+      ZK_LAUNCH(ctx, st, "msm_combine", (k_msm_combine_serial<F, SL>), dim3(gxs, nsets), dim3(256), 0, slots, end,
                 nchunks, L0, nbuckets, buckets);
+    else if (max_span > 1)
+      ZK_LAUNCH(ctx, st, "msm_combine", (k_msm_combine_serial<F, Lanes<F>>), dim3(gxs, nsets), dim3(256), 0, slots,
+                end, nchunks, L0, nbuckets, buckets);
   } else {
-    for (uint64_t step = 1; step < max_span; step *= MSM_COMBINE_S)
-      ZK_LAUNCH(ctx, st, "msm_combine", k_msm_combine<F>, dim3(gxl, nsets), dim3(256), 0, slots, start, end, nchunks,
-                L0, (uint32_t)step, nbuckets, buckets);
+    for (uint64_t step = 1; step < max_span; step *= MSM_COMBINE_S) {
+      if (split_combine)
+        ZK_LAUNCH(ctx, st, "msm_combine", (k_msm_combine<F, SL>), dim3(gxs, nsets), dim3(256), 0, slots, start, end,
+                  nchunks, L0, (uint32_t)step, nbuckets, buckets);
+      else
+        ZK_LAUNCH(ctx, st, "msm_combine", (k_msm_combine<F, Lanes<F>>), dim3(gxs, nsets), dim3(256), 0, slots, start,
+                  end, nchunks, L0, (uint32_t)step, nbuckets, buckets);
+    }
   }
 
   // bucket reduction: level 1 (T threads x G buckets per group), level 2 per window
   // items per workgroup (a G2 item is a lane pair: 256 lanes either way)
   constexpr int TMAX = sizeof(F) == sizeof(fq) ? 256 : 128;
   constexpr int KMAX = 64 / Lanes<F>::N;  // level 2 holds the K groups of a window in one wave
+  // Level 1 splits its point operations (SplitLanes) when the plain layout
+  // would fill at most half of the SIMDs.  Alone on the GPU a split
+  // workgroup takes half the items (256 lanes, one wave per SIMD) and a
+  // window twice the groups, so the chains spread over more CUs instead of
+  // sharing SIMDs (G1 2^16 0.58 -> 0.53 ms, G2 2^16 1.08 -> 1.00 ms); beside
+  // other MSMs it keeps the full items (fewer workgroups find CU slots
+  // sooner: proofs 3-5% shorter that way).
+  const bool split1 = (size_t)W * nsets * B / 4 * Lanes<F>::N <= (size_t)512 * 64;
+  const bool half1 = split1 && !beside;
+  const int TM = half1 ? TMAX / 2 : TMAX;
   // measured: T = TMAX; G = 8 for 2^15 buckets per window, else 4
-  int T1 = TMAX, log2g = B >= 32768 ? 3 : 2;
+  int T1 = TM, log2g = B >= 32768 ? 3 : 2;
   // shrink the group for small windows: T1 * G <= B
   while (log2g > 0 && (T1 << log2g) > (int)B) log2g--;
   while (T1 > 1 && (T1 << log2g) > (int)B) T1 >>= 1;
@@ -1150,7 +1173,7 @@ static int msm_run_sets(zk_context* ctx, MsmWorkspace& ws, const BaseSets& sets,
     log2g++;
     K >>= 1;
   }
-  if (T1 < 1 || T1 > TMAX || (T1 & (T1 - 1)) || K < 1 || (size_t)K * ((size_t)T1 << log2g) != B)
+  if (T1 < 1 || T1 > TM || (T1 & (T1 - 1)) || K < 1 || (size_t)K * ((size_t)T1 << log2g) != B)
     return ctx->fail(ZK_ERR_INVALID, "msm: unsupported reduction shape");
   const uint32_t WS = (uint32_t)W * nsets;  // windows of all sets
   ZK_TRY(ctx->ensure(ws.seg, (size_t)K * WS * sizeof(xyzz<F>)));
@@ -1159,13 +1182,26 @@ static int msm_run_sets(zk_context* ctx, MsmWorkspace& ws, const BaseSets& sets,
   xyzz<F>* Pk = (xyzz<F>*)ws.seg.p;
   xyzz<F>* RUNk = (xyzz<F>*)ws.grp.p;
   xyzz<F>* win = (xyzz<F>*)ws.win.p;
-  ZK_LAUNCH(ctx, st, "msm_reduce", (k_msm_reduce1<F, TMAX>), dim3(K * WS), dim3(T1 * Lanes<F>::N), 0, buckets, start,
-            end, B, K, (uint32_t)W, log2g, Pk, RUNk);
+  if (half1) {
+    ZK_LAUNCH(ctx, st, "msm_reduce", (k_msm_reduce1<F, TMAX / 2, SL>), dim3(K * WS), dim3(T1 * SL::N), 0, buckets,
+              start, end, B, K, (uint32_t)W, log2g, Pk, RUNk);
+  } else if (split1) {
+    ZK_LAUNCH(ctx, st, "msm_reduce", (k_msm_reduce1<F, TMAX, SL>), dim3(K * WS), dim3(T1 * SL::N), 0, buckets, start,
+              end, B, K, (uint32_t)W, log2g, Pk, RUNk);
+  } else {
+    ZK_LAUNCH(ctx, st, "msm_reduce", (k_msm_reduce1<F, TMAX, Lanes<F>>), dim3(K * WS), dim3(T1 * Lanes<F>::N), 0,
+              buckets, start, end, B, K, (uint32_t)W, log2g, Pk, RUNk);
+  }
   int log2k = 0;
   while ((1u << log2k) < K) log2k++;
   // one group per window: its P is the window sum (no level-2 launch, which
-  // beside other MSMs would wait for a CU with room for its two waves)
-  if (K > 1) ZK_LAUNCH(ctx, st, "msm_reduce2", k_msm_reduce2<F>, dim3(WS), dim3(128), 0, Pk, RUNk, K, log2k, win);
+  // beside other MSMs would wait for a CU with room for its two waves); level
+  // 2 holds a window's K groups in one wave, split when they fit
+  if (K > 1 && K * SL::N <= 64) {
+    ZK_LAUNCH(ctx, st, "msm_reduce2", (k_msm_reduce2<F, SL>), dim3(WS), dim3(128), 0, Pk, RUNk, K, log2k, win);
+  } else if (K > 1) {
+    ZK_LAUNCH(ctx, st, "msm_reduce2", (k_msm_reduce2<F, Lanes<F>>), dim3(WS), dim3(128), 0, Pk, RUNk, K, log2k, win);
+  }
   std::vector<xyzz<F>> parts((size_t)WS);
   ZK_HIP(ctx, hipMemcpyAsync(parts.data(), K > 1 ? win : Pk, parts.size() * sizeof(xyzz<F>), hipMemcpyDeviceToHost,
                              st));

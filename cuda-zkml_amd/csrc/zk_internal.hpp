@@ -186,7 +186,8 @@ void msm_workspace_free(MsmWorkspace* ws);
 // MSM over records with an explicit workspace (one per concurrent caller).
 // beside: the MSM shares the GPU with other kernels (a proof); a G1 MSM then
 // gives each accumulation thread half as many entries, so its waves free CU
-// slots for the other streams' kernels sooner.
+// slots for the other streams' kernels sooner, and the latency-bound combine
+// and reduction choose their lane layouts for a shared GPU.
 int msm_recs_ws(zk_context* ctx, MsmWorkspace* ws, bool g2, const void* d_recs, const void* d_scalars, size_t n,
                 uint64_t* out_affine, hipStream_t st, bool beside = false);
 // G1 MSMs of up to 3 point sets over one scalar vector of n entries, sharing
