@@ -881,10 +881,13 @@ __global__ __launch_bounds__(128) void k_msm_reduce2(const xyzz<F>* __restrict__
 }
 
 // ------------------------------------------------------------------ workspace
+constexpr int MSM_MAX_W = 32;  // windows of the narrowest window (8 bits)
+
 struct MsmWorkspace {
   DevBuf recs, dig, hist, tot, lex, bsum, bmax, boff, tmp, sorted, start, end, wstat, buckets, hkey, tkey, hpt, tpt,
       seg, grp, win;
   uint32_t* h_stat = nullptr;  // pinned, 2 words per window
+  void* h_parts = nullptr;     // pinned, the per-window partials of every set
   hipEvent_t stat_ready = nullptr;
 };
 
@@ -895,6 +898,7 @@ void msm_workspace_free(MsmWorkspace* ws) {
                     &ws->tpt, &ws->seg, &ws->grp, &ws->win})
     if (b->p) (void)hipFree(b->p);
   if (ws->h_stat) (void)hipHostFree(ws->h_stat);
+  if (ws->h_parts) (void)hipHostFree(ws->h_parts);
   if (ws->stat_ready) (void)hipEventDestroy(ws->stat_ready);
   delete ws;
 }
@@ -996,6 +1000,227 @@ static void host_finish(const std::vector<xyzz<F>>& parts, int W, int per_w, uin
   HostSide<F>::out(ax, ay, out);
 }
 
+// Sizes of one MSM: n points, W windows of about c bits, B buckets per window.
+struct MsmShape {
+  size_t n;
+  int W;
+  uint32_t B;
+  uint32_t n_pad;  // window region of the sorted list, padded to the longest chunk
+  uint32_t S;      // slices per window of the sort: about 256 blocks, each slice at least B points
+};
+
+// Counting sort of all windows on st.  The windows' entry counts and largest
+// buckets are copied to ws.h_stat, and ws.stat_ready is recorded after the
+// copy (the scatter is still running then).
+static int msm_sort(zk_context* ctx, MsmWorkspace& ws, const MsmShape& sh, hipStream_t st) {
+  const size_t n = sh.n;
+  const int W = sh.W;
+  const uint32_t B = sh.B, n_pad = sh.n_pad, S = sh.S, nb = B / SCAN_T;  // nb: column-scan blocks per window
+  const uint32_t slice = (uint32_t)cdiv(n, S);
+  const uint32_t* dig = (const uint32_t*)ws.dig.p;
+  uint32_t* hist = (uint32_t*)ws.hist.p;
+  uint32_t* tot = (uint32_t*)ws.tot.p;
+  uint32_t* lex = (uint32_t*)ws.lex.p;
+  uint32_t* bsum = (uint32_t*)ws.bsum.p;
+  uint32_t* bmax = (uint32_t*)ws.bmax.p;
+  uint32_t* boff = (uint32_t*)ws.boff.p;
+  uint32_t* start = (uint32_t*)ws.start.p;
+  uint32_t* end = (uint32_t*)ws.end.p;
+  uint32_t* wstat = (uint32_t*)ws.wstat.p;
+  uint2* sorted = (uint2*)ws.sorted.p;
+  if (B <= 4096) {
+    ZK_LAUNCH(ctx, st, "msm_hist", k_msm_hist<4096>, dim3(S, W), dim3(SORT_T), 0, dig, n, slice, S, B, hist);
+  } else {
+    ZK_LAUNCH(ctx, st, "msm_hist", k_msm_hist<32768>, dim3(S, W), dim3(SORT_T), 0, dig, n, slice, S, B, hist);
+  }
+  ZK_LAUNCH(ctx, st, "msm_scan", k_msm_colscan, dim3((uint32_t)W * nb), dim3(SCAN_T), 0, hist, S, B, tot, lex, bsum,
+            bmax);
+  ZK_LAUNCH(ctx, st, "msm_scan", k_msm_bscan, dim3(W), dim3(256), 0, bsum, bmax, nb, boff, wstat);
+  ZK_HIP(ctx, hipMemcpyAsync(ws.h_stat, wstat, (size_t)W * 8, hipMemcpyDeviceToHost, st));
+  ZK_HIP(ctx, hipEventRecord(ws.stat_ready, st));
+  if (B <= 4096) {
+    ZK_LAUNCH(ctx, st, "msm_scatter", k_msm_scatter<4096>, dim3(S, W), dim3(SORT_T), 0, dig, n, slice, S, B, n_pad,
+              hist, boff, lex, tot, start, end, sorted);
+  } else {
+    const uint32_t BPC = B / MSM_NCB;  // 32..128
+    uint2* tmp = (uint2*)ws.tmp.p;
+    ZK_LAUNCH(ctx, st, "msm_scatter", k_msm_scatter_coarse, dim3(S, W), dim3(SORT_T), 0, dig, n, slice, S, B, BPC,
+              n_pad, hist, boff, lex, tot, start, end, tmp);
+    ZK_LAUNCH(ctx, st, "msm_place", k_msm_place, dim3(MSM_NCB, W), dim3(PLACE_T), 0, tmp, B, BPC, start, end,
+              sorted);
+  }
+  return ZK_OK;
+}
+
+// Accumulation shape, from the sort statistics.
+struct AccPlan {
+  uint32_t L0;        // sorted entries per chunk
+  uint32_t cpw;       // chunks per window
+  uint32_t nchunks;   // chunks of one set
+  uint32_t max_span;  // chunks spanned by the largest bucket
+};
+
+// Entries per accumulation thread, by the entry count (G1: zero digits are
+// no entries, so skewed scalars, such as a witness of small values, count
+// for less than W*n): short chunks give small MSMs enough threads (a thread's
+// chunk is a serial chain of additions), long chunks keep the chunk-combine
+// tree of large ones shallow.  Measured on MI355X over 2^10 .. 2^20 points,
+// G1 and G2, uniform and witness-like scalars.  Beside other kernels (see
+// msm_recs_ws) a G1 chunk below the longest is one step shorter (measured in
+// the 2^16 proof: 1.97 -> 1.87 ms; the 2^22 proof's MSMs keep the longest
+// chunks, shorter ones cost it 2 ms).
+template <class F>
+static AccPlan plan_accumulation(const MsmWorkspace& ws, const MsmShape& sh, bool beside) {
+  constexpr bool G2 = sizeof(F) != sizeof(fq);
+  size_t entries = 0;
+  uint32_t maxrun = 1;
+  for (int w = 0; w < sh.W; w++) {
+    entries += ws.h_stat[2 * w];
+    maxrun = std::max(maxrun, ws.h_stat[2 * w + 1]);
+  }
+  entries += entries / 32;  // uniform scalars' few zero digits keep their chunk length
+  // a G2 chunk combine costs about 3x a G1 one: shorter G2 chunks for skewed
+  // scalars lost more there than they gained (2^16 witness-like G2 MSM 1.30 ->
+  // 1.35 ms), so G2 keeps the length of W*n entries
+  if (G2) entries = (size_t)sh.W * sh.n;
+  const uint32_t L0_alone = entries >= ((size_t)1 << 23)   ? MSM_L0
+                            : entries >= ((size_t)1 << 20) ? MSM_L0 / 2
+                            : entries >= ((size_t)1 << 18) ? MSM_L0 / 4
+                                                           : MSM_L0 / 8;
+  AccPlan ap;
+  ap.L0 = G2 ? std::max<uint32_t>(L0_alone >> ZK_MSM_G2_L0_SHIFT, MSM_L0 / 8)
+             : beside && L0_alone < (uint32_t)MSM_L0 ? std::max<uint32_t>(L0_alone / 2, MSM_L0 / 8)
+                                                      : L0_alone;
+  ap.cpw = sh.n_pad / ap.L0;
+  ap.nchunks = ap.cpw * (uint32_t)sh.W;
+  ap.max_span = (maxrun + ap.L0 - 2) / ap.L0 + 1;
+  return ap;
+}
+
+// Accumulation and chunk combine of all nsets sets, on st.
+template <class F>
+static int msm_accumulate(zk_context* ctx, MsmWorkspace& ws, const MsmShape& sh, const BaseSets& sets, int nsets,
+                          const AccPlan& ap, bool beside, hipStream_t st) {
+  constexpr bool G2 = sizeof(F) != sizeof(fq);
+  const size_t nbuckets = (size_t)sh.W * sh.B;  // buckets of one set
+  const uint2* sorted = (const uint2*)ws.sorted.p;
+  const uint32_t* start = (const uint32_t*)ws.start.p;
+  const uint32_t* end = (const uint32_t*)ws.end.p;
+  const uint32_t* wstat = (const uint32_t*)ws.wstat.p;
+  xyzz<F>* buckets = (xyzz<F>*)ws.buckets.p;
+  const uint32_t nchunks = ap.nchunks, L0 = ap.L0;
+  ZK_TRY(ctx->ensure(ws.hkey, (size_t)nsets * nchunks * 4));
+  ZK_TRY(ctx->ensure(ws.tkey, (size_t)nsets * nchunks * 4));
+  ZK_TRY(ctx->ensure(ws.hpt, (size_t)nsets * nchunks * sizeof(xyzz<F>)));
+  ZK_TRY(ctx->ensure(ws.tpt, (size_t)nsets * nchunks * sizeof(xyzz<F>)));
+  ChunkSlots<F> slots{(uint32_t*)ws.hkey.p, (uint32_t*)ws.tkey.p, (xyzz<F>*)ws.hpt.p, (xyzz<F>*)ws.tpt.p};
+  const uint32_t gxl = cdiv((size_t)nchunks * Lanes<F>::N, 256);  // accumulation: Lanes<F>::N lanes per chunk
+  const uint32_t nwaves = cdiv((size_t)nchunks * Lanes<F>::N, 64);
+  ZK_LAUNCH(ctx, st, "msm_accumulate", k_msm_accumulate<F>, dim3(gxl, nsets), dim3(256), 0, sorted, sets, start, end,
+            wstat, nchunks, ap.cpw, sh.n_pad, L0, nbuckets, buckets, slots, nwaves, wave_scatter(nwaves));
+  // The chunk combine and the bucket reduction are chains of dependent
+  // additions.  Few of their waves are busy at once (the combine's active
+  // chunks are the spanning runs), so they deal each point operation to two
+  // lane groups (SplitLanes) wherever the plain layout would leave SIMDs idle.
+  // Alone on the GPU a G2 MSM's combine stays on lane pairs (split over four
+  // lanes its sparse chains shared SIMDs: G2 2^16 0.12 -> 0.15 ms); beside
+  // other MSMs, where the SIMDs are shared anyway, it splits (proofs of 2^13
+  // and 2^16 constraints 3-5% shorter).
+  typedef SplitLanes<F> SL;
+  const bool split_combine = !G2 || beside;
+  const uint32_t gxs = cdiv((size_t)nchunks * (split_combine ? SL::N : Lanes<F>::N), 256);
+  // The largest bucket decides the combine: one serial launch for spans up to
+  // MSM_SERIAL_SPAN + 1 chunks, else levels folding MSM_COMBINE_S partials.
+  if (ap.max_span <= MSM_SERIAL_SPAN + 1) {
+    if (ap.max_span > 1 && split_combine)
+      ZK_LAUNCH(ctx, st, "msm_combine", (k_msm_combine_serial<F, SL>), dim3(gxs, nsets), dim3(256), 0, slots, end,
+                nchunks, L0, nbuckets, buckets);
+    else if (ap.max_span > 1)
+      ZK_LAUNCH(ctx, st, "msm_combine", (k_msm_combine_serial<F, Lanes<F>>), dim3(gxs, nsets), dim3(256), 0, slots,
+                end, nchunks, L0, nbuckets, buckets);
+  } else {
+    for (uint64_t step = 1; step < ap.max_span; step *= MSM_COMBINE_S) {
+      if (split_combine)
+        ZK_LAUNCH(ctx, st, "msm_combine", (k_msm_combine<F, SL>), dim3(gxs, nsets), dim3(256), 0, slots, start, end,
+                  nchunks, L0, (uint32_t)step, nbuckets, buckets);
+      else
+        ZK_LAUNCH(ctx, st, "msm_combine", (k_msm_combine<F, Lanes<F>>), dim3(gxs, nsets), dim3(256), 0, slots, start,
+                  end, nchunks, L0, (uint32_t)step, nbuckets, buckets);
+    }
+  }
+  return ZK_OK;
+}
+
+// Bucket reduction of every window of every set (level 1: T threads x G
+// buckets per group, level 2 per window); the window sums (set-major) are
+// copied to the pinned ws.h_parts on st.
+template <class F>
+static int msm_reduce(zk_context* ctx, MsmWorkspace& ws, const MsmShape& sh, int nsets, bool beside, hipStream_t st) {
+  typedef SplitLanes<F> SL;
+  const uint32_t B = sh.B;
+  // items per workgroup (a G2 item is a lane pair: 256 lanes either way)
+  constexpr int TMAX = sizeof(F) == sizeof(fq) ? 256 : 128;
+  constexpr int KMAX = 64 / Lanes<F>::N;  // level 2 holds the K groups of a window in one wave
+  // Level 1 splits its point operations (SplitLanes) when the plain layout
+  // would fill at most half of the SIMDs.  Alone on the GPU a split
+  // workgroup takes half the items (256 lanes, one wave per SIMD) and a
+  // window twice the groups, so the chains spread over more CUs instead of
+  // sharing SIMDs (G1 2^16 0.58 -> 0.53 ms, G2 2^16 1.08 -> 1.00 ms); beside
+  // other MSMs it keeps the full items (fewer workgroups find CU slots
+  // sooner: proofs 3-5% shorter that way).  At 2^15 buckets per window and
+  // one wave per SIMD splitting lost (G1 2^20: 0.28 -> 0.31 ms), and so did
+  // G = 4 there (0.37 ms).
+  const bool split1 = (size_t)sh.W * nsets * B / 4 * Lanes<F>::N <= (size_t)512 * 64;
+  const bool half1 = split1 && !beside;
+  const int TM = half1 ? TMAX / 2 : TMAX;
+  // measured: T = TMAX; G = 8 for 2^15 buckets per window, else 4
+  int T1 = TM, log2g = B >= 32768 ? 3 : 2;
+  // shrink the group for small windows: T1 * G <= B
+  while (log2g > 0 && (T1 << log2g) > (int)B) log2g--;
+  while (T1 > 1 && (T1 << log2g) > (int)B) T1 >>= 1;
+  uint32_t K = B / ((uint32_t)T1 << log2g);
+  while (K > KMAX) {  // too many groups for level 2: widen the groups
+    log2g++;
+    K >>= 1;
+  }
+  if (T1 < 1 || T1 > TM || (T1 & (T1 - 1)) || K < 1 || (size_t)K * ((size_t)T1 << log2g) != B)
+    return ctx->fail(ZK_ERR_INVALID, "msm: unsupported reduction shape");
+  const uint32_t WS = (uint32_t)sh.W * nsets;  // windows of all sets
+  ZK_TRY(ctx->ensure(ws.seg, (size_t)K * WS * sizeof(xyzz<F>)));
+  ZK_TRY(ctx->ensure(ws.grp, (size_t)K * WS * sizeof(xyzz<F>)));
+  ZK_TRY(ctx->ensure(ws.win, (size_t)WS * sizeof(xyzz<F>)));
+  const xyzz<F>* buckets = (const xyzz<F>*)ws.buckets.p;
+  const uint32_t* start = (const uint32_t*)ws.start.p;
+  const uint32_t* end = (const uint32_t*)ws.end.p;
+  xyzz<F>* Pk = (xyzz<F>*)ws.seg.p;
+  xyzz<F>* RUNk = (xyzz<F>*)ws.grp.p;
+  xyzz<F>* win = (xyzz<F>*)ws.win.p;
+  if (half1) {
+    ZK_LAUNCH(ctx, st, "msm_reduce", (k_msm_reduce1<F, TMAX / 2, SL>), dim3(K * WS), dim3(T1 * SL::N), 0, buckets,
+              start, end, B, K, (uint32_t)sh.W, log2g, Pk, RUNk);
+  } else if (split1) {
+    ZK_LAUNCH(ctx, st, "msm_reduce", (k_msm_reduce1<F, TMAX, SL>), dim3(K * WS), dim3(T1 * SL::N), 0, buckets, start,
+              end, B, K, (uint32_t)sh.W, log2g, Pk, RUNk);
+  } else {
+    ZK_LAUNCH(ctx, st, "msm_reduce", (k_msm_reduce1<F, TMAX, Lanes<F>>), dim3(K * WS), dim3(T1 * Lanes<F>::N), 0,
+              buckets, start, end, B, K, (uint32_t)sh.W, log2g, Pk, RUNk);
+  }
+  int log2k = 0;
+  while ((1u << log2k) < K) log2k++;
+  // one group per window: its P is the window sum (no level-2 launch, which
+  // beside other MSMs would wait for a CU with room for its two waves); level
+  // 2 holds a window's K groups in one wave, split when they fit
+  if (K > 1 && K * SL::N <= 64) {
+    ZK_LAUNCH(ctx, st, "msm_reduce2", (k_msm_reduce2<F, SL>), dim3(WS), dim3(128), 0, Pk, RUNk, K, log2k, win);
+  } else if (K > 1) {
+    ZK_LAUNCH(ctx, st, "msm_reduce2", (k_msm_reduce2<F, Lanes<F>>), dim3(WS), dim3(128), 0, Pk, RUNk, K, log2k, win);
+  }
+  // pinned destination: a copy to pageable memory costs a staged transfer
+  // (measured: G1 2^16 MSM 0.535 -> 0.505 ms, the 2^16 proof 1.70 -> 1.62 ms)
+  ZK_HIP(ctx, hipMemcpyAsync(ws.h_parts, K > 1 ? win : Pk, (size_t)WS * sizeof(xyzz<F>), hipMemcpyDeviceToHost, st));
+  return ZK_OK;
+}
+
 // MSMs of `nsets` point sets over one scalar vector of n entries (see
 // BaseSets): one digit sort, then accumulation, chunk combine and bucket
 // reduction for all sets in the same launches (the set is a grid dimension),
@@ -1012,206 +1237,52 @@ static int msm_run_sets(zk_context* ctx, MsmWorkspace& ws, const BaseSets& sets,
   if (n > MSM_MAX_N) return ctx->fail(ZK_ERR_SIZE, "msm: n above 2^26");
   constexpr bool G2 = sizeof(F) != sizeof(fq);
   const int c = choose_c(n, G2);
-  const int W = (MSM_BITS + c - 1) / c;
-  const uint32_t B = 1u << (c - 1);  // buckets per window
-  const size_t nbuckets = (size_t)W * B;
+  MsmShape sh;
+  sh.n = n;
+  sh.W = (MSM_BITS + c - 1) / c;
+  sh.B = 1u << (c - 1);
   // window regions of the sorted list are padded to the longest chunk, so
   // every chunk length divides them (the length is chosen after the sort's
   // counts are known)
-  const uint32_t n_pad = (uint32_t)((n + MSM_L0 - 1) / MSM_L0 * MSM_L0);
-  // slices per window: about 256 blocks, each slice at least B points
-  uint32_t S = (uint32_t)std::max<size_t>(1, std::min<size_t>({(size_t)cdiv(256, W), (size_t)64, n / B}));
-  const uint32_t slice = (uint32_t)cdiv(n, S);
+  sh.n_pad = (uint32_t)((n + MSM_L0 - 1) / MSM_L0 * MSM_L0);
+  sh.S = (uint32_t)std::max<size_t>(1, std::min<size_t>({(size_t)cdiv(256, sh.W), (size_t)64, n / sh.B}));
+  const int W = sh.W;
+  if (W > MSM_MAX_W) return ctx->fail(ZK_ERR_INVALID, "msm: too many windows");
+  const size_t nbuckets = (size_t)W * sh.B;
   ZK_TRY(ctx->ensure(ws.dig, (size_t)W * n * 4));
-  ZK_TRY(ctx->ensure(ws.hist, (size_t)W * S * B * 4));
+  ZK_TRY(ctx->ensure(ws.hist, nbuckets * sh.S * 4));
   ZK_TRY(ctx->ensure(ws.tot, nbuckets * 4));
   ZK_TRY(ctx->ensure(ws.lex, nbuckets * 4));
   ZK_TRY(ctx->ensure(ws.bsum, nbuckets / SCAN_T * 4));
   ZK_TRY(ctx->ensure(ws.bmax, nbuckets / SCAN_T * 4));
   ZK_TRY(ctx->ensure(ws.boff, nbuckets / SCAN_T * 4));
-  ZK_TRY(ctx->ensure(ws.sorted, (size_t)W * n_pad * 8));
+  ZK_TRY(ctx->ensure(ws.sorted, (size_t)W * sh.n_pad * 8));
+  if (sh.B > 4096) ZK_TRY(ctx->ensure(ws.tmp, (size_t)W * sh.n_pad * 8));
   ZK_TRY(ctx->ensure(ws.start, nbuckets * 4));
   ZK_TRY(ctx->ensure(ws.end, nbuckets * 4));
   ZK_TRY(ctx->ensure(ws.wstat, (size_t)W * 8));
   ZK_TRY(ctx->ensure(ws.buckets, nsets * nbuckets * sizeof(xyzz<F>)));
-  if (!ws.h_stat) ZK_HIP(ctx, hipHostMalloc((void**)&ws.h_stat, 2 * 32 * 4, hipHostMallocDefault));
+  if (!ws.h_stat) ZK_HIP(ctx, hipHostMalloc((void**)&ws.h_stat, 2 * MSM_MAX_W * 4, hipHostMallocDefault));
+  if (!ws.h_parts)
+    ZK_HIP(ctx, hipHostMalloc(&ws.h_parts, MSM_SETS * MSM_MAX_W * sizeof(xyzz<fq2>), hipHostMallocDefault));
   if (!ws.stat_ready) ZK_HIP(ctx, hipEventCreateWithFlags(&ws.stat_ready, hipEventDisableTiming));
 
-  uint32_t* dig = (uint32_t*)ws.dig.p;
-  uint32_t* hist = (uint32_t*)ws.hist.p;
-  uint32_t* tot = (uint32_t*)ws.tot.p;
-  uint32_t* lex = (uint32_t*)ws.lex.p;
-  uint32_t* bsum = (uint32_t*)ws.bsum.p;
-  uint32_t* bmax = (uint32_t*)ws.bmax.p;
-  uint32_t* boff = (uint32_t*)ws.boff.p;
-  uint2* sorted = (uint2*)ws.sorted.p;
-  uint32_t* start = (uint32_t*)ws.start.p;
-  uint32_t* end = (uint32_t*)ws.end.p;
-  uint32_t* wstat = (uint32_t*)ws.wstat.p;
-  xyzz<F>* buckets = (xyzz<F>*)ws.buckets.p;
-
-  ZK_LAUNCH(ctx, st, "msm_digits", k_msm_digits, dim3(cdiv(n, 256)), dim3(256), 0, dig, (const uint4*)d_scalars, n,
-            W);
-  if (B <= 4096) {
-    ZK_LAUNCH(ctx, st, "msm_hist", k_msm_hist<4096>, dim3(S, W), dim3(SORT_T), 0, dig, n, slice, S, B, hist);
-  } else {
-    ZK_LAUNCH(ctx, st, "msm_hist", k_msm_hist<32768>, dim3(S, W), dim3(SORT_T), 0, dig, n, slice, S, B, hist);
-  }
-  const uint32_t nb = B / SCAN_T;  // column-scan blocks per window
-  ZK_LAUNCH(ctx, st, "msm_scan", k_msm_colscan, dim3((uint32_t)(nbuckets / SCAN_T)), dim3(SCAN_T), 0, hist, S, B,
-            tot, lex, bsum, bmax);
-  ZK_LAUNCH(ctx, st, "msm_scan", k_msm_bscan, dim3(W), dim3(256), 0, bsum, bmax, nb, boff, wstat);
-  ZK_HIP(ctx, hipMemcpyAsync(ws.h_stat, wstat, (size_t)W * 8, hipMemcpyDeviceToHost, st));
-  ZK_HIP(ctx, hipEventRecord(ws.stat_ready, st));
-  if (B <= 4096) {
-    ZK_LAUNCH(ctx, st, "msm_scatter", k_msm_scatter<4096>, dim3(S, W), dim3(SORT_T), 0, dig, n, slice, S, B, n_pad,
-              hist, boff, lex, tot, start, end, sorted);
-  } else {
-    const uint32_t BPC = B / MSM_NCB;  // 32..128
-    ZK_TRY(ctx->ensure(ws.tmp, (size_t)W * n_pad * 8));
-    uint2* tmp = (uint2*)ws.tmp.p;
-    ZK_LAUNCH(ctx, st, "msm_scatter", k_msm_scatter_coarse, dim3(S, W), dim3(SORT_T), 0, dig, n, slice, S, B, BPC,
-              n_pad, hist, boff, lex, tot, start, end, tmp);
-    ZK_LAUNCH(ctx, st, "msm_place", k_msm_place, dim3(MSM_NCB, W), dim3(PLACE_T), 0, tmp, B, BPC, start, end,
-              sorted);
-  }
-
-  // The windows' entry counts and largest buckets come back while the scatter
-  // and placement run.  Entries per accumulation thread, by the entry count
-  // (G1: zero digits are no entries, so skewed scalars, such as a witness of
-  // small values, count for less than W*n): short chunks give small MSMs
-  // enough threads (a thread's chunk is a serial chain of additions), long
-  // chunks keep the chunk-combine tree of large ones shallow.  Measured on
-  // MI355X over 2^10 .. 2^20 points, G1 and G2, uniform and witness-like
-  // scalars.  Beside other kernels (see msm_recs_ws) a G1 chunk below the
-  // longest is one step shorter (measured in the 2^16 proof: 1.97 -> 1.87 ms;
-  // the 2^22 proof's MSMs keep the longest chunks, shorter ones cost it 2 ms).
+  ZK_LAUNCH(ctx, st, "msm_digits", k_msm_digits, dim3(cdiv(n, 256)), dim3(256), 0, (uint32_t*)ws.dig.p,
+            (const uint4*)d_scalars, n, W);
+  ZK_TRY(msm_sort(ctx, ws, sh, st));
+  // the windows' entry counts and largest buckets come back while the
+  // scatter runs
   ZK_HIP(ctx, hipEventSynchronize(ws.stat_ready));
-  size_t entries = 0;
-  uint32_t maxrun = 1;
-  for (int w = 0; w < W; w++) {
-    entries += ws.h_stat[2 * w];
-    maxrun = std::max(maxrun, ws.h_stat[2 * w + 1]);
-  }
-  entries += entries / 32;  // uniform scalars' few zero digits keep their chunk length
-  // a G2 chunk combine costs about 3x a G1 one: shorter G2 chunks for skewed
-  // scalars lost more there than they gained (2^16 witness-like G2 MSM 1.30 ->
-  // 1.35 ms), so G2 keeps the length of W*n entries
-  if (G2) entries = (size_t)W * n;
-  const uint32_t L0_alone = entries >= ((size_t)1 << 23)   ? MSM_L0
-                            : entries >= ((size_t)1 << 20) ? MSM_L0 / 2
-                            : entries >= ((size_t)1 << 18) ? MSM_L0 / 4
-                                                           : MSM_L0 / 8;
-  const uint32_t L0 = G2 ? std::max<uint32_t>(L0_alone >> ZK_MSM_G2_L0_SHIFT, MSM_L0 / 8)
-                     : beside && L0_alone < (uint32_t)MSM_L0 ? std::max<uint32_t>(L0_alone / 2, MSM_L0 / 8)
-                                                              : L0_alone;
-  const uint32_t cpw = n_pad / L0;  // chunks per window
-  const uint32_t nchunks = cpw * (uint32_t)W;
-  ZK_TRY(ctx->ensure(ws.hkey, (size_t)nsets * nchunks * 4));
-  ZK_TRY(ctx->ensure(ws.tkey, (size_t)nsets * nchunks * 4));
-  ZK_TRY(ctx->ensure(ws.hpt, (size_t)nsets * nchunks * sizeof(xyzz<F>)));
-  ZK_TRY(ctx->ensure(ws.tpt, (size_t)nsets * nchunks * sizeof(xyzz<F>)));
-
-  ChunkSlots<F> slots{(uint32_t*)ws.hkey.p, (uint32_t*)ws.tkey.p, (xyzz<F>*)ws.hpt.p, (xyzz<F>*)ws.tpt.p};
-  const uint32_t gxl = cdiv((size_t)nchunks * Lanes<F>::N, 256);  // accumulation: Lanes<F>::N lanes per chunk
-  const uint32_t nwaves = cdiv((size_t)nchunks * Lanes<F>::N, 64);
-  ZK_LAUNCH(ctx, st, "msm_accumulate", k_msm_accumulate<F>, dim3(gxl, nsets), dim3(256), 0, sorted, sets, start, end,
-            wstat, nchunks, cpw, n_pad, L0, nbuckets, buckets, slots, nwaves, wave_scatter(nwaves));
-  // The chunk combine and the bucket reduction are chains of dependent
-  // additions.  Few of their waves are busy at once (the combine's active
-  // chunks are the spanning runs), so they deal each point operation to two
-  // lane groups (SplitLanes) wherever the plain layout would leave SIMDs idle.
-  // Alone on the GPU a G2 MSM's combine stays on lane pairs (split over four
-  // lanes its sparse chains shared SIMDs: G2 2^16 0.12 -> 0.15 ms); beside
-  // other MSMs, where the SIMDs are shared anyway, it splits (proofs of 2^13
-  // and 2^16 constraints 3-5% shorter).
-  typedef SplitLanes<F> SL;
-  const bool split_combine = !G2 || beside;
-  const uint32_t gxs = cdiv((size_t)nchunks * (split_combine ? SL::N : Lanes<F>::N), 256);
-  // The largest bucket decides the combine: one serial launch for spans up to
-  // MSM_SERIAL_SPAN + 1 chunks, else levels folding MSM_COMBINE_S partials.
-  const uint32_t max_span = (maxrun + L0 - 2) / L0 + 1;  // chunks spanned by the largest bucket
-  if (max_span <= MSM_SERIAL_SPAN + 1) {
-    if (max_span > 1 && split_combine)
-      ZK_LAUNCH(ctx, st, "msm_combine", (k_msm_combine_serial<F, SL>), dim3(gxs, nsets), dim3(256), 0, slots, end,
-                nchunks, L0, nbuckets, buckets);
-    else if (max_span > 1)
-      ZK_LAUNCH(ctx, st, "msm_combine", (k_msm_combine_serial<F, Lanes<F>>), dim3(gxs, nsets), dim3(256), 0, slots,
-                end, nchunks, L0, nbuckets, buckets);
-  } else {
-    for (uint64_t step = 1; step < max_span; step *= MSM_COMBINE_S) {
-      if (split_combine)
-        ZK_LAUNCH(ctx, st, "msm_combine", (k_msm_combine<F, SL>), dim3(gxs, nsets), dim3(256), 0, slots, start, end,
-                  nchunks, L0, (uint32_t)step, nbuckets, buckets);
-      else
-        ZK_LAUNCH(ctx, st, "msm_combine", (k_msm_combine<F, Lanes<F>>), dim3(gxs, nsets), dim3(256), 0, slots, start,
-                  end, nchunks, L0, (uint32_t)step, nbuckets, buckets);
-    }
-  }
-
-  // bucket reduction: level 1 (T threads x G buckets per group), level 2 per window
-  // items per workgroup (a G2 item is a lane pair: 256 lanes either way)
-  constexpr int TMAX = sizeof(F) == sizeof(fq) ? 256 : 128;
-  constexpr int KMAX = 64 / Lanes<F>::N;  // level 2 holds the K groups of a window in one wave
-  // Level 1 splits its point operations (SplitLanes) when the plain layout
-  // would fill at most half of the SIMDs.  Alone on the GPU a split
-  // workgroup takes half the items (256 lanes, one wave per SIMD) and a
-  // window twice the groups, so the chains spread over more CUs instead of
-  // sharing SIMDs (G1 2^16 0.58 -> 0.53 ms, G2 2^16 1.08 -> 1.00 ms); beside
-  // other MSMs it keeps the full items (fewer workgroups find CU slots
-  // sooner: proofs 3-5% shorter that way).
-  const bool split1 = (size_t)W * nsets * B / 4 * Lanes<F>::N <= (size_t)512 * 64;
-  const bool half1 = split1 && !beside;
-  const int TM = half1 ? TMAX / 2 : TMAX;
-  // measured: T = TMAX; G = 8 for 2^15 buckets per window, else 4
-  int T1 = TM, log2g = B >= 32768 ? 3 : 2;
-  // shrink the group for small windows: T1 * G <= B
-  while (log2g > 0 && (T1 << log2g) > (int)B) log2g--;
-  while (T1 > 1 && (T1 << log2g) > (int)B) T1 >>= 1;
-  uint32_t K = B / ((uint32_t)T1 << log2g);
-  while (K > KMAX) {  // too many groups for level 2: widen the groups
-    log2g++;
-    K >>= 1;
-  }
-  if (T1 < 1 || T1 > TM || (T1 & (T1 - 1)) || K < 1 || (size_t)K * ((size_t)T1 << log2g) != B)
-    return ctx->fail(ZK_ERR_INVALID, "msm: unsupported reduction shape");
-  const uint32_t WS = (uint32_t)W * nsets;  // windows of all sets
-  ZK_TRY(ctx->ensure(ws.seg, (size_t)K * WS * sizeof(xyzz<F>)));
-  ZK_TRY(ctx->ensure(ws.grp, (size_t)K * WS * sizeof(xyzz<F>)));
-  ZK_TRY(ctx->ensure(ws.win, (size_t)WS * sizeof(xyzz<F>)));
-  xyzz<F>* Pk = (xyzz<F>*)ws.seg.p;
-  xyzz<F>* RUNk = (xyzz<F>*)ws.grp.p;
-  xyzz<F>* win = (xyzz<F>*)ws.win.p;
-  if (half1) {
-    ZK_LAUNCH(ctx, st, "msm_reduce", (k_msm_reduce1<F, TMAX / 2, SL>), dim3(K * WS), dim3(T1 * SL::N), 0, buckets,
-              start, end, B, K, (uint32_t)W, log2g, Pk, RUNk);
-  } else if (split1) {
-    ZK_LAUNCH(ctx, st, "msm_reduce", (k_msm_reduce1<F, TMAX, SL>), dim3(K * WS), dim3(T1 * SL::N), 0, buckets, start,
-              end, B, K, (uint32_t)W, log2g, Pk, RUNk);
-  } else {
-    ZK_LAUNCH(ctx, st, "msm_reduce", (k_msm_reduce1<F, TMAX, Lanes<F>>), dim3(K * WS), dim3(T1 * Lanes<F>::N), 0,
-              buckets, start, end, B, K, (uint32_t)W, log2g, Pk, RUNk);
-  }
-  int log2k = 0;
-  while ((1u << log2k) < K) log2k++;
-  // one group per window: its P is the window sum (no level-2 launch, which
-  // beside other MSMs would wait for a CU with room for its two waves); level
-  // 2 holds a window's K groups in one wave, split when they fit
-  if (K > 1 && K * SL::N <= 64) {
-    ZK_LAUNCH(ctx, st, "msm_reduce2", (k_msm_reduce2<F, SL>), dim3(WS), dim3(128), 0, Pk, RUNk, K, log2k, win);
-  } else if (K > 1) {
-    ZK_LAUNCH(ctx, st, "msm_reduce2", (k_msm_reduce2<F, Lanes<F>>), dim3(WS), dim3(128), 0, Pk, RUNk, K, log2k, win);
-  }
-  std::vector<xyzz<F>> parts((size_t)WS);
-  ZK_HIP(ctx, hipMemcpyAsync(parts.data(), K > 1 ? win : Pk, parts.size() * sizeof(xyzz<F>), hipMemcpyDeviceToHost,
-                             st));
+  const AccPlan ap = plan_accumulation<F>(ws, sh, beside);
+  ZK_TRY(msm_accumulate<F>(ctx, ws, sh, sets, nsets, ap, beside, st));
+  ZK_TRY(msm_reduce<F>(ctx, ws, sh, nsets, beside, st));
   ZK_HIP(ctx, hipStreamSynchronize(st));
+  const xyzz<F>* parts = (const xyzz<F>*)ws.h_parts;
   // window combination on the host (W * c doublings per set): one thread per set
   int rc_fin[MSM_SETS] = {ZK_OK, ZK_OK, ZK_OK};
   auto finish = [&](int k) {
     try {
-      host_finish<F>(std::vector<xyzz<F>>(parts.begin() + (size_t)k * W, parts.begin() + (size_t)(k + 1) * W), W,
-                     1, outs[k]);
+      host_finish<F>(std::vector<xyzz<F>>(parts + (size_t)k * W, parts + (size_t)(k + 1) * W), W, 1, outs[k]);
     } catch (...) {
       rc_fin[k] = ZK_ERR_OOM;
     }

@@ -174,6 +174,26 @@ def test_msm_g1_edge_cases(ctx):
     assert np.array_equal(got, oracle_msm(pts, sc))
 
 
+@pytest.mark.parametrize("g2", [False, True])
+def test_msm_equal_partials(ctx, g2):
+    """One point repeated with one scalar: every chunk partial and every
+    bucket's running sum meets an equal point, so the chunk combine and the
+    bucket reduction take their doubling branch (P == 0 in the addition),
+    in the plain and the split lane layouts.  Closed form: (n s mod r) k G."""
+    n = 4096 if not g2 else 1024
+    rng = np.random.default_rng(90 + g2)
+    k = from_std_arr(rand_std(1, rng))[0]
+    s = from_std_arr(rand_std(1, rng))[0]
+    km = to_mont(std_words([k] * n))
+    pts = oracle_points(km[:1], g2=g2)
+    pts = np.repeat(pts, n, axis=0)
+    sc = to_mont(std_words([s] * n))
+    got = run_msm(ctx, pts, sc, g2=g2)
+    assert np.array_equal(got, oracle_msm(pts, sc, g2=g2))
+    if not g2:
+        assert Z.g1_from_words(got) == Z.g1.pmul(Z.G1, k * s * n % Z.R)
+
+
 @pytest.mark.parametrize("log_n", [14, 20])
 def test_msm_g1_all_equal_scalars(ctx, log_n):
     """Every scalar equal: one bucket per window holds all n points (at 2^20
