@@ -50,7 +50,14 @@ namespace zk {
 constexpr int NTT_MAX_LOG = 24;
 constexpr int NTT_MAX_LOGR = 8;
 
-// SoA table of internal-form field elements: limb l of entry i at l*count+i.
+// Table of internal-form field elements.  Twiddles of a DFT step (copied to
+// LDS planes) are limb-major: limb l of entry i at l*count + i.  Tables read
+// per element from HBM (inter-pass twiddles, coset factors) are packed like
+// the elements, 8 words per entry: a tile row of T columns then reads T * 32
+// contiguous bytes, where nine limb planes would read nine runs of T * 4
+// bytes, each a fraction of a cache line (measured at 2^22: the first pass
+// fetched 0.74 GB for 0.28 GB of elements and table).
+constexpr int PACKED_WORDS = 8;
 struct FrTable {
   uint32_t* d = nullptr;
   size_t count = 0;
@@ -70,13 +77,6 @@ struct NttPlan {
 struct CosetTables {
   FrTable pre, post_inv, post_fold;
 };
-
-__device__ __forceinline__ fr load_table(const uint32_t* __restrict__ t, size_t count, size_t i) {
-  fr x;
-#pragma unroll
-  for (int l = 0; l < NL; l++) x.l[l] = t[l * count + i];
-  return x;
-}
 
 __device__ __forceinline__ void store_table(uint32_t* __restrict__ t, size_t count, size_t i, const fr& x) {
   fr c = fcanon(x);
@@ -105,6 +105,14 @@ __device__ __forceinline__ void store_elem_raw(uint4* __restrict__ p, size_t i, 
   }
   p[2 * i] = make_uint4(w[0], w[1], w[2], w[3]);
   p[2 * i + 1] = make_uint4(w[4], w[5], w[6], w[7]);
+}
+
+// Packed tables: canonical values (below m < 2^256) in the element layout.
+__device__ __forceinline__ fr load_packed(const uint32_t* __restrict__ t, size_t i) {
+  return load_elem((const uint4*)t, i);
+}
+__device__ __forceinline__ void store_packed(uint32_t* __restrict__ t, size_t i, const fr& x) {
+  store_elem_raw((uint4*)t, i, fcanon(x));
 }
 
 __device__ __forceinline__ uint32_t bitrev(uint32_t x, int bits) { return bits ? __brev(x) >> (32 - bits) : 0; }
@@ -251,11 +259,11 @@ __device__ __forceinline__ fr finish(const PassGeo& g, const PassIO& io, const T
   if (!LAST) {
     const size_t rel = ((size_t)k << g.logS) + o.m0 + c;
     pos = o.base + ((size_t)k << g.logS) + c;
-    return fmul(x, load_table(io.twp, (size_t)1 << (g.logR + g.logS), rel));
+    return fmul(x, load_packed(io.twp, rel));
   }
   pos = (size_t)(o.k0s + c) + ((size_t)o.v << g.logR0) + ((size_t)k << g.logNR);
   if (io.post_mode == POST_NONE) return freduce(x);
-  const fr m = io.post_mode == POST_TABLE ? load_table(io.post, g.n, pos) : io.scale;
+  const fr m = io.post_mode == POST_TABLE ? load_packed(io.post, pos) : io.scale;
   return fcanon(fmul(x, m));
 }
 
@@ -283,7 +291,7 @@ __device__ __forceinline__ void tile_first(const TileCtx& tc, const PassGeo& g, 
     } else {
       unroll<(1 << K)>([&](auto T) { x[T] = load_elem(src, row(T)); });
       if (io.pre_mode == PRE_TABLE)
-        unroll<(1 << K)>([&](auto T) { x[T] = fmul(x[T], load_table(io.pre, g.n, row(T))); });
+        unroll<(1 << K)>([&](auto T) { x[T] = fmul(x[T], load_packed(io.pre, row(T))); });
     }
     first_step<K>(x, tc.tw, tc.half, tc.logR);
     unroll<(1 << K)>([&](auto T) { lds_put(tc.s, tc.E, lds_ix((q << K) + T, c, tc.logT, tc.smask), x[T]); });
@@ -408,9 +416,9 @@ void k_ntt_pass(PassGeo g, PassIO io) {
 }
 
 // ------------------------------------------------------------------ tables
-// table[e] = base^(e_hi * e_lo) * mul with (e_hi, e_lo) = (e >> log_cols, e mod
-// 2^log_cols), the exponent reduced mod 2^log_order; base and mul in internal
-// form.  log_cols = 0 gives base^e (e_lo = 0 would give base^0: handled by
+// Packed table[e] = base^(e_hi * e_lo) * mul with (e_hi, e_lo) = (e >> log_cols,
+// e mod 2^log_cols), the exponent reduced mod 2^log_order; base and mul in
+// internal form.  log_cols = 0 gives base^e (e_lo = 0 would give base^0: handled by
 // the linear variant below).
 __global__ void k_fill_pow_table(uint32_t* __restrict__ t, size_t count, uint32_t log_cols, fr base, int log_order,
                                  fr mul) {
@@ -424,11 +432,11 @@ __global__ void k_fill_pow_table(uint32_t* __restrict__ t, size_t count, uint32_
     b = fsqr(b);
     ex >>= 1;
   }
-  r = fmul(r, mul);
-  store_table(t, count, e, r);
+  store_packed(t, e, fmul(r, mul));
 }
 
-__global__ void k_fill_pow_linear(uint32_t* __restrict__ t, size_t count, fr base, fr mul) {
+// table[e] = base^e * mul, limb-major or packed.
+__global__ void k_fill_pow_linear(uint32_t* __restrict__ t, size_t count, fr base, fr mul, int packed) {
   size_t e = blockIdx.x * (size_t)blockDim.x + threadIdx.x;
   if (e >= count) return;
   uint64_t ex = e;
@@ -438,7 +446,10 @@ __global__ void k_fill_pow_linear(uint32_t* __restrict__ t, size_t count, fr bas
     b = fsqr(b);
     ex >>= 1;
   }
-  store_table(t, count, e, fmul(r, mul));
+  if (packed)
+    store_packed(t, e, fmul(r, mul));
+  else
+    store_table(t, count, e, fmul(r, mul));
 }
 
 // h = (a*b - c) * zinv on the reference's Montgomery words (kept for callers
@@ -523,15 +534,16 @@ static size_t plan_table_words(const PassShape& sh, int log_n) {
   int below = log_n;
   for (int q = 0; q < sh.P; q++) {
     w += 2 * ((size_t)1 << (sh.logR[q] - 1)) * NL;
-    if (q < sh.P - 1) w += 2 * ((size_t)1 << below) * NL;
+    if (q < sh.P - 1) w += 2 * ((size_t)1 << below) * PACKED_WORDS;
     below -= sh.logR[q];
   }
   return w;
 }
 
-static int launch_fill_linear(zk_context* ctx, const FrTable& t, const fr& base, const fr& mul, hipStream_t st) {
+static int launch_fill_linear(zk_context* ctx, const FrTable& t, const fr& base, const fr& mul, bool packed,
+                              hipStream_t st) {
   ZK_LAUNCH(ctx, st, "ntt_twiddle_fill", k_fill_pow_linear, dim3(cdiv(t.count, 256)), dim3(256), 0, t.d, t.count,
-            base, mul);
+            base, mul, packed ? 1 : 0);
   return ZK_OK;
 }
 
@@ -556,7 +568,7 @@ static int plan_fill(zk_context* ctx, NttPlan* p, hipStream_t st) {
       const int lr = p->logR[q];
       fr wr = w;  // w_{R_q} = w_n^(n / R_q)
       for (int i = 0; i < log_n - lr; i++) wr = fsqr(wr);
-      ZK_TRY(launch_fill_linear(ctx, p->twr[q][d], wr, one, st));
+      ZK_TRY(launch_fill_linear(ctx, p->twr[q][d], wr, one, false, st));
       if (q < p->P - 1) {
         fr wm = w;  // w_{R_q S_q} = w_n^(n / (R_q S_q)); table over (k, m) in [R_q) x [S_q)
         for (int i = 0; i < log_n - below; i++) wm = fsqr(wm);
@@ -580,7 +592,7 @@ static void plan_place(NttPlan* p, uint32_t* words) {
       if (q < p->P - 1) {
         p->twp[q][d].count = (size_t)1 << below;
         p->twp[q][d].d = words;
-        words += p->twp[q][d].count * NL;
+        words += p->twp[q][d].count * PACKED_WORDS;
       }
     }
     below -= p->logR[q];
@@ -648,17 +660,18 @@ static int coset_get(zk_context* ctx, int log_n, uint64_t g, const NttPlan* plan
   const size_t n = (size_t)1 << log_n;
   std::unique_ptr<CosetTables> c(new CosetTables());
   void* mem = nullptr;
-  if (hipMalloc(&mem, 3 * n * NL * 4) != hipSuccess) return ctx->fail(ZK_ERR_OOM, "coset table allocation failed");
+  if (hipMalloc(&mem, 3 * n * PACKED_WORDS * 4) != hipSuccess)
+    return ctx->fail(ZK_ERR_OOM, "coset table allocation failed");
   uint32_t* w = (uint32_t*)mem;
   c->pre = FrTable{w, n};
-  c->post_inv = FrTable{w + n * NL, n};
-  c->post_fold = FrTable{w + 2 * n * NL, n};
+  c->post_inv = FrTable{w + n * PACKED_WORDS, n};
+  c->post_fold = FrTable{w + 2 * n * PACKED_WORDS, n};
   const fr gi = fr_small(g), ginv = fr_inv_host(gi);
   fr scale = fe_one<FrP>();
   if (plan->P == 1) memcpy(scale.l, plan->ninv, sizeof(scale.l));
-  int rc = launch_fill_linear(ctx, c->pre, gi, fe_one<FrP>(), st);            // g^i
-  if (rc == ZK_OK) rc = launch_fill_linear(ctx, c->post_inv, ginv, scale, st);  // g^-i (/ n when P == 1)
-  if (rc == ZK_OK) rc = launch_fill_linear(ctx, c->post_fold, gi, scale, st);   // g^i (/ n when P == 1)
+  int rc = launch_fill_linear(ctx, c->pre, gi, fe_one<FrP>(), true, st);            // g^i
+  if (rc == ZK_OK) rc = launch_fill_linear(ctx, c->post_inv, ginv, scale, true, st);  // g^-i (/ n when P == 1)
+  if (rc == ZK_OK) rc = launch_fill_linear(ctx, c->post_fold, gi, scale, true, st);   // g^i (/ n when P == 1)
   if (rc == ZK_OK && hipStreamSynchronize(st) != hipSuccess) rc = ctx->fail(ZK_ERR_HIP, "coset table fill failed");
   if (rc != ZK_OK) {
     (void)hipFree(mem);
@@ -894,7 +907,7 @@ constexpr int NTT_NA_MAX_LOG = 16;
 constexpr int NTT_NA_MAX_ELEMS_LOG = 18;
 // tables of the largest plan (log_n = 16: two passes of 2^8, a 2^16-entry
 // inter-pass table per direction) and the pass-to-pass buffer, in words
-constexpr size_t NTT_NA_TABLE_WORDS = 2 * 2 * 128 * NL + 2 * ((size_t)1 << 16) * NL;
+constexpr size_t NTT_NA_TABLE_WORDS = 2 * 2 * 128 * NL + 2 * ((size_t)1 << 16) * PACKED_WORDS;
 constexpr size_t NTT_NA_MID_WORDS = ((size_t)1 << NTT_NA_MAX_ELEMS_LOG) * 8;
 constexpr size_t NTT_NA_WORDS = NTT_NA_TABLE_WORDS + NTT_NA_MID_WORDS;
 

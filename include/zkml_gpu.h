@@ -23,6 +23,11 @@
  * Streams: `stream` arguments are hipStream_t values; NULL selects the
  * context's own stream.  Calls that return a host value synchronize.
  * A context is not re-entrant: one host thread per context at a time.
+ * The NTT calls (zk_ntt, zk_coset_ntt, zk_quotient_h) of one context share
+ * its pass-to-pass scratch buffer whatever stream they are given: two such
+ * calls on different streams must not overlap (order the second stream after
+ * the first with an event, or synchronize between them).  Twiddle and coset
+ * tables are complete before a call returns, so they are safe on any stream.
  */
 #ifndef ZKML_GPU_H
 #define ZKML_GPU_H
