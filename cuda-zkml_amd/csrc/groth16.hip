@@ -45,6 +45,9 @@ struct zk_pk {
   uint64_t beta2[16], gamma2[16], delta2[16];
   size_t nA = 0, nB1 = 0, nB2 = 0, nL = 0, nH = 0, ntau1 = 0, ntau2 = 0;
   void *A = nullptr, *B1 = nullptr, *B2 = nullptr, *L = nullptr, *H = nullptr;  // device point records
+  // window tables of the queries (null: the MSM runs over the records)
+  void *tA = nullptr, *tB1 = nullptr, *tB2 = nullptr, *tL = nullptr, *tH = nullptr;
+  zk::MsmTab tab_w, tab_b2, tab_h;  // shapes: A, B1 and L (one shared sort), B2, H
 };
 
 namespace {
@@ -521,6 +524,70 @@ int zk_quotient_h(zk_context* ctx, const zk_r1cs* c, const void* d_witness, size
   return zk::guard(ctx, [&] { return zk_quotient_h_impl(ctx, c, d_witness, m, d_h, stream); });
 }
 
+// Window tables of the proving-key queries, built at load for MSMs of
+// 2^ZK_PK_TAB_MIN_LOG .. 2^ZK_PK_TAB_MAX_LOG scalars.  The digit windows of a
+// table MSM share one bucket space, so wider windows cost no reduction per
+// window: 16 windows of 16 bits (or 20 of 13), against 24-26 windows of 10-11
+// bits in the plain MSMs at 2^16 points, reduced in sub-windows of 2^SUB
+// buckets.  A table holds W copies of its query.  Measured on the 2^16 proof
+// (config 4): 1.63 -> 1.45 ms with W = 16 for the witness G1 sets (A, B1, L
+// share one sort) and W = 20 for B2 and H (a 16-bit single window sorts
+// slower, and H's sort runs beside the other MSMs' accumulations); 2^13
+// (config 1) was 5% slower with tables (W = 20 or 26), so they start at 2^14.
+#ifndef ZK_PK_TAB_MIN_LOG
+#define ZK_PK_TAB_MIN_LOG 14
+#endif
+#ifndef ZK_PK_TAB_MAX_LOG
+#define ZK_PK_TAB_MAX_LOG 18
+#endif
+#ifndef ZK_PK_TAB_SUB
+#define ZK_PK_TAB_SUB 10
+#endif
+#ifndef ZK_PK_TAB_W_LARGE
+#define ZK_PK_TAB_W_LARGE 16
+#endif
+#ifndef ZK_PK_TAB_W_LARGE_B2
+#define ZK_PK_TAB_W_LARGE_B2 20
+#endif
+#ifndef ZK_PK_TAB_W_LARGE_H
+#define ZK_PK_TAB_W_LARGE_H 20
+#endif
+
+// Table shape for MSMs of n scalars (W = 0: no table); wlarge: windows from
+// 2^15 scalars on.
+static MsmTab table_shape(size_t n, int wlarge) {
+  MsmTab t;
+  if (n < ((size_t)1 << ZK_PK_TAB_MIN_LOG) || n > ((size_t)1 << ZK_PK_TAB_MAX_LOG)) return t;
+  t.W = n >= ((size_t)1 << 15) ? wlarge : 20;
+  const int c = (254 + t.W - 1) / t.W;  // widest window
+  t.log_sub = std::min(ZK_PK_TAB_SUB, c - 1);
+  return t;
+}
+
+static int pk_table(zk_context* ctx, bool g2, const void* recs, size_t count, const MsmTab& t, void** out) {
+  *out = nullptr;
+  if (count == 0) return ZK_OK;
+  if (hipMalloc(out, msm_table_bytes(g2, count, t)) != hipSuccess) {
+    *out = nullptr;
+    return ctx->fail(ZK_ERR_OOM, "proving key: window table allocation failed");
+  }
+  return msm_table_build(ctx, g2, recs, count, t, *out, ctx->stream);
+}
+
+static int pk_tables(zk_context* ctx, zk_pk* pk) {
+  pk->tab_w = table_shape((size_t)pk->m, ZK_PK_TAB_W_LARGE);
+  pk->tab_b2 = table_shape((size_t)pk->m, ZK_PK_TAB_W_LARGE_B2);
+  pk->tab_h = table_shape((size_t)pk->n, ZK_PK_TAB_W_LARGE_H);
+  if (pk->tab_w.W) {
+    ZK_TRY(pk_table(ctx, false, pk->A, pk->nA, pk->tab_w, &pk->tA));
+    ZK_TRY(pk_table(ctx, false, pk->B1, pk->nB1, pk->tab_w, &pk->tB1));
+    ZK_TRY(pk_table(ctx, false, pk->L, pk->nL, pk->tab_w, &pk->tL));
+  }
+  if (pk->tab_b2.W) ZK_TRY(pk_table(ctx, true, pk->B2, pk->nB2, pk->tab_b2, &pk->tB2));
+  if (pk->tab_h.W) ZK_TRY(pk_table(ctx, false, pk->H, pk->nH, pk->tab_h, &pk->tH));
+  return ZK_OK;
+}
+
 static int zk_pk_load_impl(zk_context* ctx, const char* path, zk_pk** out) {
   if (!ctx || !path || !out) return ZK_ERR_INVALID;
   *out = nullptr;
@@ -575,6 +642,7 @@ static int zk_pk_load_impl(zk_context* ctx, const char* path, zk_pk** out) {
   if (st == ZK_OK && !f.ok) st = ctx->fail(ZK_ERR_IO, "proving key truncated or malformed");
   if (st == ZK_OK && ((int)pk->nA < pk->m || (int)pk->nB1 < pk->m || (int)pk->nB2 < pk->m))
     st = ctx->fail(ZK_ERR_IO, "incomplete proving key (A/B queries shorter than num_variables)");
+  if (st == ZK_OK) st = pk_tables(ctx, pk);
   if (st != ZK_OK) {
     zk_pk_destroy(pk);
     return st;
@@ -589,7 +657,7 @@ int zk_pk_load(zk_context* ctx, const char* path, zk_pk** out) {
 
 void zk_pk_destroy(zk_pk* pk) {
   if (!pk) return;
-  for (void* p : {pk->A, pk->B1, pk->B2, pk->L, pk->H})
+  for (void* p : {pk->A, pk->B1, pk->B2, pk->L, pk->H, pk->tA, pk->tB1, pk->tB2, pk->tL, pk->tH})
     if (p) (void)hipFree(p);
   delete pk;
 }
@@ -684,7 +752,10 @@ static int zk_prove_impl(zk_context* ctx, const zk_pk* pk, const zk_r1cs* c, con
   auto run_b2 = [&] {
     hipStream_t js = ctx->job_stream[S_G2];
     record(4 + 2 * JOB_B2, js, rc_b2);
-    if (rc_b2 == ZK_OK && nb2)
+    if (rc_b2 == ZK_OK && nb2 && pk->tB2)
+      rc_b2 = msm_recs_tab(ctx, ctx->job_ws[JOB_B2], true, pk->tB2, pk->nB2, pk->tab_b2, d_w, nb2, b2_msm, js,
+                           /*beside=*/true);
+    else if (rc_b2 == ZK_OK && nb2)
       rc_b2 = msm_recs_ws(ctx, ctx->job_ws[JOB_B2], true, pk->B2, d_w, nb2, b2_msm, js, /*beside=*/true);
     record(5 + 2 * JOB_B2, js, rc_b2);
   };
@@ -692,23 +763,27 @@ static int zk_prove_impl(zk_context* ctx, const zk_pk* pk, const zk_r1cs* c, con
     hipStream_t js = ctx->job_stream[S_G1];
     record(4 + 2 * JOB_G1, js, rc_g1);
     const void* recs[3];
-    size_t lo[3], cnt[3];
+    size_t lo[3], cnt[3], rows[3];
     uint64_t* outs[3];
     int ns = 0;
-    auto add = [&](const void* r, size_t l, size_t k, uint64_t* o) {
+    // the three sets run over their window tables when the key has them
+    const bool tab = pk->tA != nullptr;
+    auto add = [&](const void* r, const void* t, size_t nrows, size_t l, size_t k, uint64_t* o) {
       if (k == 0) return;  // empty set: the result stays the identity
-      recs[ns] = r;
+      recs[ns] = tab ? t : r;
+      rows[ns] = nrows;
       lo[ns] = l;
       cnt[ns] = k;
       outs[ns++] = o;
     };
     memset(a_msm, 0, sizeof(a_msm));
     memset(b1_msm, 0, sizeof(b1_msm));
-    add(pk->A, 0, na, a_msm);
-    add(pk->B1, 0, nb1, b1_msm);
-    add(pk->L, 1 + (size_t)pk->npub, npriv_l > 0 ? (size_t)npriv_l : 0, l_msm);
+    add(pk->A, pk->tA, pk->nA, 0, na, a_msm);
+    add(pk->B1, pk->tB1, pk->nB1, 0, nb1, b1_msm);
+    add(pk->L, pk->tL, pk->nL, 1 + (size_t)pk->npub, npriv_l > 0 ? (size_t)npriv_l : 0, l_msm);
     if (rc_g1 == ZK_OK && ns)
-      rc_g1 = msm_g1_sets_ws(ctx, ctx->job_ws[JOB_G1], ns, recs, lo, cnt, d_w, m, outs, js, /*beside=*/true);
+      rc_g1 = msm_g1_sets_ws(ctx, ctx->job_ws[JOB_G1], ns, recs, lo, cnt, d_w, m, outs, js, /*beside=*/true,
+                             tab ? &pk->tab_w : nullptr, tab ? rows : nullptr);
     record(5 + 2 * JOB_G1, js, rc_g1);
     if (rc_g1 == ZK_OK) {
       g1_tail = g1_from_words(a_msm).mul(s).add(g1_from_words(l_msm));
@@ -750,7 +825,10 @@ static int zk_prove_impl(zk_context* ctx, const zk_pk* pk, const zk_r1cs* c, con
   if (qrc == ZK_OK && hipEventRecord(ev[2], st) != hipSuccess) qrc = ctx->fail(ZK_ERR_HIP, "prove: event record");
   if (qrc == ZK_OK) {  // H after the quotient, same stream
     record(4 + 2 * JOB_H, st, rc_h);
-    if (rc_h == ZK_OK && nh)
+    if (rc_h == ZK_OK && nh && pk->tH)
+      rc_h = msm_recs_tab(ctx, ctx->job_ws[JOB_H], false, pk->tH, pk->nH, pk->tab_h, d_h, nh, h_msm, st,
+                          /*beside=*/true);
+    else if (rc_h == ZK_OK && nh)
       rc_h = msm_recs_ws(ctx, ctx->job_ws[JOB_H], false, pk->H, d_h, nh, h_msm, st, /*beside=*/true);
     else if (!nh) memset(h_msm, 0, sizeof(h_msm));
     record(5 + 2 * JOB_H, st, rc_h);

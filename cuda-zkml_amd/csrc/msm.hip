@@ -70,6 +70,9 @@ constexpr uint32_t MSM_COMBINE_S = ZK_MSM_COMBINE_S;
 #ifndef ZK_MSM_G2_ACC_WAVES
 #define ZK_MSM_G2_ACC_WAVES 3
 #endif
+#ifndef ZK_MSM_TAB_SLICE
+#define ZK_MSM_TAB_SLICE 8192
+#endif
 // Bits covered by the windows.  After the optional negation s <= (r-1)/2 <
 // 2^253, and signed digits need one more bit for the final carry.
 constexpr int MSM_BITS = 254;
@@ -548,10 +551,15 @@ struct ChunkSlots {
 // Point sets sharing one scalar vector (and so one sorted digit list): set s
 // takes the scalars with index i in [lo[s], hi[s]) and the point recs[s][i -
 // lo[s]]; entries outside the range add nothing to that set's buckets.
+// Window tables (pstride != 0): the sorted entries are positions p = w n + i
+// of one bucket space over all windows (n = pstride), and recs[s] holds the
+// window multiples 2^(shift of w) P: row w (tstride[s] records) per window.
 constexpr int MSM_SETS = 3;
 struct BaseSets {
   const uint4* recs[MSM_SETS];
   uint32_t lo[MSM_SETS], hi[MSM_SETS];
+  uint32_t pstride;
+  uint32_t tstride[MSM_SETS];
 };
 
 // Record load into the accumulation's registers: G1 the whole record, G2
@@ -587,7 +595,7 @@ __device__ __forceinline__ bool load_rec_lanes(const uint4* __restrict__ recs, u
 // sit in a few windows (small witness values fill the low ones); in chunk
 // order those windows' waves would land on a fraction of the CUs, scattered
 // they spread over all of them.
-template <class F>
+template <class F, bool TAB>
 __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(sizeof(F) == sizeof(fq) ? 4 : ZK_MSM_G2_ACC_WAVES))) void k_msm_accumulate(const uint2* __restrict__ sorted, BaseSets sets,
                                                         const uint32_t* __restrict__ start,
                                                         const uint32_t* __restrict__ end,
@@ -607,6 +615,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(sizeof(F) =
   const uint32_t set = blockIdx.y;
   const uint4* __restrict__ recs = sets.recs[set];
   const uint32_t ilo = sets.lo[set], ilen = sets.hi[set] - ilo;
+  const uint32_t pstride = sets.pstride, tstride = sets.tstride[set];
   buckets += set * nbuckets;
   const ChunkSlots<F> slots = all_slots.at(set, nchunks);
   const uint32_t w = ch / chunks_per_window;
@@ -635,9 +644,14 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(sizeof(F) =
         empty = true;
       }
       const uint32_t v = e.y;
-      const uint32_t i = (v & 0x7fffffffu) - ilo;  // wraps below lo
+      uint32_t i = (v & 0x7fffffffu), row = 0;
+      if constexpr (TAB) {
+        row = i / pstride;
+        i -= row * pstride;
+      }
+      i -= ilo;  // wraps below lo
       R x, y;
-      if (i < ilen && !load_rec_lanes(recs, i, x, y)) {
+      if (i < ilen && !load_rec_lanes(recs, row * tstride + i, x, y)) {
         if (v >> 31) y = fneg(y);
         if (empty) {
           xyzz_set_affine(acc, x, y);
@@ -842,9 +856,11 @@ __device__ __forceinline__ xyzz<R> shfl_down_pt(const xyzz<R>& p, int lanes) {
 //                   = sum_k [SR_k + K (P_k - RUN_k)],  SR_k = sum_{k' >= k} RUN_k'.
 // Wave 1 forms K (P_k - RUN_k) (log2 K doublings) while wave 0 forms the
 // suffix sums with lane shuffles; wave 0 then adds them and sums the items.
+// plain (when not null) gets the window's plain bucket sum SR_0.
 template <class F, class LN>
 __global__ __launch_bounds__(128) void k_msm_reduce2(const xyzz<F>* __restrict__ P, const xyzz<F>* __restrict__ RUN,
-                                                     uint32_t K, int log2k, xyzz<F>* __restrict__ out) {
+                                                     uint32_t K, int log2k, xyzz<F>* __restrict__ out,
+                                                     xyzz<F>* __restrict__ plain) {
   typedef typename LN::R R;
   msm_priority<F>();
   __shared__ xyzz<F> ku[64];
@@ -868,6 +884,7 @@ __global__ __launch_bounds__(128) void k_msm_reduce2(const xyzz<F>* __restrict__
       const xyzz<R> o = shfl_down_pt(v, (int)(d * LN::N));
       if (t + d < K) xyzz_add(v, o);
     }
+    if (plain && t == 0) LN::store(plain[w], v);
   }
   __syncthreads();
   if (wave0) {
@@ -881,7 +898,8 @@ __global__ __launch_bounds__(128) void k_msm_reduce2(const xyzz<F>* __restrict__
 }
 
 // ------------------------------------------------------------------ workspace
-constexpr int MSM_MAX_W = 32;  // windows of the narrowest window (8 bits)
+constexpr int MSM_MAX_W = 32;   // windows of the narrowest window (8 bits)
+constexpr int MSM_PARTS = 192;  // window (or sub-window) partials of one MSM, all sets
 
 struct MsmWorkspace {
   DevBuf recs, dig, hist, tot, lex, bsum, bmax, boff, tmp, sorted, start, end, wstat, buckets, hkey, tkey, hpt, tpt,
@@ -1116,8 +1134,14 @@ static int msm_accumulate(zk_context* ctx, MsmWorkspace& ws, const MsmShape& sh,
   ChunkSlots<F> slots{(uint32_t*)ws.hkey.p, (uint32_t*)ws.tkey.p, (xyzz<F>*)ws.hpt.p, (xyzz<F>*)ws.tpt.p};
   const uint32_t gxl = cdiv((size_t)nchunks * Lanes<F>::N, 256);  // accumulation: Lanes<F>::N lanes per chunk
   const uint32_t nwaves = cdiv((size_t)nchunks * Lanes<F>::N, 64);
-  ZK_LAUNCH(ctx, st, "msm_accumulate", k_msm_accumulate<F>, dim3(gxl, nsets), dim3(256), 0, sorted, sets, start, end,
-            wstat, nchunks, ap.cpw, sh.n_pad, L0, nbuckets, buckets, slots, nwaves, wave_scatter(nwaves));
+  if (sets.pstride)
+    ZK_LAUNCH(ctx, st, "msm_accumulate", (k_msm_accumulate<F, true>), dim3(gxl, nsets), dim3(256), 0, sorted, sets,
+              start, end, wstat, nchunks, ap.cpw, sh.n_pad, L0, nbuckets, buckets, slots, nwaves,
+              wave_scatter(nwaves));
+  else
+    ZK_LAUNCH(ctx, st, "msm_accumulate", (k_msm_accumulate<F, false>), dim3(gxl, nsets), dim3(256), 0, sorted, sets,
+              start, end, wstat, nchunks, ap.cpw, sh.n_pad, L0, nbuckets, buckets, slots, nwaves,
+              wave_scatter(nwaves));
   // The chunk combine and the bucket reduction are chains of dependent
   // additions.  Few of their waves are busy at once (the combine's active
   // chunks are the spanning runs), so they deal each point operation to two
@@ -1151,13 +1175,15 @@ static int msm_accumulate(zk_context* ctx, MsmWorkspace& ws, const MsmShape& sh,
   return ZK_OK;
 }
 
-// Bucket reduction of every window of every set (level 1: T threads x G
-// buckets per group, level 2 per window); the window sums (set-major) are
-// copied to the pinned ws.h_parts on st.
+// Bucket reduction of Wr windows of Br buckets per set (level 1: T threads
+// x G buckets per group, level 2 per window); the window sums sum_b (b+1) S_b
+// (set-major) are copied to the pinned ws.h_parts on st, followed, with
+// `plain`, by the windows' plain sums sum_b S_b.
 template <class F>
-static int msm_reduce(zk_context* ctx, MsmWorkspace& ws, const MsmShape& sh, int nsets, bool beside, hipStream_t st) {
+static int msm_reduce(zk_context* ctx, MsmWorkspace& ws, int Wr, uint32_t Br, int nsets, bool beside, bool plain,
+                      hipStream_t st) {
   typedef SplitLanes<F> SL;
-  const uint32_t B = sh.B;
+  const uint32_t B = Br;
   // items per workgroup (a G2 item is a lane pair: 256 lanes either way)
   constexpr int TMAX = sizeof(F) == sizeof(fq) ? 256 : 128;
   constexpr int KMAX = 64 / Lanes<F>::N;  // level 2 holds the K groups of a window in one wave
@@ -1170,7 +1196,7 @@ static int msm_reduce(zk_context* ctx, MsmWorkspace& ws, const MsmShape& sh, int
   // sooner: proofs 3-5% shorter that way).  At 2^15 buckets per window and
   // one wave per SIMD splitting lost (G1 2^20: 0.28 -> 0.31 ms), and so did
   // G = 4 there (0.37 ms).
-  const bool split1 = (size_t)sh.W * nsets * B / 4 * Lanes<F>::N <= (size_t)512 * 64;
+  const bool split1 = (size_t)Wr * nsets * B / 4 * Lanes<F>::N <= (size_t)512 * 64;
   const bool half1 = split1 && !beside;
   const int TM = half1 ? TMAX / 2 : TMAX;
   // measured: T = TMAX; G = 8 for 2^15 buckets per window, else 4
@@ -1185,25 +1211,27 @@ static int msm_reduce(zk_context* ctx, MsmWorkspace& ws, const MsmShape& sh, int
   }
   if (T1 < 1 || T1 > TM || (T1 & (T1 - 1)) || K < 1 || (size_t)K * ((size_t)T1 << log2g) != B)
     return ctx->fail(ZK_ERR_INVALID, "msm: unsupported reduction shape");
-  const uint32_t WS = (uint32_t)sh.W * nsets;  // windows of all sets
+  const uint32_t WS = (uint32_t)Wr * nsets;  // windows of all sets
+  if (WS > MSM_PARTS) return ctx->fail(ZK_ERR_INVALID, "msm: too many windows");
   ZK_TRY(ctx->ensure(ws.seg, (size_t)K * WS * sizeof(xyzz<F>)));
   ZK_TRY(ctx->ensure(ws.grp, (size_t)K * WS * sizeof(xyzz<F>)));
-  ZK_TRY(ctx->ensure(ws.win, (size_t)WS * sizeof(xyzz<F>)));
+  ZK_TRY(ctx->ensure(ws.win, (size_t)2 * WS * sizeof(xyzz<F>)));
   const xyzz<F>* buckets = (const xyzz<F>*)ws.buckets.p;
   const uint32_t* start = (const uint32_t*)ws.start.p;
   const uint32_t* end = (const uint32_t*)ws.end.p;
   xyzz<F>* Pk = (xyzz<F>*)ws.seg.p;
   xyzz<F>* RUNk = (xyzz<F>*)ws.grp.p;
   xyzz<F>* win = (xyzz<F>*)ws.win.p;
+  xyzz<F>* pln = plain ? win + WS : nullptr;
   if (half1) {
     ZK_LAUNCH(ctx, st, "msm_reduce", (k_msm_reduce1<F, TMAX / 2, SL>), dim3(K * WS), dim3(T1 * SL::N), 0, buckets,
-              start, end, B, K, (uint32_t)sh.W, log2g, Pk, RUNk);
+              start, end, B, K, (uint32_t)Wr, log2g, Pk, RUNk);
   } else if (split1) {
     ZK_LAUNCH(ctx, st, "msm_reduce", (k_msm_reduce1<F, TMAX, SL>), dim3(K * WS), dim3(T1 * SL::N), 0, buckets, start,
-              end, B, K, (uint32_t)sh.W, log2g, Pk, RUNk);
+              end, B, K, (uint32_t)Wr, log2g, Pk, RUNk);
   } else {
     ZK_LAUNCH(ctx, st, "msm_reduce", (k_msm_reduce1<F, TMAX, Lanes<F>>), dim3(K * WS), dim3(T1 * Lanes<F>::N), 0,
-              buckets, start, end, B, K, (uint32_t)sh.W, log2g, Pk, RUNk);
+              buckets, start, end, B, K, (uint32_t)Wr, log2g, Pk, RUNk);
   }
   int log2k = 0;
   while ((1u << log2k) < K) log2k++;
@@ -1211,14 +1239,64 @@ static int msm_reduce(zk_context* ctx, MsmWorkspace& ws, const MsmShape& sh, int
   // beside other MSMs would wait for a CU with room for its two waves); level
   // 2 holds a window's K groups in one wave, split when they fit
   if (K > 1 && K * SL::N <= 64) {
-    ZK_LAUNCH(ctx, st, "msm_reduce2", (k_msm_reduce2<F, SL>), dim3(WS), dim3(128), 0, Pk, RUNk, K, log2k, win);
+    ZK_LAUNCH(ctx, st, "msm_reduce2", (k_msm_reduce2<F, SL>), dim3(WS), dim3(128), 0, Pk, RUNk, K, log2k, win, pln);
   } else if (K > 1) {
-    ZK_LAUNCH(ctx, st, "msm_reduce2", (k_msm_reduce2<F, Lanes<F>>), dim3(WS), dim3(128), 0, Pk, RUNk, K, log2k, win);
+    ZK_LAUNCH(ctx, st, "msm_reduce2", (k_msm_reduce2<F, Lanes<F>>), dim3(WS), dim3(128), 0, Pk, RUNk, K, log2k, win,
+              pln);
   }
   // pinned destination: a copy to pageable memory costs a staged transfer
   // (measured: G1 2^16 MSM 0.535 -> 0.505 ms, the 2^16 proof 1.70 -> 1.62 ms)
   ZK_HIP(ctx, hipMemcpyAsync(ws.h_parts, K > 1 ? win : Pk, (size_t)WS * sizeof(xyzz<F>), hipMemcpyDeviceToHost, st));
+  // with one group per window the plain sum is that group's RUN
+  if (plain)
+    ZK_HIP(ctx, hipMemcpyAsync((xyzz<F>*)ws.h_parts + WS, K > 1 ? pln : RUNk, (size_t)WS * sizeof(xyzz<F>),
+                               hipMemcpyDeviceToHost, st));
   return ZK_OK;
+}
+
+// Window-table MSM: one bucket space split into H sub-windows of 2^log_sub
+// buckets; P[h] = sum_b (b+1) S_{h,b}, R[h] = sum_b S_{h,b} (device XYZZ).
+// The sum over all buckets of (h 2^log_sub + b + 1) S_{h,b} is
+//   sum_h P[h] + 2^log_sub sum_h h R[h],
+// the second sum as running sums from the top sub-window down.
+template <class F>
+static void host_finish_sub(const xyzz<F>* P, const xyzz<F>* R, int H, int log_sub, uint64_t* out) {
+  typedef typename HostSide<F>::E E;
+  typedef zkh::Jac<E> J;
+  const size_t m = 2 * (size_t)H;
+  std::vector<E> X(m), Y(m), ZZ(m), ZZZ(m), prod(m);
+  std::vector<char> inf(m);
+  E acc = E::one();
+  for (size_t i = 0; i < m; i++) {
+    const xyzz<F>& q = i < (size_t)H ? P[i] : R[i - H];
+    X[i] = HostSide<F>::conv(q.x);
+    Y[i] = HostSide<F>::conv(q.y);
+    ZZ[i] = HostSide<F>::conv(q.zz);
+    ZZZ[i] = HostSide<F>::conv(q.zzz);
+    inf[i] = ZZ[i].is_zero();
+    prod[i] = acc;
+    if (!inf[i]) acc = acc * (ZZ[i] * ZZZ[i]);
+  }
+  E inv = acc.inv();
+  std::vector<J> pt(m, J::inf());
+  for (size_t i = m; i-- > 0;) {
+    if (inf[i]) continue;
+    E d = ZZ[i] * ZZZ[i];
+    E di = inv * prod[i];
+    inv = inv * d;
+    pt[i] = J::affine(X[i] * (di * ZZZ[i]), Y[i] * (di * ZZ[i]));
+  }
+  J run = J::inf(), weighted = J::inf(), sum = J::inf();
+  for (int h = H - 1; h >= 1; h--) {
+    run = run.add(pt[H + h]);
+    weighted = weighted.add(run);
+  }
+  for (int k = 0; k < log_sub; k++) weighted = weighted.dbl();
+  for (int h = 0; h < H; h++) sum = sum.add(pt[h]);
+  J r = sum.add(weighted);
+  E ax, ay;
+  r.to_affine(ax, ay);
+  HostSide<F>::out(ax, ay, out);
 }
 
 // MSMs of `nsets` point sets over one scalar vector of n entries (see
@@ -1228,28 +1306,50 @@ static int msm_reduce(zk_context* ctx, MsmWorkspace& ws, const MsmShape& sh, int
 // internal form (see Rec<F>): the workspace's conversion buffer or a proving
 // key's resident queries.  outs[s] receives set s's affine result.
 template <class F>
-static int msm_run_sets(zk_context* ctx, MsmWorkspace& ws, const BaseSets& sets, int nsets, const void* d_scalars,
-                        size_t n, uint64_t* const* outs, hipStream_t st, bool beside = false) {
+static int msm_run_sets(zk_context* ctx, MsmWorkspace& ws, const BaseSets& sets_in, int nsets, const void* d_scalars,
+                        size_t n, uint64_t* const* outs, hipStream_t st, bool beside = false,
+                        const MsmTab* tab = nullptr) {
   constexpr int OUTW = sizeof(F) == sizeof(fq) ? 8 : 16;
   if (nsets < 1 || nsets > MSM_SETS) return ctx->fail(ZK_ERR_INVALID, "msm: 1 to 3 point sets");
   for (int k = 0; k < nsets; k++) memset(outs[k], 0, OUTW * 8);
   if (n == 0) return ZK_OK;
   if (n > MSM_MAX_N) return ctx->fail(ZK_ERR_SIZE, "msm: n above 2^26");
   constexpr bool G2 = sizeof(F) != sizeof(fq);
-  const int c = choose_c(n, G2);
+  BaseSets sets = sets_in;
   MsmShape sh;
-  sh.n = n;
-  sh.W = (MSM_BITS + c - 1) / c;
-  sh.B = 1u << (c - 1);
+  int Wd;  // digit windows
+  if (!tab) {
+    const int c = choose_c(n, G2);
+    Wd = (MSM_BITS + c - 1) / c;
+    sh.n = n;
+    sh.W = Wd;
+    sh.B = 1u << (c - 1);
+    sets.pstride = 0;
+  } else {
+    // one bucket space for the positions w n + i of all windows
+    Wd = tab->W;
+    if (Wd < 1 || Wd > MSM_MAX_W || (size_t)Wd * n > MSM_MAX_N)
+      return ctx->fail(ZK_ERR_INVALID, "msm: window table shape");
+    sh.n = (size_t)Wd * n;
+    sh.W = 1;
+    sh.B = 1u << (window_width(0, Wd) - 1);
+    if (tab->log_sub < 7 || ((size_t)1 << tab->log_sub) > sh.B)
+      return ctx->fail(ZK_ERR_INVALID, "msm: window table sub-window size");
+    sets.pstride = (uint32_t)n;
+  }
   // window regions of the sorted list are padded to the longest chunk, so
   // every chunk length divides them (the length is chosen after the sort's
   // counts are known)
-  sh.n_pad = (uint32_t)((n + MSM_L0 - 1) / MSM_L0 * MSM_L0);
-  sh.S = (uint32_t)std::max<size_t>(1, std::min<size_t>({(size_t)cdiv(256, sh.W), (size_t)64, n / sh.B}));
+  sh.n_pad = (uint32_t)((sh.n + MSM_L0 - 1) / MSM_L0 * MSM_L0);
+  // slices per window: about 256 blocks; each slice at least B points, or,
+  // for the one bucket space of a window table, at least ZK_MSM_TAB_SLICE
+  // (a slice's histogram of B counters is written and scanned once)
+  sh.S = tab ? (uint32_t)std::max<size_t>(1, std::min<size_t>(256, sh.n / ZK_MSM_TAB_SLICE))
+             : (uint32_t)std::max<size_t>(1, std::min<size_t>({(size_t)cdiv(256, sh.W), (size_t)64, sh.n / sh.B}));
   const int W = sh.W;
   if (W > MSM_MAX_W) return ctx->fail(ZK_ERR_INVALID, "msm: too many windows");
   const size_t nbuckets = (size_t)W * sh.B;
-  ZK_TRY(ctx->ensure(ws.dig, (size_t)W * n * 4));
+  ZK_TRY(ctx->ensure(ws.dig, (size_t)W * sh.n * 4));
   ZK_TRY(ctx->ensure(ws.hist, nbuckets * sh.S * 4));
   ZK_TRY(ctx->ensure(ws.tot, nbuckets * 4));
   ZK_TRY(ctx->ensure(ws.lex, nbuckets * 4));
@@ -1264,25 +1364,31 @@ static int msm_run_sets(zk_context* ctx, MsmWorkspace& ws, const BaseSets& sets,
   ZK_TRY(ctx->ensure(ws.buckets, nsets * nbuckets * sizeof(xyzz<F>)));
   if (!ws.h_stat) ZK_HIP(ctx, hipHostMalloc((void**)&ws.h_stat, 2 * MSM_MAX_W * 4, hipHostMallocDefault));
   if (!ws.h_parts)
-    ZK_HIP(ctx, hipHostMalloc(&ws.h_parts, MSM_SETS * MSM_MAX_W * sizeof(xyzz<fq2>), hipHostMallocDefault));
+    ZK_HIP(ctx, hipHostMalloc(&ws.h_parts, 2 * MSM_PARTS * sizeof(xyzz<fq2>), hipHostMallocDefault));
   if (!ws.stat_ready) ZK_HIP(ctx, hipEventCreateWithFlags(&ws.stat_ready, hipEventDisableTiming));
 
   ZK_LAUNCH(ctx, st, "msm_digits", k_msm_digits, dim3(cdiv(n, 256)), dim3(256), 0, (uint32_t*)ws.dig.p,
-            (const uint4*)d_scalars, n, W);
+            (const uint4*)d_scalars, n, Wd);
   ZK_TRY(msm_sort(ctx, ws, sh, st));
   // the windows' entry counts and largest buckets come back while the
   // scatter runs
   ZK_HIP(ctx, hipEventSynchronize(ws.stat_ready));
   const AccPlan ap = plan_accumulation<F>(ws, sh, beside);
   ZK_TRY(msm_accumulate<F>(ctx, ws, sh, sets, nsets, ap, beside, st));
-  ZK_TRY(msm_reduce<F>(ctx, ws, sh, nsets, beside, st));
+  // a window table's bucket space reduces as sub-windows of 2^log_sub buckets
+  const int Wr = tab ? (int)(sh.B >> tab->log_sub) : W;
+  const uint32_t Br = tab ? 1u << tab->log_sub : sh.B;
+  ZK_TRY(msm_reduce<F>(ctx, ws, Wr, Br, nsets, beside, tab != nullptr, st));
   ZK_HIP(ctx, hipStreamSynchronize(st));
   const xyzz<F>* parts = (const xyzz<F>*)ws.h_parts;
   // window combination on the host (W * c doublings per set): one thread per set
   int rc_fin[MSM_SETS] = {ZK_OK, ZK_OK, ZK_OK};
   auto finish = [&](int k) {
     try {
-      host_finish<F>(std::vector<xyzz<F>>(parts + (size_t)k * W, parts + (size_t)(k + 1) * W), W, 1, outs[k]);
+      if (tab)
+        host_finish_sub<F>(parts + (size_t)k * Wr, parts + (size_t)(nsets + k) * Wr, Wr, tab->log_sub, outs[k]);
+      else
+        host_finish<F>(std::vector<xyzz<F>>(parts + (size_t)k * W, parts + (size_t)(k + 1) * W), W, 1, outs[k]);
     } catch (...) {
       rc_fin[k] = ZK_ERR_OOM;
     }
@@ -1345,16 +1451,117 @@ MsmWorkspace* msm_workspace_new() { return new MsmWorkspace(); }
 
 int msm_g1_sets_ws(zk_context* ctx, MsmWorkspace* ws, int nsets, const void* const* recs, const size_t* lo,
                    const size_t* count, const void* d_scalars, size_t n, uint64_t* const* outs, hipStream_t st,
-                   bool beside) {
+                   bool beside, const MsmTab* tab, const size_t* rows) {
   if (!ws || nsets < 1 || nsets > MSM_SETS) return ctx->fail(ZK_ERR_INVALID, "msm: 1 to 3 point sets");
+  if (tab && !rows) return ctx->fail(ZK_ERR_INVALID, "msm: window table without its row length");
   BaseSets sets{};
   for (int k = 0; k < nsets; k++) {
     if (lo[k] + count[k] > n) return ctx->fail(ZK_ERR_INVALID, "msm: point set beyond the scalars");
+    if (tab && count[k] > rows[k]) return ctx->fail(ZK_ERR_INVALID, "msm: point set beyond its window table");
     sets.recs[k] = (const uint4*)recs[k];
     sets.lo[k] = (uint32_t)lo[k];
     sets.hi[k] = (uint32_t)(lo[k] + count[k]);
+    sets.tstride[k] = tab ? (uint32_t)rows[k] : 0u;
   }
-  return msm_run_sets<fq>(ctx, *ws, sets, nsets, d_scalars, n, outs, st, beside);
+  return msm_run_sets<fq>(ctx, *ws, sets, nsets, d_scalars, n, outs, st, beside, tab);
+}
+
+int msm_recs_tab(zk_context* ctx, MsmWorkspace* ws, bool g2, const void* d_table, size_t rows, const MsmTab& tab,
+                 const void* d_scalars, size_t n, uint64_t* out, hipStream_t st, bool beside) {
+  if (!ws) return ctx->fail(ZK_ERR_INVALID, "msm: no workspace");
+  if (n > rows) return ctx->fail(ZK_ERR_INVALID, "msm: more scalars than window table rows");
+  BaseSets sets{};
+  sets.recs[0] = (const uint4*)d_table;
+  sets.lo[0] = 0;
+  sets.hi[0] = (uint32_t)n;
+  sets.tstride[0] = (uint32_t)rows;
+  uint64_t* outs[1] = {out};
+  if (g2) return msm_run_sets<fq2>(ctx, *ws, sets, 1, d_scalars, n, outs, st, beside, &tab);
+  return msm_run_sets<fq>(ctx, *ws, sets, 1, d_scalars, n, outs, st, beside, &tab);
+}
+
+// ------------------------------------------------------------------ window tables
+__device__ __forceinline__ fq coord_canon(const fq& a) { return fcanon(a); }
+__device__ __forceinline__ fq2 coord_canon(const fq2& a) { return fq2{fcanon(a.c0), fcanon(a.c1)}; }
+
+// tmp[w count + j] = 2^(bits of the windows below w) P_j, XYZZ.
+template <class F>
+__global__ void k_msm_tab_double(const uint4* __restrict__ recs, size_t count, int W, xyzz<F>* __restrict__ tmp) {
+  const size_t j = blockIdx.x * (size_t)blockDim.x + threadIdx.x;
+  if (j >= count) return;
+  F x, y;
+  xyzz<F> p;
+  if (load_rec(recs, (uint32_t)j, x, y))
+    xyzz_set_inf(p);
+  else
+    xyzz_set_affine(p, x, y);
+  for (int w = 0; w < W; w++) {
+    tmp[(size_t)w * count + j] = p;
+    if (w + 1 < W)
+      for (int k = 0; k < window_width(w, W); k++) xyzz_dbl(p);
+  }
+}
+
+// XYZZ -> canonical affine records, PER points per thread sharing one inversion.
+template <class F, int PER>
+__global__ void k_msm_tab_affine(const xyzz<F>* __restrict__ tmp, size_t total, uint4* __restrict__ out) {
+  const size_t base = (blockIdx.x * (size_t)blockDim.x + threadIdx.x) * PER;
+  if (base >= total) return;
+  xyzz<F> p[PER];
+  for (int k = 0; k < PER; k++) {
+    if (base + k < total)
+      p[k] = tmp[base + k];
+    else
+      xyzz_set_inf(p[k]);
+  }
+  F x[PER], y[PER];
+  bool inf[PER];
+  xyzz_to_affine_batch<F, PER>(p, x, y, inf);
+  for (int k = 0; k < PER; k++) {
+    if (base + k >= total) continue;
+    if (inf[k]) {
+      fset_zero(x[k]);
+      fset_zero(y[k]);
+    }
+    store_rec(out, base + k, coord_canon(x[k]), coord_canon(y[k]), inf[k]);
+  }
+}
+
+size_t msm_table_bytes(bool g2, size_t count, const MsmTab& t) {
+  return (size_t)t.W * count * (g2 ? Rec<fq2>::WORDS : Rec<fq>::WORDS) * 4;
+}
+
+template <class F>
+static int table_build(zk_context* ctx, const uint4* recs, size_t count, const MsmTab& t, uint4* table,
+                       hipStream_t st) {
+  if (t.W < 1 || t.W > MSM_MAX_W || (size_t)t.W * count > MSM_MAX_N)
+    return ctx->fail(ZK_ERR_INVALID, "msm table: window count");
+  if (count == 0) return ZK_OK;
+  DevBuf tmp;
+  ZK_TRY(ctx->ensure(tmp, (size_t)t.W * count * sizeof(xyzz<F>)));
+  int rc = ZK_OK;
+  {
+    zk::TimingToken tk = ctx->tic("msm_table", st);
+    hipLaunchKernelGGL(k_msm_tab_double<F>, dim3(cdiv(count, 128)), dim3(128), 0, st, recs, count, t.W,
+                       (xyzz<F>*)tmp.p);
+    constexpr int PER = sizeof(F) == sizeof(fq) ? 4 : 2;
+    const size_t total = (size_t)t.W * count;
+    hipLaunchKernelGGL((k_msm_tab_affine<F, PER>), dim3(cdiv(cdiv(total, PER), 128)), dim3(128), 0, st,
+                       (const xyzz<F>*)tmp.p, total, table);
+    if (hipGetLastError() != hipSuccess) rc = ctx->fail(ZK_ERR_HIP, "msm table: launch");
+    ctx->toc(tk, st);
+  }
+  // the temporary goes once the kernels are done
+  if (hipStreamSynchronize(st) != hipSuccess && rc == ZK_OK) rc = ctx->fail(ZK_ERR_HIP, "msm table: build");
+  (void)hipFree(tmp.p);
+  return rc;
+}
+
+int msm_table_build(zk_context* ctx, bool g2, const void* d_recs, size_t count, const MsmTab& t, void* d_table,
+                    hipStream_t st) {
+  if (!d_recs || !d_table) return ctx->fail(ZK_ERR_INVALID, "msm table: null buffer");
+  if (g2) return table_build<fq2>(ctx, (const uint4*)d_recs, count, t, (uint4*)d_table, st);
+  return table_build<fq>(ctx, (const uint4*)d_recs, count, t, (uint4*)d_table, st);
 }
 
 int msm_recs_ws(zk_context* ctx, MsmWorkspace* ws, bool g2, const void* d_recs, const void* d_scalars, size_t n,

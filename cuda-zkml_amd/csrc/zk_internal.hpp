@@ -190,12 +190,29 @@ void msm_workspace_free(MsmWorkspace* ws);
 // and reduction choose their lane layouts for a shared GPU.
 int msm_recs_ws(zk_context* ctx, MsmWorkspace* ws, bool g2, const void* d_recs, const void* d_scalars, size_t n,
                 uint64_t* out_affine, hipStream_t st, bool beside = false);
+// Window tables of fixed bases (proving-key queries): for W digit windows
+// (the widths of the MSM's window split of 254 bits) row w holds 2^(bits of
+// the windows below w) P_j for every point; an MSM over a table has one
+// bucket space for all windows, reduced in sub-windows of 2^log_sub buckets.
+struct MsmTab {
+  int W = 0;
+  int log_sub = 0;
+};
+size_t msm_table_bytes(bool g2, size_t count, const MsmTab& t);
+// Fills d_table (msm_table_bytes) from count point records on st; uses
+// count * W * (point size) bytes of temporary device memory.
+int msm_table_build(zk_context* ctx, bool g2, const void* d_recs, size_t count, const MsmTab& t, void* d_table,
+                    hipStream_t st);
 // G1 MSMs of up to 3 point sets over one scalar vector of n entries, sharing
 // the digit sort and every latency-bound step: set k multiplies recs[k][j] by
-// scalar lo[k] + j for j < count[k]; outs[k] gets its affine result.
+// scalar lo[k] + j for j < count[k]; outs[k] gets its affine result.  With
+// `tab`, recs[k] are window tables of rows[k] >= count[k] points per window.
 int msm_g1_sets_ws(zk_context* ctx, MsmWorkspace* ws, int nsets, const void* const* recs, const size_t* lo,
                    const size_t* count, const void* d_scalars, size_t n, uint64_t* const* outs, hipStream_t st,
-                   bool beside = false);
+                   bool beside = false, const MsmTab* tab = nullptr, const size_t* rows = nullptr);
+// msm_recs_ws over a window table of `rows` points per window (n <= rows).
+int msm_recs_tab(zk_context* ctx, MsmWorkspace* ws, bool g2, const void* d_table, size_t rows, const MsmTab& tab,
+                 const void* d_scalars, size_t n, uint64_t* out_affine, hipStream_t st, bool beside = false);
 
 // ---- fixed base (pointgen.hip)
 int g1_generator_mul(zk_context* ctx, const void* d_scalars, size_t n, void* d_out, hipStream_t st);
