@@ -538,7 +538,10 @@ int zk_quotient_h(zk_context* ctx, const zk_r1cs* c, const void* d_witness, size
 #define ZK_PK_TAB_MIN_LOG 14
 #endif
 #ifndef ZK_PK_TAB_MAX_LOG
-#define ZK_PK_TAB_MAX_LOG 18
+#define ZK_PK_TAB_MAX_LOG 23
+#endif
+#ifndef ZK_PK_TAB_W_HUGE
+#define ZK_PK_TAB_W_HUGE 13
 #endif
 #ifndef ZK_PK_TAB_SUB
 #define ZK_PK_TAB_SUB 10
@@ -558,9 +561,13 @@ int zk_quotient_h(zk_context* ctx, const zk_r1cs* c, const void* d_witness, size
 static MsmTab table_shape(size_t n, int wlarge) {
   MsmTab t;
   if (n < ((size_t)1 << ZK_PK_TAB_MIN_LOG) || n > ((size_t)1 << ZK_PK_TAB_MAX_LOG)) return t;
-  t.W = n >= ((size_t)1 << 15) ? wlarge : 20;
+  const bool huge = n > ((size_t)1 << 18);
+  t.W = huge ? ZK_PK_TAB_W_HUGE : n >= ((size_t)1 << 15) ? wlarge : 20;
+  if ((size_t)t.W * n > MSM_MAX_N) return MsmTab{};  // positions of all windows beyond the sort's range
   const int c = (254 + t.W - 1) / t.W;  // widest window
-  t.log_sub = std::min(ZK_PK_TAB_SUB, c - 1);
+  // above 2^18 scalars: 2^15-bucket sub-windows (the plain MSMs' reduction
+  // shape at 2^20 .. 2^22 points)
+  t.log_sub = std::min(huge ? 15 : ZK_PK_TAB_SUB, c - 1);
   return t;
 }
 

@@ -48,6 +48,7 @@ namespace zk {
 constexpr uint32_t KEY_INVALID = 0xffffffffu;
 constexpr int MSM_L0 = 64;         // sorted entries per accumulation thread (largest)
 constexpr int MSM_CMAX = 16;       // widest window: 2^15 LDS counters (128 KB)
+constexpr uint32_t MSM_LDS_B = 32768;  // most buckets a window's slice histogram holds in LDS
 constexpr int SORT_T = 1024;       // threads of the histogram / scatter blocks
 constexpr int SORT_U = 8;          // loads in flight per thread in the sort passes
 constexpr int SCAN_T = 128;        // buckets per column-scan block (<= the smallest B)
@@ -529,6 +530,227 @@ __global__ __launch_bounds__(PLACE_T) void k_msm_place(const uint2* __restrict__
       if (agg[u]) pos[u] = __builtin_amdgcn_readfirstlane(pos[u]) + rank[u];
       if (e[u].x != KEY_INVALID) out[pos[u]] = e[u];
     }
+  }
+}
+
+// ------------------------------------------------------------------ wide sort
+// One bucket space of B = 2^b > 2^15 buckets (window tables with windows of
+// more than 16 bits): too many counters for a slice histogram in LDS, so the
+// entries go first to NB = 1024 coarse bins of BPC = B / NB consecutive
+// buckets (slice histograms of NB counters), then each bin is counted,
+// scanned and placed by one block with BPC counters in LDS (measured on the
+// 2^22 proof: 256 bins of 2048 buckets placed 1.7 ms per MSM).
+constexpr int WIDE_NB = 1024;
+constexpr int WIDE_LOG_NB = 10;
+
+// The lanes of a wave that share `key` take their positions with one atomic
+// when all active lanes hold the same key (a hot bucket or bin), else one
+// atomic each; returns this lane's position.  KEY_INVALID lanes take none.
+__device__ __forceinline__ uint32_t wave_claim(uint32_t* ctr, uint32_t key, uint32_t idx) {
+  const uint32_t lead = __builtin_amdgcn_readfirstlane(key);
+  const uint64_t same = __ballot(key == lead);
+  uint32_t pos = 0;
+  if (same == __ballot(1) && lead != KEY_INVALID) {
+    const uint32_t rank = __builtin_amdgcn_mbcnt_hi((uint32_t)(same >> 32), __builtin_amdgcn_mbcnt_lo((uint32_t)same, 0u));
+    if (rank == 0) pos = atomicAdd(&ctr[idx], (uint32_t)__popcll(same));
+    pos = __builtin_amdgcn_readfirstlane(pos) + rank;
+  } else if (key != KEY_INVALID) {
+    pos = atomicAdd(&ctr[idx], 1u);
+  }
+  return pos;
+}
+
+// Pass 1a: coarse-bin counts of slice s -> cnt[bin * S + s].
+__global__ __launch_bounds__(SORT_T) void k_wide_count(const uint32_t* __restrict__ dig, size_t np, uint32_t slice,
+                                                      uint32_t S, uint32_t shift, uint32_t* __restrict__ cnt) {
+  msm_short_priority();
+  __shared__ uint32_t h[WIDE_NB];
+  const uint32_t s = blockIdx.x, t = threadIdx.x;
+  for (uint32_t i = t; i < WIDE_NB; i += SORT_T) h[i] = 0;
+  __syncthreads();
+  const size_t lo = (size_t)s * slice, hi = min(np, lo + slice);
+  for (size_t p0 = lo + t; p0 < hi; p0 += (size_t)SORT_T * SORT_U) {
+    uint32_t v[SORT_U];
+#pragma unroll
+    for (int u = 0; u < SORT_U; u++) {
+      const size_t p = p0 + (size_t)u * SORT_T;
+      v[u] = p < hi ? dig[p] & 0x7fffffffu : 0u;
+    }
+#pragma unroll
+    for (int u = 0; u < SORT_U; u++) {
+      const uint32_t bin = v[u] ? (v[u] - 1) >> shift : KEY_INVALID;
+      (void)wave_claim(h, bin, bin == KEY_INVALID ? 0 : bin);
+    }
+  }
+  __syncthreads();
+  for (uint32_t i = t; i < WIDE_NB; i += SORT_T) cnt[(size_t)i * S + s] = h[i];
+}
+
+// Pass 1b: per coarse bin (block of 256 threads, up to 4 slices each),
+// cnt[bin * S + s] becomes the exclusive prefix over the bin's slices and
+// bintot[bin] its entry count.
+__global__ __launch_bounds__(256) void k_wide_scan_rows(uint32_t* __restrict__ cnt, uint32_t S,
+                                                      uint32_t* __restrict__ bintot) {
+  msm_short_priority();
+  __shared__ uint32_t wsum[4];
+  const uint32_t t = threadIdx.x, lane = t & 63, wv = t >> 6;
+  uint32_t* row = cnt + (size_t)blockIdx.x * S;
+  const uint32_t PER = (S + 255) / 256;  // S <= 1024
+  const uint32_t s0 = min(t * PER, S), s1 = min(s0 + PER, S);
+  uint32_t v[4], sum = 0;
+  for (uint32_t i = 0; i < 4; i++) {
+    v[i] = s0 + i < s1 ? row[s0 + i] : 0u;
+    sum += v[i];
+  }
+  uint32_t inc = sum;
+  for (int off = 1; off < 64; off <<= 1) {
+    const uint32_t o = (uint32_t)__shfl_up((int)inc, off);
+    if (lane >= (uint32_t)off) inc += o;
+  }
+  if (lane == 63) wsum[wv] = inc;
+  __syncthreads();
+  uint32_t base = 0, all = 0;
+#pragma unroll
+  for (int k = 0; k < 4; k++) {
+    if ((uint32_t)k < wv) base += wsum[k];
+    all += wsum[k];
+  }
+  base += inc - sum;
+  for (uint32_t i = 0; i < 4; i++) {
+    if (s0 + i < s1) row[s0 + i] = base;
+    base += v[i];
+  }
+  if (t == 0) bintot[blockIdx.x] = all;
+}
+
+// Pass 1c (one block, a thread per bin): binoff[bin] = the bin's first entry,
+// binoff[NB] = the entry count (also wstat[0]; wstat[1] = 0 for the
+// placement's maximum).
+__global__ __launch_bounds__(WIDE_NB) void k_wide_scan_bins(const uint32_t* __restrict__ bintot,
+                                                          uint32_t* __restrict__ binoff, uint32_t* __restrict__ wstat) {
+  msm_short_priority();
+  __shared__ uint32_t wsum[WIDE_NB / 64];
+  const uint32_t b = threadIdx.x, lane = b & 63, wv = b >> 6;
+  const uint32_t tot = bintot[b];
+  uint32_t inc = tot;
+  for (int off = 1; off < 64; off <<= 1) {
+    const uint32_t o = (uint32_t)__shfl_up((int)inc, off);
+    if (lane >= (uint32_t)off) inc += o;
+  }
+  if (lane == 63) wsum[wv] = inc;
+  __syncthreads();
+  uint32_t base = 0, all = 0;
+#pragma unroll
+  for (int v = 0; v < WIDE_NB / 64; v++) {
+    if ((uint32_t)v < wv) base += wsum[v];
+    all += wsum[v];
+  }
+  binoff[b] = base + inc - tot;
+  if (b == 0) {
+    binoff[WIDE_NB] = all;
+    wstat[0] = all;
+    wstat[1] = 0;
+  }
+}
+
+// Pass 1d: slice s's entries to their coarse bins: tmp[pos] = (bucket, p | sign).
+__global__ __launch_bounds__(SORT_T) void k_wide_scatter(const uint32_t* __restrict__ dig, size_t np, uint32_t slice,
+                                                        uint32_t S, uint32_t shift, const uint32_t* __restrict__ cnt,
+                                                        const uint32_t* __restrict__ binoff, uint2* __restrict__ tmp) {
+  msm_short_priority();
+  __shared__ uint32_t cur[WIDE_NB];
+  const uint32_t s = blockIdx.x, t = threadIdx.x;
+  for (uint32_t i = t; i < WIDE_NB; i += SORT_T) cur[i] = binoff[i] + cnt[(size_t)i * S + s];
+  __syncthreads();
+  const size_t lo = (size_t)s * slice, hi = min(np, lo + slice);
+  for (size_t p0 = lo + t; p0 < hi; p0 += (size_t)SORT_T * SORT_U) {
+    uint32_t v[SORT_U];
+#pragma unroll
+    for (int u = 0; u < SORT_U; u++) {
+      const size_t p = p0 + (size_t)u * SORT_T;
+      v[u] = p < hi ? dig[p] : 0u;
+    }
+#pragma unroll
+    for (int u = 0; u < SORT_U; u++) {
+      const uint32_t m = v[u] & 0x7fffffffu;
+      const uint32_t bin = m ? (m - 1) >> shift : KEY_INVALID;
+      const uint32_t pos = wave_claim(cur, bin, bin == KEY_INVALID ? 0 : bin);
+      if (m) tmp[pos] = make_uint2(m - 1, (uint32_t)(p0 + (size_t)u * SORT_T) | (v[u] & 0x80000000u));
+    }
+  }
+}
+
+// Pass 2 (block per coarse bin, 2^shift buckets): LDS counts, their scan
+// (bucket bounds start/end; the largest bucket into wstat[1]), placement.
+__global__ __launch_bounds__(PLACE_T) void k_wide_place(const uint2* __restrict__ tmp,
+                                                       const uint32_t* __restrict__ binoff, uint32_t shift,
+                                                       uint32_t* __restrict__ start, uint32_t* __restrict__ end,
+                                                       uint2* __restrict__ out, uint32_t* __restrict__ wstat) {
+  msm_short_priority();
+  extern __shared__ uint32_t cur[];  // 2^shift counters, then cursors
+  __shared__ uint32_t wsum[PLACE_T / 64], wmx[PLACE_T / 64];
+  const uint32_t cb = blockIdx.x, t = threadIdx.x, lane = t & 63, wv = t >> 6;
+  const uint32_t BPC = 1u << shift, k0 = cb << shift;
+  const uint32_t lo = binoff[cb], hi = binoff[cb + 1];
+  for (uint32_t j = t; j < BPC; j += PLACE_T) cur[j] = 0;
+  __syncthreads();
+  for (uint32_t p0 = lo + t; p0 < hi; p0 += PLACE_T * SORT_U) {
+    uint32_t key[SORT_U];
+#pragma unroll
+    for (int u = 0; u < SORT_U; u++) {
+      const uint32_t p = p0 + u * PLACE_T;
+      key[u] = p < hi ? tmp[p].x : KEY_INVALID;
+    }
+#pragma unroll
+    for (int u = 0; u < SORT_U; u++) (void)wave_claim(cur, key[u], key[u] == KEY_INVALID ? 0 : key[u] - k0);
+  }
+  __syncthreads();
+  // exclusive scan: thread t owns counters [t PER, t PER + PER)
+  const uint32_t PER = (BPC + PLACE_T - 1) / PLACE_T;
+  const uint32_t j0 = min(t * PER, BPC), j1 = min(j0 + PER, BPC);
+  uint32_t sum = 0, mx = 0;
+  for (uint32_t j = j0; j < j1; j++) {
+    sum += cur[j];
+    mx = max(mx, cur[j]);
+  }
+  uint32_t inc = sum;
+  for (int off = 1; off < 64; off <<= 1) {
+    const uint32_t o = (uint32_t)__shfl_up((int)inc, off);
+    if (lane >= (uint32_t)off) inc += o;
+  }
+  for (int off = 32; off >= 1; off >>= 1) mx = max(mx, (uint32_t)__shfl_xor((int)mx, off));
+  if (lane == 63) wsum[wv] = inc;
+  if (lane == 0) wmx[wv] = mx;
+  __syncthreads();
+  uint32_t base = lo, m = 0;
+#pragma unroll
+  for (int v = 0; v < PLACE_T / 64; v++) {
+    if ((uint32_t)v < wv) base += wsum[v];
+    m = max(m, wmx[v]);
+  }
+  base += inc - sum;
+  for (uint32_t j = j0; j < j1; j++) {
+    const uint32_t c = cur[j];
+    start[k0 + j] = base;
+    end[k0 + j] = base + c;
+    cur[j] = base;
+    base += c;
+  }
+  if (t == 0 && m) atomicMax(&wstat[1], m);
+  __syncthreads();
+  for (uint32_t p0 = lo + t; p0 < hi; p0 += PLACE_T * SORT_U) {
+    uint2 e[SORT_U];
+#pragma unroll
+    for (int u = 0; u < SORT_U; u++) {
+      const uint32_t p = p0 + u * PLACE_T;
+      e[u] = p < hi ? tmp[p] : make_uint2(KEY_INVALID, 0u);
+    }
+    uint32_t pos[SORT_U];
+#pragma unroll
+    for (int u = 0; u < SORT_U; u++) pos[u] = wave_claim(cur, e[u].x, e[u].x == KEY_INVALID ? 0 : e[u].x - k0);
+#pragma unroll
+    for (int u = 0; u < SORT_U; u++)
+      if (e[u].x != KEY_INVALID) out[pos[u]] = e[u];
   }
 }
 
@@ -1030,7 +1252,10 @@ struct MsmShape {
 // Counting sort of all windows on st.  The windows' entry counts and largest
 // buckets are copied to ws.h_stat, and ws.stat_ready is recorded after the
 // copy (the scatter is still running then).
+static int msm_sort_wide(zk_context* ctx, MsmWorkspace& ws, const MsmShape& sh, hipStream_t st);
+
 static int msm_sort(zk_context* ctx, MsmWorkspace& ws, const MsmShape& sh, hipStream_t st) {
+  if (sh.B > MSM_LDS_B) return msm_sort_wide(ctx, ws, sh, st);
   const size_t n = sh.n;
   const int W = sh.W;
   const uint32_t B = sh.B, n_pad = sh.n_pad, S = sh.S, nb = B / SCAN_T;  // nb: column-scan blocks per window
@@ -1067,6 +1292,40 @@ static int msm_sort(zk_context* ctx, MsmWorkspace& ws, const MsmShape& sh, hipSt
     ZK_LAUNCH(ctx, st, "msm_place", k_msm_place, dim3(MSM_NCB, W), dim3(PLACE_T), 0, tmp, B, BPC, start, end,
               sorted);
   }
+  return ZK_OK;
+}
+
+// The sort of one wide bucket space (window tables, B > 2^15) on st: coarse
+// bins, then per-bin counting and placement; the entry count and largest
+// bucket come back after the placement.
+static int msm_sort_wide(zk_context* ctx, MsmWorkspace& ws, const MsmShape& sh, hipStream_t st) {
+  if (sh.W != 1) return ctx->fail(ZK_ERR_INVALID, "msm: wide sort of several windows");
+  int b = 0;
+  while ((1u << b) < sh.B) b++;
+  const uint32_t shift = (uint32_t)(b - WIDE_LOG_NB);  // log2 of the buckets per coarse bin
+  if ((1u << b) != sh.B || b <= WIDE_LOG_NB || shift > 13)
+    return ctx->fail(ZK_ERR_INVALID, "msm: wide sort bucket count");
+  const size_t np = sh.n;
+  const uint32_t S = (uint32_t)std::max<size_t>(1, std::min<size_t>(1024, cdiv(np, 32768)));
+  const uint32_t slice = (uint32_t)cdiv(np, S);
+  ZK_TRY(ctx->ensure(ws.hist, (size_t)WIDE_NB * S * 4));
+  ZK_TRY(ctx->ensure(ws.boff, (size_t)(WIDE_NB + 1) * 4));
+  ZK_TRY(ctx->ensure(ws.bsum, (size_t)WIDE_NB * 4));
+  const uint32_t* dig = (const uint32_t*)ws.dig.p;
+  uint32_t* cnt = (uint32_t*)ws.hist.p;
+  uint32_t* binoff = (uint32_t*)ws.boff.p;
+  uint32_t* bintot = (uint32_t*)ws.bsum.p;
+  uint32_t* wstat = (uint32_t*)ws.wstat.p;
+  uint2* tmp = (uint2*)ws.tmp.p;
+  ZK_LAUNCH(ctx, st, "msm_hist", k_wide_count, dim3(S), dim3(SORT_T), 0, dig, np, slice, S, shift, cnt);
+  ZK_LAUNCH(ctx, st, "msm_scan", k_wide_scan_rows, dim3(WIDE_NB), dim3(256), 0, cnt, S, bintot);
+  ZK_LAUNCH(ctx, st, "msm_scan", k_wide_scan_bins, dim3(1), dim3(WIDE_NB), 0, bintot, binoff, wstat);
+  ZK_LAUNCH(ctx, st, "msm_scatter", k_wide_scatter, dim3(S), dim3(SORT_T), 0, dig, np, slice, S, shift, cnt, binoff,
+            tmp);
+  ZK_LAUNCH(ctx, st, "msm_place", k_wide_place, dim3(WIDE_NB), dim3(PLACE_T), (size_t)4 << shift, tmp, binoff,
+            shift, (uint32_t*)ws.start.p, (uint32_t*)ws.end.p, (uint2*)ws.sorted.p, wstat);
+  ZK_HIP(ctx, hipMemcpyAsync(ws.h_stat, wstat, 8, hipMemcpyDeviceToHost, st));
+  ZK_HIP(ctx, hipEventRecord(ws.stat_ready, st));
   return ZK_OK;
 }
 
