@@ -556,9 +556,15 @@ int zk_quotient_h(zk_context* ctx, const zk_r1cs* c, const void* d_witness, size
 #define ZK_PK_TAB_W_LARGE_H 20
 #endif
 
+// H's sub-windows: 2^8 buckets, level 1 one bucket per thread (H sorts and
+// reduces after the quotient, on the 2^16 proof's critical path: its reduction
+// 4 -> 16 workgroups, H 0.70 -> 0.66 ms)
+#ifndef ZK_PK_TAB_SUB_H
+#define ZK_PK_TAB_SUB_H 8
+#endif
 // Table shape for MSMs of n scalars (W = 0: no table); wlarge: windows from
-// 2^15 scalars on.
-static MsmTab table_shape(size_t n, int wlarge) {
+// 2^15 scalars on; sub: log2 of the sub-window size up to 2^18 scalars.
+static MsmTab table_shape(size_t n, int wlarge, int sub = ZK_PK_TAB_SUB) {
   MsmTab t;
   if (n < ((size_t)1 << ZK_PK_TAB_MIN_LOG) || n > ((size_t)1 << ZK_PK_TAB_MAX_LOG)) return t;
   const bool huge = n > ((size_t)1 << 18);
@@ -567,7 +573,7 @@ static MsmTab table_shape(size_t n, int wlarge) {
   const int c = (254 + t.W - 1) / t.W;  // widest window
   // above 2^18 scalars: 2^15-bucket sub-windows (the plain MSMs' reduction
   // shape at 2^20 .. 2^22 points)
-  t.log_sub = std::min(huge ? 15 : ZK_PK_TAB_SUB, c - 1);
+  t.log_sub = std::min(huge ? 15 : sub, c - 1);
   return t;
 }
 
@@ -584,7 +590,7 @@ static int pk_table(zk_context* ctx, bool g2, const void* recs, size_t count, co
 static int pk_tables(zk_context* ctx, zk_pk* pk) {
   pk->tab_w = table_shape((size_t)pk->m, ZK_PK_TAB_W_LARGE);
   pk->tab_b2 = table_shape((size_t)pk->m, ZK_PK_TAB_W_LARGE_B2);
-  pk->tab_h = table_shape((size_t)pk->n, ZK_PK_TAB_W_LARGE_H);
+  pk->tab_h = table_shape((size_t)pk->n, ZK_PK_TAB_W_LARGE_H, ZK_PK_TAB_SUB_H);
   if (pk->tab_w.W) {
     ZK_TRY(pk_table(ctx, false, pk->A, pk->nA, pk->tab_w, &pk->tA));
     ZK_TRY(pk_table(ctx, false, pk->B1, pk->nB1, pk->tab_w, &pk->tB1));
@@ -684,6 +690,12 @@ static int zk_prove_impl(zk_context* ctx, const zk_pk* pk, const zk_r1cs* c, con
   // events: 0 start, 1 witness resident, 2 quotient done, 3 end,
   // 4 + 2j / 5 + 2j start / end of MSM job j
   constexpr int NEV = 4 + 2 * ZK_JOBS;
+// From a 2^21 domain on, the three-set G1 job holds its accumulation until
+// the quotient is done: the quotient's transforms then get the CU slots
+// they wait for beside the accumulations (2^22 proof 45.9 -> 45.0 ms).  At
+// 2^16 every such gate lost (1.42 ms -> 1.53 ms gating the G1 job, 1.70 ms
+// gating B2, 1.69 ms both).
+constexpr size_t GATE_G1_MIN_N = (size_t)1 << 21;
   hipEvent_t ev[NEV];
   for (auto& e : ev) ZK_HIP(ctx, hipEventCreate(&e));
   struct EvGuard {
@@ -710,6 +722,23 @@ static int zk_prove_impl(zk_context* ctx, const zk_pk* pk, const zk_r1cs* c, con
     if (!ctx->job_stream[j]) ZK_HIP(ctx, hipStreamCreateWithFlags(&ctx->job_stream[j], hipStreamNonBlocking));
   for (int j = 0; j < ZK_JOBS; j++)
     if (!ctx->job_ws[j]) ctx->job_ws[j] = msm_workspace_new();
+  // The quotient gate: jobs set here hold their accumulation until the
+  // quotient is done, so that its transforms find CU slots.
+  MsmGate quotient_done;
+  quotient_done.ev = ev[2];
+  struct GateUnset {  // after the jobs are joined: the gate lives on this stack
+    zk_context* ctx;
+    ~GateUnset() {
+      for (int j = 0; j < ZK_JOBS; j++) msm_workspace_gate(ctx->job_ws[j], nullptr);
+    }
+  } gate_unset{ctx};
+  struct GateRelease {  // before the jobs are joined, on every way out: no waiter is left waiting
+    MsmGate& g;
+    ~GateRelease() {
+      int pending = 0;
+      g.state.compare_exchange_strong(pending, 2);
+    }
+  };
   uint8_t* base = (uint8_t*)ctx->scratch_c.p;
   void* d_h = base;
   void* d_w = base + n * 32;
@@ -810,8 +839,10 @@ static int zk_prove_impl(zk_context* ctx, const zk_pk* pk, const zk_r1cs* c, con
     };
   };
   const std::function<void()> f_b2(run_b2), f_g1(run_g1), f_pre(precompute);
+  if (n >= GATE_G1_MIN_N) msm_workspace_gate(ctx->job_ws[JOB_G1], &quotient_done);
   std::vector<std::thread> workers;
   ThreadJoiner joiner{workers};
+  GateRelease gate_release{quotient_done};
   const std::function<void()> jobs[3] = {job(f_b2, rc_b2), job(f_g1, rc_g1), job(f_pre, rc_pre)};
   for (const std::function<void()>& fn : jobs) {
     try {
@@ -830,6 +861,7 @@ static int zk_prove_impl(zk_context* ctx, const zk_pk* pk, const zk_r1cs* c, con
       qrc = ctx->fail(ZK_ERR_HIP, "prove: witness check read-back");
   }
   if (qrc == ZK_OK && hipEventRecord(ev[2], st) != hipSuccess) qrc = ctx->fail(ZK_ERR_HIP, "prove: event record");
+  quotient_done.state.store(qrc == ZK_OK ? 1 : 2);
   if (qrc == ZK_OK) {  // H after the quotient, same stream
     record(4 + 2 * JOB_H, st, rc_h);
     if (rc_h == ZK_OK && nh && pk->tH)

@@ -1129,7 +1129,10 @@ struct MsmWorkspace {
   uint32_t* h_stat = nullptr;  // pinned, 2 words per window
   void* h_parts = nullptr;     // pinned, the per-window partials of every set
   hipEvent_t stat_ready = nullptr;
+  MsmGate* gate = nullptr;  // waited for before the accumulation
 };
+
+void msm_workspace_gate(MsmWorkspace* ws, MsmGate* wait_before_accumulate) { ws->gate = wait_before_accumulate; }
 
 void msm_workspace_free(MsmWorkspace* ws) {
   if (!ws) return;
@@ -1633,6 +1636,11 @@ static int msm_run_sets(zk_context* ctx, MsmWorkspace& ws, const BaseSets& sets_
   // scatter runs
   ZK_HIP(ctx, hipEventSynchronize(ws.stat_ready));
   const AccPlan ap = plan_accumulation<F>(ws, sh, beside);
+  if (ws.gate) {
+    int gs;
+    while ((gs = ws.gate->state.load()) == 0) std::this_thread::yield();
+    if (gs == 1) ZK_HIP(ctx, hipStreamWaitEvent(st, ws.gate->ev, 0));
+  }
   ZK_TRY(msm_accumulate<F>(ctx, ws, sh, sets, nsets, ap, beside, st));
   // a window table's bucket space reduces as sub-windows of 2^log_sub buckets
   const int Wr = tab ? (int)(sh.B >> tab->log_sub) : W;

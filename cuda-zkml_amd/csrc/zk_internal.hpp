@@ -4,6 +4,7 @@
 #include <stdint.h>
 #include <stdio.h>
 
+#include <atomic>
 #include <map>
 #include <memory>
 #include <mutex>
@@ -183,6 +184,17 @@ int recs_from_std(zk_context* ctx, bool g2, void* d_recs, const void* d_std, con
 size_t rec_bytes(bool g2);
 MsmWorkspace* msm_workspace_new();
 void msm_workspace_free(MsmWorkspace* ws);
+// Holds an MSM's accumulation until another stream's work is done (MSMs of
+// one proof on different streams and host threads): the signalling thread
+// records `ev` and then sets state 1, or sets 2 when it records nothing; the
+// MSM waits on the host for a nonzero state and, for 1, makes its stream
+// wait for `ev` before the accumulation.
+struct MsmGate {
+  std::atomic<int> state{0};
+  hipEvent_t ev = nullptr;
+};
+// Gate of a workspace's next MSMs (null: none).
+void msm_workspace_gate(MsmWorkspace* ws, MsmGate* wait_before_accumulate);
 // MSM over records with an explicit workspace (one per concurrent caller).
 // beside: the MSM shares the GPU with other kernels (a proof); a G1 MSM then
 // gives each accumulation thread half as many entries, so its waves free CU
