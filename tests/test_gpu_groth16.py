@@ -182,6 +182,34 @@ def test_prove_2_16_matches_oracle(ctx, tmp_path):
         assert ref().ref_verify_files(str(vk_path).encode(), str(pf).encode(), str(pub).encode()) == 1
 
 
+@pytest.mark.parametrize("nc", [(1 << 14) - 8, (1 << 18) - 64, (1 << 18) + 64])
+def test_prove_window_table_shapes(ctx, tmp_path, nc):
+    """Proofs whose MSMs run on the proving key's window tables at each shape
+    boundary (m = nc + 21 variables): 2^14..2^15 (20 windows of 13 bits for
+    every query, a 2^14 domain),
+    up to 2^18 (16-bit windows for the witness sets, 13-bit for B2 and H;
+    sub-windows of 2^10 and 2^8 buckets) and just above 2^18 (13 windows of
+    19-20 bits through the two-level wide sort, 2^15-bucket sub-windows).
+    Byte-identical to the oracle's prove on the same key and seed."""
+    import zkml_amd
+    npub = 4
+    A, B, C, w = zkml_amd.synthetic_r1cs(nc, npub, 16, nc % 97)
+    r = ctx.r1cs(nc, w.shape[0], npub, A, B, C)
+    pk_path, vk_path = tmp_path / "pk.bin", tmp_path / "vk.bin"
+    print(f"[prove tables] nc={nc} m={w.shape[0]} domain 2^{r.log_n}", flush=True)
+    ctx.setup(r, SETUP_SEED, pk_path, vk_path)
+    pk = ctx.load_pk(pk_path)
+    proof, _ = ctx.prove(pk, r, w, npub, PROVE_SEED)
+    oc = _oracle_of(A, B, C, nc, w.shape[0], npub)
+    rc, proof_o, _ = oc.prove(str(pk_path), w, PROVE_SEED, threads=16)
+    assert rc == 0 and proof == proof_o
+    pub = [Z.from_mont(Z.from_limbs([int(x) for x in w[1 + i]]), Z.R) for i in range(npub)]
+    pub_words = np.array([Z.limbs(v) for v in pub], dtype=np.uint64)
+    assert zkml_amd.verify(vk_path.read_bytes(), proof, pub_words)
+    pk.close()
+    r.close()
+
+
 def _oracle_of(A, B, C, nc, nv, npub):
     mats = [(M["row"], M["col"], np.ascontiguousarray(M["value"])) for M in (A, B, C)]
     return OracleR1CS(nc, nv, npub, nv - 1 - npub, mats)
