@@ -587,7 +587,15 @@ static int pk_table(zk_context* ctx, bool g2, const void* recs, size_t count, co
   return msm_table_build(ctx, g2, recs, count, t, *out, ctx->stream);
 }
 
-static int pk_tables(zk_context* ctx, zk_pk* pk) {
+// Frees a key's window tables: its MSMs then run over the query records.
+static void pk_drop_tables(zk_pk* pk) {
+  for (void** t : {&pk->tA, &pk->tB1, &pk->tB2, &pk->tL, &pk->tH}) {
+    if (*t) (void)hipFree(*t);
+    *t = nullptr;
+  }
+}
+
+static int pk_tables_build(zk_context* ctx, zk_pk* pk) {
   pk->tab_w = table_shape((size_t)pk->m, ZK_PK_TAB_W_LARGE);
   pk->tab_b2 = table_shape((size_t)pk->m, ZK_PK_TAB_W_LARGE_B2);
   pk->tab_h = table_shape((size_t)pk->n, ZK_PK_TAB_W_LARGE_H, ZK_PK_TAB_SUB_H);
@@ -598,6 +606,19 @@ static int pk_tables(zk_context* ctx, zk_pk* pk) {
   }
   if (pk->tab_b2.W) ZK_TRY(pk_table(ctx, true, pk->B2, pk->nB2, pk->tab_b2, &pk->tB2));
   if (pk->tab_h.W) ZK_TRY(pk_table(ctx, false, pk->H, pk->nH, pk->tab_h, &pk->tH));
+  return ZK_OK;
+}
+
+// The tables only speed the proof up: when device memory for them (or for
+// their temporary) runs out, the key loads without any (the three witness
+// G1 sets use them all or none) and proofs take the plain MSMs, same bytes.
+static int pk_tables(zk_context* ctx, zk_pk* pk) {
+  const int rc = pk_tables_build(ctx, pk);
+  if (rc != ZK_ERR_OOM) return rc;
+  pk_drop_tables(pk);
+  (void)hipGetLastError();  // the failed allocation's error is not this call's
+  std::lock_guard<std::mutex> lk(ctx->mu);
+  ctx->last_error.clear();
   return ZK_OK;
 }
 
@@ -670,7 +691,8 @@ int zk_pk_load(zk_context* ctx, const char* path, zk_pk** out) {
 
 void zk_pk_destroy(zk_pk* pk) {
   if (!pk) return;
-  for (void* p : {pk->A, pk->B1, pk->B2, pk->L, pk->H, pk->tA, pk->tB1, pk->tB2, pk->tL, pk->tH})
+  pk_drop_tables(pk);
+  for (void* p : {pk->A, pk->B1, pk->B2, pk->L, pk->H})
     if (p) (void)hipFree(p);
   delete pk;
 }

@@ -1808,6 +1808,7 @@ static int table_build(zk_context* ctx, const uint4* recs, size_t count, const M
   ZK_TRY(ctx->ensure(tmp, (size_t)t.W * count * sizeof(xyzz<F>)));
   int rc = ZK_OK;
   {
+    (void)hipGetLastError();
     zk::TimingToken tk = ctx->tic("msm_table", st);
     hipLaunchKernelGGL(k_msm_tab_double<F>, dim3(cdiv(count, 128)), dim3(128), 0, st, recs, count, t.W,
                        (xyzz<F>*)tmp.p);

@@ -140,8 +140,12 @@ int guard(zk_context* ctx, Fn&& fn) noexcept {
 __device__ __forceinline__ void quotient_priority() { __builtin_amdgcn_s_setprio(3); }
 
 // Launch helper with error capture.
+// The error state is cleared first: a handled failure earlier in the thread
+// (an allocation that ran out of memory and was answered with a fallback or
+// a status) must not read as this launch's failure.
 #define ZK_LAUNCH(ctx, st, name, kernel, grid, block, shmem, ...)                            \
   do {                                                                                     \
+    (void)hipGetLastError();                                                               \
     zk::TimingToken _tk = (ctx)->tic(name, st);                                            \
     hipLaunchKernelGGL(kernel, grid, block, shmem, st, __VA_ARGS__);                       \
     hipError_t _e = hipGetLastError();                                                     \
