@@ -9,8 +9,9 @@
 // column accumulator and no carry has to be propagated until the column is
 // finished (18 products of < 2^60 plus a 2^35 carry stay below 2^64).  On
 // gfx950 the 32x32->64 mad issues at full rate, so the instruction count of
-// the multiply is what matters; this layout needs 162 mads and ~45 other ops
-// against ~560 instructions for a compiler-lowered 8x32-bit CIOS.
+// the multiply is what matters; this layout needs 162 mads and 42 other ops
+// (a square 126 and 50) against ~560 instructions for a compiler-lowered
+// 8x32-bit CIOS.
 //
 // At the memory boundary elements are the reference's 32-byte little-endian
 // form (4 x u64 = 8 x u32 words), Montgomery form with R = 2^256
@@ -24,6 +25,8 @@
 
 #if defined(__HIPCC__)
 #include <hip/hip_runtime.h>
+#include <utility>
+#include "mad_chain.hpp"
 #define ZK_HD __host__ __device__ __forceinline__
 #else
 #define ZK_HD static inline
@@ -115,12 +118,111 @@ ZK_HD fe<P> fe_one() {
   return fe_const<P>(P::ONE);
 }
 
+#if defined(__HIP_DEVICE_COMPILE__)
+// Device columns of the Montgomery products below: the same terms in the
+// same columns, each column one serial multiply-add chain seeded with the
+// incoming carry (mad_chain.hpp).  Every partial sum is a prefix of the
+// column's sum, so the bounds stated for the products hold at every step.
+//
+// Reduction part of column K: q_i m_(K-i) for i < K, 1 <= K - i <= 8, then
+// the column's own quotient (K < 9) or output limb (K >= 9), then the carry.
+template <class P, int K>
+__device__ __forceinline__ void mont_col_reduce(uint64_t& acc, uint32_t* q, fe<P>& r) {
+  constexpr int rlo = K > NL - 1 ? K - (NL - 1) : 0;
+  constexpr int nr = (K < NL ? K : NL) - rlo;
+  if constexpr (nr > 0) {
+    uint32_t x[nr], y[nr];
+#pragma unroll
+    for (int u = 0; u < nr; u++) {
+      x[u] = q[rlo + u];
+      y[u] = P::MOD[K - rlo - u];
+    }
+    mad_vs<nr>(acc, x, y);
+  }
+  if constexpr (K < NL) {
+    q[K] = ((uint32_t)acc * P::INV) & LMASK;
+    const uint32_t x[1] = {q[K]}, y[1] = {P::MOD[0]};
+    mad_vs<1>(acc, x, y);
+  } else {
+    r.l[K - NL] = (uint32_t)acc & LMASK;
+  }
+  acc >>= 29;
+}
+
+// Column K of sum_t a[t]*b[t]: the products a[t]_i b[t]_(K-i), then the reduction.
+template <class P, int N, int K>
+__device__ __forceinline__ void mont_col(uint64_t& acc, const fe<P>* a, const fe<P>* b, uint32_t* q, fe<P>& r) {
+  constexpr int ilo = K < NL ? 0 : K - NL + 1;
+  constexpr int np = (K < NL ? K : NL - 1) - ilo + 1;
+  uint32_t x[N * np], y[N * np];
+#pragma unroll
+  for (int t = 0; t < N; t++) {
+#pragma unroll
+    for (int u = 0; u < np; u++) {
+      x[t * np + u] = a[t].l[ilo + u];
+      y[t * np + u] = b[t].l[K - ilo - u];
+    }
+  }
+  mad_vv<N * np>(acc, x, y);
+  mont_col_reduce<P, K>(acc, q, r);
+}
+
+template <class P, int N, int... K>
+__device__ __forceinline__ fe<P> mont_product(const fe<P>* a, const fe<P>* b, std::integer_sequence<int, K...>) {
+  uint32_t q[NL];
+  fe<P> r;
+  uint64_t acc = 0;
+  (mont_col<P, N, K>(acc, a, b, q, r), ...);
+  r.l[NL - 1] = (uint32_t)acc;
+  return r;
+}
+
+// Column K of a^2: cross products a_i (2 a_j), i < j, and the square of
+// a_(K/2) for even K.  With limbs below 2^30 the largest column (K = 8: four
+// cross products below 2^61, a square below 2^60, nine reduction products
+// below 2^58, a carry below 2^35) stays below 1.41 * 2^63.
+template <class P, int K>
+__device__ __forceinline__ void sqr_col(uint64_t& acc, const fe<P>& a, const uint32_t* a2, uint32_t* q, fe<P>& r) {
+  constexpr int ilo = K < NL ? 0 : K - NL + 1;
+  constexpr int ihi = K >= 1 ? (K - 1) / 2 : -1;  // i < K - i
+  constexpr int nc = ihi >= ilo ? ihi - ilo + 1 : 0;
+  constexpr int nd = (K % 2 == 0) ? 1 : 0;
+  uint32_t x[nc + nd], y[nc + nd];
+#pragma unroll
+  for (int u = 0; u < nc; u++) {
+    x[u] = a.l[ilo + u];
+    y[u] = a2[K - ilo - u];
+  }
+  if constexpr (nd) {
+    x[nc] = a.l[K / 2];
+    y[nc] = a.l[K / 2];
+  }
+  mad_vv<nc + nd>(acc, x, y);
+  mont_col_reduce<P, K>(acc, q, r);
+}
+
+template <class P, int... K>
+__device__ __forceinline__ fe<P> mont_square(const fe<P>& a, std::integer_sequence<int, K...>) {
+  uint32_t q[NL], a2[NL];
+  fe<P> r;
+#pragma unroll
+  for (int i = 0; i < NL; i++) a2[i] = a.l[i] << 1;
+  uint64_t acc = 0;
+  (sqr_col<P, K>(acc, a, a2, q, r), ...);
+  r.l[NL - 1] = (uint32_t)acc;
+  return r;
+}
+#endif
+
 // Montgomery product a*b*2^-261 mod m, column (product-scanning) order with the
 // reduction interleaved per column.  Inputs: limbs < 2^30.  Output: limbs
 // < 2^29, value < a*b/2^261 + m, so below 2m for values < 8m, and also when
 // one operand is below m and the other anywhere below 2^261.
 template <class P>
 ZK_HD fe<P> fmul(const fe<P>& a, const fe<P>& b) {
+#if defined(__HIP_DEVICE_COMPILE__)
+  return mont_product<P, 1>(&a, &b, std::make_integer_sequence<int, 2 * NL - 1>{});
+#else
   uint32_t q[NL];
   fe<P> r;
   uint64_t acc = 0;
@@ -146,6 +248,7 @@ ZK_HD fe<P> fmul(const fe<P>& a, const fe<P>& b) {
   }
   r.l[NL - 1] = (uint32_t)acc;
   return r;
+#endif
 }
 
 // sum_t a[t]*b[t] * 2^-261 mod m, N <= 4, with one Montgomery reduction for
@@ -155,6 +258,9 @@ ZK_HD fe<P> fmul(const fe<P>& a, const fe<P>& b) {
 template <class P, int N>
 ZK_HD fe<P> fmul_sum(const fe<P> (&a)[N], const fe<P> (&b)[N]) {
   static_assert(N >= 1 && N <= 4, "column accumulator bound");
+#if defined(__HIP_DEVICE_COMPILE__)
+  return mont_product<P, N>(a, b, std::make_integer_sequence<int, 2 * NL - 1>{});
+#else
   uint32_t q[NL];
   fe<P> r;
   uint64_t acc = 0;
@@ -183,6 +289,7 @@ ZK_HD fe<P> fmul_sum(const fe<P> (&a)[N], const fe<P> (&b)[N]) {
   }
   r.l[NL - 1] = (uint32_t)acc;
   return r;
+#endif
 }
 
 // (a*b + c*e) * 2^-261 mod m: fmul_sum of two products (values < 4m).
@@ -195,6 +302,9 @@ ZK_HD fe<P> fmul2(const fe<P>& a, const fe<P>& b, const fe<P>& c, const fe<P>& e
 // Squaring: cross products are summed once and doubled per column.
 template <class P>
 ZK_HD fe<P> fsqr(const fe<P>& a) {
+#if defined(__HIP_DEVICE_COMPILE__)
+  return mont_square<P>(a, std::make_integer_sequence<int, 2 * NL - 1>{});
+#else
   uint32_t q[NL];
   fe<P> r;
   uint64_t acc = 0;
@@ -223,6 +333,7 @@ ZK_HD fe<P> fsqr(const fe<P>& a) {
   }
   r.l[NL - 1] = (uint32_t)acc;
   return r;
+#endif
 }
 
 // (a + b) mod m into [0, 2m).  Inputs normalized, values < 2m.
