@@ -23,6 +23,8 @@ ZK_HD fq2 fadd(const fq2& a, const fq2& b) { return fq2{fadd(a.c0, b.c0), fadd(a
 ZK_HD fq2 fsub(const fq2& a, const fq2& b) { return fq2{fsub(a.c0, b.c0), fsub(a.c1, b.c1)}; }
 ZK_HD fq2 fdbl(const fq2& a) { return fq2{fdbl(a.c0), fdbl(a.c1)}; }
 ZK_HD fq2 fneg(const fq2& a) { return fq2{fneg(a.c0), fneg(a.c1)}; }
+ZK_HD fq fneg_canon_if(const fq& a, bool neg) { return fneg_canon_if<FqP>(a, neg); }
+ZK_HD fq2 fneg_canon_if(const fq2& a, bool neg) { return fq2{fneg_canon_if(a.c0, neg), fneg_canon_if(a.c1, neg)}; }
 // (a0 + a1 u)(b0 + b1 u) = (a0 b0 - a1 b1) + (a0 b1 + a1 b0) u, each
 // coordinate one fmul_sum (4 limb products, 2 reductions; the reference uses
 // Karatsuba, src/field/fp2.cuh:73-78: 3 multiplies, each with its own
@@ -140,9 +142,9 @@ template <class F>
 ZK_HD bool xyzz_madd_fin(xyzz<F>& p, const F& x2, const F& y2) {
   F u2 = fmul(x2, p.zz);
   F s2 = fmul(y2, p.zzz);
-  F P = fsub(u2, p.x);
+  F P = fsub_m(u2, p.x);  // lazy, (0, 4m): only squared, multiplied as the lazy operand and tested
   F R = fsub_m(s2, p.y);  // lazy, (0, 4m)
-  if (fis_zero(P)) {
+  if (fis_zero4(P)) {
     if (fis_zero4(R)) {
       xyzz_mdbl(p, x2, y2);
       return false;
@@ -151,7 +153,7 @@ ZK_HD bool xyzz_madd_fin(xyzz<F>& p, const F& x2, const F& y2) {
     return true;
   }
   F pp = fsqr(P);
-  F ppp = fmul(P, pp);
+  F ppp = fmul(pp, P);
   F q = fmul(p.x, pp);
   F x3 = fsub3(fsqr(R), ppp, q);
   F y3 = fmul_sub(R, fsub_m(q, x3), p.y, ppp);
@@ -183,15 +185,15 @@ ZK_HD void xyzz_add(xyzz<F>& p, const xyzz<F>& q) {
   F u2 = fmul(q.x, p.zz);
   F s1 = fmul(p.y, q.zzz);
   F s2 = fmul(q.y, p.zzz);
-  F P = fsub(u2, u1);
+  F P = fsub_m(u2, u1);  // lazy, (0, 4m)
   F R = fsub_m(s2, s1);  // lazy, (0, 4m)
-  if (fis_zero(P)) {
+  if (fis_zero4(P)) {
     if (fis_zero4(R)) xyzz_dbl(p);
     else xyzz_set_inf(p);
     return;
   }
   F pp = fsqr(P);
-  F ppp = fmul(P, pp);
+  F ppp = fmul(pp, P);
   F qq = fmul(u1, pp);
   F x3 = fsub3(fsqr(R), ppp, qq);
   F y3 = fmul_sub(R, fsub_m(qq, x3), s1, ppp);

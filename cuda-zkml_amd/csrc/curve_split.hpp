@@ -42,6 +42,7 @@ __device__ __forceinline__ fq2h fadd(const fq2h& a, const fq2h& b) { return fq2h
 __device__ __forceinline__ fq2h fsub(const fq2h& a, const fq2h& b) { return fq2h{fsub(a.c, b.c)}; }
 __device__ __forceinline__ fq2h fdbl(const fq2h& a) { return fq2h{fdbl(a.c)}; }
 __device__ __forceinline__ fq2h fneg(const fq2h& a) { return fq2h{fneg(a.c)}; }
+__device__ __forceinline__ fq2h fneg_canon_if(const fq2h& a, bool neg) { return fq2h{fneg_canon_if(a.c, neg)}; }
 __device__ __forceinline__ fq2h fsub3(const fq2h& a, const fq2h& b, const fq2h& c) {
   return fq2h{fsub3<FqP>(a.c, b.c, c.c)};
 }
@@ -234,9 +235,9 @@ __device__ __forceinline__ void xyzz_add(xyzz<split<E>>& p, const xyzz<split<E>>
   const E U1 = pick(r1, ao, a), U2 = pick(r1, a, ao);
   const E S1 = pick(r1, bo, b), S2 = pick(r1, b, bo);
   const E ZZ12 = pick(r1, co, c), ZZZ12 = pick(r1, c, co);
-  const E P = fsub(U2, U1);
+  const E P = fsub_m(U2, U1);  // lazy, (0, 4m)
   const E R = fsub_m(S2, S1);  // lazy, (0, 4m)
-  if (fis_zero(P)) {
+  if (fis_zero4(P)) {
     if (fis_zero4(R)) xyzz_dbl(p);
     else xyzz_set_inf(p);
     return;
@@ -244,7 +245,7 @@ __device__ __forceinline__ void xyzz_add(xyzz<split<E>>& p, const xyzz<split<E>>
   const E t = fsqr(pick(r1, R, P));  // PP | RR
   const E to = other_role(t);
   const E PP = pick(r1, to, t), RR = pick(r1, t, to);
-  const E v = fmul(pick(r1, U1, P), PP);  // PPP | Q
+  const E v = fmul(PP, pick(r1, U1, P));  // PPP | Q (P lazy: the second factor)
   const E ZZ3 = fmul(ZZ12, PP);
   const E vo = other_role(v);
   const E PPP = pick(r1, vo, v), Q = pick(r1, v, vo);

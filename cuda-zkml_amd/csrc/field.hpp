@@ -412,6 +412,23 @@ ZK_HD fe<P> fneg_lazy(const fe<P>& a) {
   return d;
 }
 
+// neg ? m - a : a for a canonical (in [0, m)); m - a is in (0, m], a valid
+// value of the lazy range [0, 2m).
+template <class P>
+ZK_HD fe<P> fneg_canon_if(const fe<P>& a, bool neg) {
+  fe<P> d;
+  int32_t br = 0;
+#pragma unroll
+  for (int i = 0; i < NL; i++) {
+    int32_t v = (int32_t)P::MOD[i] - (int32_t)a.l[i] + br;
+    br = v >> 29;
+    d.l[i] = (uint32_t)v & LMASK;
+  }
+#pragma unroll
+  for (int i = 0; i < NL; i++) d.l[i] = neg ? d.l[i] : a.l[i];
+  return d;
+}
+
 template <class P>
 ZK_HD fe<P> fneg(const fe<P>& a) {
   return fsub(fe_zero<P>(), a);

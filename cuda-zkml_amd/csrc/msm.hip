@@ -129,6 +129,8 @@ __device__ __forceinline__ bool load_rec(const uint4* __restrict__ recs, uint32_
   return any == 0;
 }
 
+// pack_coord stores canonical values (repack_out), so a negative digit's -y
+// is the cheap q - y in the accumulation (fneg_canon_if).
 template <class F>
 __device__ __forceinline__ void store_rec(uint4* __restrict__ recs, size_t idx, const F& x, const F& y, bool inf) {
   constexpr int W = Rec<F>::WORDS;
@@ -854,7 +856,10 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(sizeof(F) =
       const uint2 e = sorted[p];
       const uint32_t key = e.x;
       if (key != cur) {
-        // run `cur` ended inside the chunk
+        // run `cur` ended inside the chunk; acc holds whatever the last run
+        // left while `empty` (the next point overwrites it), so a run that
+        // summed to nothing stores the point at infinity explicitly
+        if (__builtin_expect(empty, 0)) xyzz_set_inf(acc);
         if (start[cur] < lo) {
           hk = cur;
           LN::store(slots.hpt[ch], acc);
@@ -862,7 +867,6 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(sizeof(F) =
           LN::store(buckets[cur], acc);
         }
         cur = key;
-        xyzz_set_inf(acc);
         empty = true;
       }
       const uint32_t v = e.y;
@@ -874,7 +878,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(sizeof(F) =
       i -= ilo;  // wraps below lo
       R x, y;
       if (i < ilen && !load_rec_lanes(recs, row * tstride + i, x, y)) {
-        if (v >> 31) y = fneg(y);
+        y = fneg_canon_if(y, (v >> 31) != 0);  // negative digit: -P
         if (empty) {
           xyzz_set_affine(acc, x, y);
           empty = false;
@@ -884,6 +888,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(sizeof(F) =
       }
     }
     // last run of the chunk
+    if (__builtin_expect(empty, 0)) xyzz_set_inf(acc);
     const uint32_t rs = start[cur], re = end[cur];
     if (rs >= lo && re <= lo + L0) {
       LN::store(buckets[cur], acc);
@@ -1748,8 +1753,6 @@ int msm_recs_tab(zk_context* ctx, MsmWorkspace* ws, bool g2, const void* d_table
 }
 
 // ------------------------------------------------------------------ window tables
-__device__ __forceinline__ fq coord_canon(const fq& a) { return fcanon(a); }
-__device__ __forceinline__ fq2 coord_canon(const fq2& a) { return fq2{fcanon(a.c0), fcanon(a.c1)}; }
 
 // tmp[w count + j] = 2^(bits of the windows below w) P_j, XYZZ.
 template <class F>
@@ -1790,7 +1793,7 @@ __global__ void k_msm_tab_affine(const xyzz<F>* __restrict__ tmp, size_t total, 
       fset_zero(x[k]);
       fset_zero(y[k]);
     }
-    store_rec(out, base + k, coord_canon(x[k]), coord_canon(y[k]), inf[k]);
+    store_rec(out, base + k, x[k], y[k], inf[k]);
   }
 }
 
