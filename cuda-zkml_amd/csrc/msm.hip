@@ -56,13 +56,15 @@ constexpr int MSM_NCB = 256;       // coarse bins per window of the two-pass pla
 constexpr int MSM_BPC_MAX = 128;   // buckets per coarse bin at B = 2^15
 constexpr int PLACE_T = 1024;      // threads of a placement block
 constexpr uint32_t MSM_SERIAL_SPAN = 8;  // longest serial chunk-partial chain of the one-launch combine
-// Partials folded per bucket group by each level of a deeper combine.  A
+// Partials folded per bucket group by each level of the level combine.  A
 // level costs a launch plus S - 1 dependent additions; measured on MI355X
 // (G2 2^16 and G1 witness-like 2^20 MSMs, the 2^16 proof) S = 2 beats 4 and 8.
-#ifndef ZK_MSM_COMBINE_S
-#define ZK_MSM_COMBINE_S 2
+constexpr uint32_t MSM_COMBINE_S = 2;
+// Spans above which the tree combine replaces the level combine.
+#ifndef ZK_MSM_TREE_SPAN
+#define ZK_MSM_TREE_SPAN 1024
 #endif
-constexpr uint32_t MSM_COMBINE_S = ZK_MSM_COMBINE_S;
+constexpr uint32_t MSM_TREE_SPAN = ZK_MSM_TREE_SPAN;
 // G2 accumulation tuning: chunk length divided by 2^ZK_MSM_G2_L0_SHIFT (down
 // to MSM_L0 / 8), waves per SIMD the register budget is cut to.
 #ifndef ZK_MSM_G2_L0_SHIFT
@@ -914,32 +916,39 @@ template <class LN>
 __device__ __forceinline__ uint32_t lane_item() {
   return (blockIdx.x * blockDim.x + threadIdx.x) / LN::N;
 }
+__device__ __forceinline__ uint32_t cdiv_dev(uint32_t a, uint32_t b) { return (a + b - 1) / b; }
 
 // Chunk combine.  The partials of a bucket whose run spans chunks c0 .. c1
-// are the tail partial of c0 and the head partials of c0+1 .. c1.
+// are the tail partial of c0 and the head partials of c0+1 .. c1 (every chunk
+// holds at most one head and one tail partial).
 //
-// When no bucket spans more than MSM_SERIAL_SPAN + 1 chunks, one launch:
-// the chunk where a spanning run starts adds the head partials of the
-// following chunks it covers, in order, and stores the bucket.
+// Spans of up to MSM_SERIAL_SPAN + 1 chunks: one launch in which the chunk
+// where the run starts adds the head partials of the chunks it covers, in
+// order, and stores the bucket.  Longer spans (hot buckets such as many
+// scalars equal to 1, or the large buckets of a window-table MSM) are left to
+// k_msm_combine_tree, whose fold counters this launch clears.
 template <class F, class LN>
 __global__ __launch_bounds__(256) void k_msm_combine_serial(ChunkSlots<F> all_slots,
                                                             const uint32_t* __restrict__ end, uint32_t nchunks,
                                                             uint32_t L0, size_t nbuckets,
-                                                            xyzz<F>* __restrict__ buckets) {
+                                                            xyzz<F>* __restrict__ buckets,
+                                                            uint32_t* __restrict__ fold_cnt, uint32_t tb) {
   msm_priority<F>();
   const uint32_t ch = lane_item<LN>();
   if (ch >= nchunks) return;
+  if (fold_cnt && ch % tb == 0) fold_cnt[(size_t)blockIdx.y * cdiv_dev(nchunks, tb) + ch / tb] = 0;
   const ChunkSlots<F> slots = all_slots.at(blockIdx.y, nchunks);
   buckets += blockIdx.y * nbuckets;
   const uint32_t tk = slots.tkey[ch];
   if (tk == KEY_INVALID) return;
   const uint32_t c1 = (end[tk] - 1) / L0;
+  if (c1 - ch > MSM_SERIAL_SPAN) return;  // a long span: the tree combine
   auto acc = LN::load(slots.tpt[ch]);
   for (uint32_t j = ch + 1; j <= c1; j++) xyzz_add(acc, LN::load(slots.hpt[j]));
   LN::store(buckets[tk], acc);
 }
 
-// Longer spans (hot buckets, such as many scalars equal to 1): levels with
+// Longer spans up to MSM_TREE_SPAN chunks: levels with
 // step = 1, S, S^2, ... (S = MSM_COMBINE_S) fold the partials in groups of
 // S: the chunk at j = ch - c0 with j % (S*step) == 0 adds the partials at
 // j + step, ..., j + (S-1) step that exist.  After the level with S*step >=
@@ -970,6 +979,146 @@ __global__ __launch_bounds__(256) void k_msm_combine(ChunkSlots<F> all_slots, co
   for (uint32_t m = 1; m < S && ch + m * step <= c1; m++) xyzz_add(acc, LN::load(slots.hpt[ch + m * step]));
   if (tail && c1 - c0 + 1 <= S * step) self = &buckets[key];
   LN::store(*self, acc);
+}
+
+// Tree combine of the buckets spanning more than MSM_SERIAL_SPAN + 1 chunks,
+// in one launch.  Block j covers the TB chunks [j TB, j TB + TB), one item
+// per chunk.  Inside a block every long bucket's head partials form one
+// segment of consecutive items, summed by a tree over the item's position in
+// its segment (log2 of the segment's length levels, all segments at once);
+// the item holding the bucket's tail then adds the sum of the heads that
+// follow it in the block.  A bucket inside one block is stored there.  A
+// bucket crossing blocks j0 .. j1 gets one contribution per block: OUT[j0]
+// (the tail plus the heads of block j0) and IN[j] for j0 < j <= j1 (the
+// block's leading segment).  Each contribution is written, fenced and
+// counted on fold_cnt[j0]; the block that brings the count to j1 - j0 + 1
+// folds the contributions with the same tree and stores the bucket.  A block
+// has at most one leading (IN) and one trailing (OUT) bucket, so it folds at
+// most two.  Point addition is commutative, so the fold order does not change
+// the bucket's value.
+template <class F, class LN, int TB>
+__global__ __launch_bounds__(TB * LN::N) void k_msm_combine_tree(ChunkSlots<F> all_slots,
+                                                                 const uint32_t* __restrict__ start,
+                                                                 const uint32_t* __restrict__ end,
+                                                                 uint32_t nchunks, uint32_t L0, size_t nbuckets,
+                                                                 xyzz<F>* __restrict__ buckets,
+                                                                 uint32_t* __restrict__ fold_cnt,
+                                                                 xyzz<F>* __restrict__ cin, xyzz<F>* __restrict__ cout) {
+  typedef typename LN::R R;
+  msm_priority<F>();
+  __shared__ xyzz<F> V[TB];
+  __shared__ uint32_t fold_key[2], fold_j0[2], fold_n[2], maxlen;
+  const uint32_t t = threadIdx.x / LN::N;
+  const bool lead = threadIdx.x % LN::N == 0;  // the lane of an item that does its atomics
+  const uint32_t set = blockIdx.y;
+  const uint32_t nblk = cdiv_dev(nchunks, TB);
+  const ChunkSlots<F> slots = all_slots.at(set, nchunks);
+  buckets += set * nbuckets;
+  fold_cnt += (size_t)set * nblk;
+  cin += (size_t)set * nblk;
+  cout += (size_t)set * nblk;
+  const uint32_t j = blockIdx.x, b0 = j * TB, b1 = min(b0 + TB, nchunks);  // the block's chunks [b0, b1)
+  const uint32_t ch = b0 + t;
+  if (t < 2) fold_key[t] = KEY_INVALID;
+  if (t == 0) maxlen = 0;
+
+  // this item's head partial, when it belongs to a long bucket
+  uint32_t hk = KEY_INVALID, r = 0, len = 0, hc0 = 0, hc1 = 0;
+  if (ch < b1) {
+    const uint32_t k = slots.hkey[ch];
+    if (k != KEY_INVALID) {
+      hc0 = start[k] / L0;
+      hc1 = (end[k] - 1) / L0;
+      if (hc1 - hc0 > MSM_SERIAL_SPAN) {
+        hk = k;
+        const uint32_t lo = max(hc0 + 1, b0), hi = min(hc1, b1 - 1);
+        r = ch - lo;
+        len = hi - lo + 1;
+      }
+    }
+  }
+  // this item's tail partial, when it starts a long bucket
+  uint32_t tk = KEY_INVALID, tc1 = 0;
+  if (ch < b1) {
+    const uint32_t k = slots.tkey[ch];
+    if (k != KEY_INVALID) {
+      tc1 = (end[k] - 1) / L0;
+      if (tc1 - ch > MSM_SERIAL_SPAN) tk = k;
+    }
+  }
+  __syncthreads();
+  if (!__syncthreads_or(hk != KEY_INVALID || tk != KEY_INVALID)) return;  // no long bucket here
+  if (hk != KEY_INVALID && r == 0 && lead) atomicMax(&maxlen, len);
+  xyzz<R> v;
+  xyzz_set_inf(v);
+  if (hk != KEY_INVALID) {
+    v = LN::load(slots.hpt[ch]);
+    LN::store(V[t], v);
+  }
+  __syncthreads();
+  const uint32_t levels_len = maxlen;
+  for (uint32_t d = 1; d < levels_len; d <<= 1) {
+    if (hk != KEY_INVALID && r % (2 * d) == 0 && r + d < len) {
+      xyzz_add(v, LN::load(V[t + d]));
+      LN::store(V[t], v);
+    }
+    __syncthreads();
+  }
+  // V[first item of a segment] = the segment's sum.  Contributions:
+  if (tk != KEY_INVALID) {
+    xyzz<R> acc = LN::load(slots.tpt[ch]);
+    if (ch + 1 < b1) xyzz_add(acc, LN::load(V[t + 1]));  // the heads that follow in this block
+    if (tc1 < b1) {
+      LN::store(buckets[tk], acc);  // the whole bucket is in this block
+    } else {
+      LN::store(cout[j], acc);
+      __threadfence();
+      if (lead) {
+        const uint32_t j1 = tc1 / TB, need = j1 - j + 1;
+        if (atomicAdd(&fold_cnt[j], 1u) == need - 1) {
+          fold_key[1] = tk;
+          fold_j0[1] = j;
+          fold_n[1] = need;
+        }
+      }
+    }
+  }
+  if (hk != KEY_INVALID && r == 0 && hc0 < b0) {  // the leading segment of a bucket from an earlier block
+    LN::store(cin[j], v);
+    __threadfence();
+    if (lead) {
+      const uint32_t j0 = hc0 / TB, j1 = hc1 / TB, need = j1 - j0 + 1;
+      if (atomicAdd(&fold_cnt[j0], 1u) == need - 1) {
+        fold_key[0] = hk;
+        fold_j0[0] = j0;
+        fold_n[0] = need;
+      }
+    }
+  }
+  __syncthreads();
+  // The last contributor of a crossing bucket folds OUT[j0], IN[j0+1 .. j1].
+  for (int f = 0; f < 2; f++) {
+    const uint32_t key = fold_key[f];
+    if (key == KEY_INVALID) continue;  // uniform over the block
+    __threadfence();
+    const uint32_t j0 = fold_j0[f], n = fold_n[f];
+    xyzz<R> a;
+    xyzz_set_inf(a);
+    for (uint32_t i = t; i < n; i += TB) xyzz_add(a, LN::load(i == 0 ? cout[j0] : cin[j0 + i]));
+    __syncthreads();
+    LN::store(V[t], a);
+    __syncthreads();
+    const uint32_t m = min(n, (uint32_t)TB);
+    for (uint32_t d = 1; d < m; d <<= 1) {
+      if (t % (2 * d) == 0 && t + d < m) {
+        xyzz_add(a, LN::load(V[t + d]));
+        LN::store(V[t], a);
+      }
+      __syncthreads();
+    }
+    if (t == 0) LN::store(buckets[key], a);
+    __syncthreads();
+  }
 }
 
 // ------------------------------------------------------------------ bucket reduction
@@ -1130,7 +1279,7 @@ constexpr int MSM_PARTS = 192;  // window (or sub-window) partials of one MSM, a
 
 struct MsmWorkspace {
   DevBuf recs, dig, hist, tot, lex, bsum, bmax, boff, tmp, sorted, start, end, wstat, buckets, hkey, tkey, hpt, tpt,
-      seg, grp, win;
+      seg, grp, win, fcnt, fin, fout;
   uint32_t* h_stat = nullptr;  // pinned, 2 words per window
   void* h_parts = nullptr;     // pinned, the per-window partials of every set
   hipEvent_t stat_ready = nullptr;
@@ -1143,7 +1292,7 @@ void msm_workspace_free(MsmWorkspace* ws) {
   if (!ws) return;
   for (DevBuf* b : {&ws->recs, &ws->dig, &ws->hist, &ws->tot, &ws->lex, &ws->bsum, &ws->bmax, &ws->boff, &ws->tmp,
                     &ws->sorted, &ws->start, &ws->end, &ws->wstat, &ws->buckets, &ws->hkey, &ws->tkey, &ws->hpt,
-                    &ws->tpt, &ws->seg, &ws->grp, &ws->win})
+                    &ws->tpt, &ws->seg, &ws->grp, &ws->win, &ws->fcnt, &ws->fin, &ws->fout})
     if (b->p) (void)hipFree(b->p);
   if (ws->h_stat) (void)hipHostFree(ws->h_stat);
   if (ws->h_parts) (void)hipHostFree(ws->h_parts);
@@ -1420,16 +1569,12 @@ static int msm_accumulate(zk_context* ctx, MsmWorkspace& ws, const MsmShape& sh,
   typedef SplitLanes<F> SL;
   const bool split_combine = !G2 || beside;
   const uint32_t gxs = cdiv((size_t)nchunks * (split_combine ? SL::N : Lanes<F>::N), 256);
-  // The largest bucket decides the combine: one serial launch for spans up to
-  // MSM_SERIAL_SPAN + 1 chunks, else levels folding MSM_COMBINE_S partials.
-  if (ap.max_span <= MSM_SERIAL_SPAN + 1) {
-    if (ap.max_span > 1 && split_combine)
-      ZK_LAUNCH(ctx, st, "msm_combine", (k_msm_combine_serial<F, SL>), dim3(gxs, nsets), dim3(256), 0, slots, end,
-                nchunks, L0, nbuckets, buckets);
-    else if (ap.max_span > 1)
-      ZK_LAUNCH(ctx, st, "msm_combine", (k_msm_combine_serial<F, Lanes<F>>), dim3(gxs, nsets), dim3(256), 0, slots,
-                end, nchunks, L0, nbuckets, buckets);
-  } else {
+  // The largest bucket decides the combine: spans of up to MSM_SERIAL_SPAN + 1
+  // chunks fold serially in one launch; up to MSM_TREE_SPAN chunks, levels
+  // folding MSM_COMBINE_S partials each; beyond, the serial launch takes the
+  // short spans and the tree combine the long ones in a second launch (its
+  // fold counters cleared by the first).
+  if (ap.max_span > MSM_SERIAL_SPAN + 1 && ap.max_span <= MSM_TREE_SPAN) {
     for (uint64_t step = 1; step < ap.max_span; step *= MSM_COMBINE_S) {
       if (split_combine)
         ZK_LAUNCH(ctx, st, "msm_combine", (k_msm_combine<F, SL>), dim3(gxs, nsets), dim3(256), 0, slots, start, end,
@@ -1437,6 +1582,33 @@ static int msm_accumulate(zk_context* ctx, MsmWorkspace& ws, const MsmShape& sh,
       else
         ZK_LAUNCH(ctx, st, "msm_combine", (k_msm_combine<F, Lanes<F>>), dim3(gxs, nsets), dim3(256), 0, slots, start,
                   end, nchunks, L0, (uint32_t)step, nbuckets, buckets);
+    }
+  } else if (ap.max_span > 1) {
+    const bool tree = ap.max_span > MSM_SERIAL_SPAN + 1;
+    constexpr int TB = G2 ? 128 : 256;  // chunks per tree block (36 KB of LDS points)
+    const uint32_t nblk = cdiv(nchunks, TB);
+    uint32_t* fcnt = nullptr;
+    if (tree) {
+      ZK_TRY(ctx->ensure(ws.fcnt, (size_t)nsets * nblk * 4));
+      ZK_TRY(ctx->ensure(ws.fin, (size_t)nsets * nblk * sizeof(xyzz<F>)));
+      ZK_TRY(ctx->ensure(ws.fout, (size_t)nsets * nblk * sizeof(xyzz<F>)));
+      fcnt = (uint32_t*)ws.fcnt.p;
+    }
+    if (split_combine)
+      ZK_LAUNCH(ctx, st, "msm_combine", (k_msm_combine_serial<F, SL>), dim3(gxs, nsets), dim3(256), 0, slots, end,
+                nchunks, L0, nbuckets, buckets, fcnt, (uint32_t)TB);
+    else
+      ZK_LAUNCH(ctx, st, "msm_combine", (k_msm_combine_serial<F, Lanes<F>>), dim3(gxs, nsets), dim3(256), 0, slots,
+                end, nchunks, L0, nbuckets, buckets, fcnt, (uint32_t)TB);
+    if (tree) {
+      xyzz<F>* fin = (xyzz<F>*)ws.fin.p;
+      xyzz<F>* fout = (xyzz<F>*)ws.fout.p;
+      if (split_combine)
+        ZK_LAUNCH(ctx, st, "msm_combine", (k_msm_combine_tree<F, SL, TB>), dim3(nblk, nsets), dim3(TB * SL::N), 0,
+                  slots, start, end, nchunks, L0, nbuckets, buckets, fcnt, fin, fout);
+      else
+        ZK_LAUNCH(ctx, st, "msm_combine", (k_msm_combine_tree<F, Lanes<F>, TB>), dim3(nblk, nsets),
+                  dim3(TB * Lanes<F>::N), 0, slots, start, end, nchunks, L0, nbuckets, buckets, fcnt, fin, fout);
     }
   }
   return ZK_OK;

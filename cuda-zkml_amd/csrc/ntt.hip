@@ -343,23 +343,37 @@ __device__ __forceinline__ void tile_copy_out(const TileCtx& tc, const PassGeo& 
 // planes of T*R words plus nine planes of R/2 twiddles.  Inputs below 2m
 // (canonical words, or the previous pass's outputs).  The DFT runs in steps
 // of KMAX stages, the remainder in the last step.
-template <int KMAX, bool LAST>
+//
+// LR > 0 fixes the geometry at compile time: R = 2^LR rows in tiles of
+// NTT_TILE_FIXED elements (the large transforms' shape).  The LDS plane and
+// twiddle strides are then constants, so the nine limb accesses of an element
+// share one address register and differ by immediate offsets, where runtime
+// strides cost an address computation per limb.  LR = 0 reads the geometry
+// from g.
+constexpr uint32_t NTT_TILE_FIXED_LOG = 11;
+template <int KMAX, bool LAST, int LR = 0>
 __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(KMAX == 3 ? 2 : 3)))
 void k_ntt_pass(PassGeo g, PassIO io) {
   quotient_priority();
   extern __shared__ uint32_t smem[];
   constexpr int EPT = 1 << KMAX;
   TileCtx tc;
-  tc.logR = g.logR;
-  tc.logT = g.logT;
-  tc.E = 1u << (g.logR + g.logT);
-  tc.half = 1u << (g.logR - 1);
+  if constexpr (LR > 0) {
+    tc.logR = LR;
+    tc.logT = NTT_TILE_FIXED_LOG - LR;
+    tc.nthr = 1u << (NTT_TILE_FIXED_LOG - KMAX);
+  } else {
+    tc.logR = g.logR;
+    tc.logT = g.logT;
+    tc.nthr = blockDim.x;
+  }
+  tc.E = 1u << (tc.logR + tc.logT);
+  tc.half = 1u << (tc.logR - 1);
   tc.smask = tc.logT >= 5 ? 0u : (tc.logT >= 3 ? (32u >> tc.logT) - 1u : 7u);
   tc.cmask = (1u << tc.logT) - 1;
   tc.s = smem;
   tc.tw = smem + NL * tc.E;
   tc.tid = threadIdx.x;
-  tc.nthr = blockDim.x;
 
   const size_t boff = (size_t)blockIdx.y * g.n;
   const uint4* src = io.src + 2 * boff;
@@ -370,7 +384,7 @@ void k_ntt_pass(PassGeo g, PassIO io) {
     const uint32_t lt = g.logS - tc.logT;  // tiles per block of R*S elements (log)
     const size_t u = blockIdx.x >> lt;
     o.m0 = (blockIdx.x & ((1u << lt) - 1)) << tc.logT;
-    o.base = (u << (g.logR + g.logS)) + o.m0;
+    o.base = (u << (tc.logR + g.logS)) + o.m0;
   } else {
     const uint32_t lt = g.logR0 - tc.logT;
     o.v = blockIdx.x >> lt;
@@ -385,8 +399,8 @@ void k_ntt_pass(PassGeo g, PassIO io) {
   }
   __syncthreads();
 
-  const uint32_t nsteps = (g.logR + KMAX - 1) / KMAX;
-  const uint32_t klast = g.logR - KMAX * (nsteps - 1);
+  const uint32_t nsteps = (tc.logR + KMAX - 1) / KMAX;
+  const uint32_t klast = tc.logR - KMAX * (nsteps - 1);
   if (nsteps == 1) {
     // a single step (R <= 2^KMAX): the whole DFT in the first step, then out
     switch (klast) {
@@ -706,6 +720,12 @@ static void ntt_lds_limits() {
   std::call_once(once, [] {
     const int bytes = 160 * 1024;
     (void)hipFuncSetAttribute((const void*)k_ntt_pass<3, true>, hipFuncAttributeMaxDynamicSharedMemorySize, bytes);
+    (void)hipFuncSetAttribute((const void*)k_ntt_pass<3, true, 8>, hipFuncAttributeMaxDynamicSharedMemorySize, bytes);
+    (void)hipFuncSetAttribute((const void*)k_ntt_pass<3, false, 8>, hipFuncAttributeMaxDynamicSharedMemorySize, bytes);
+    (void)hipFuncSetAttribute((const void*)k_ntt_pass<3, true, 7>, hipFuncAttributeMaxDynamicSharedMemorySize, bytes);
+    (void)hipFuncSetAttribute((const void*)k_ntt_pass<3, false, 7>, hipFuncAttributeMaxDynamicSharedMemorySize, bytes);
+    (void)hipFuncSetAttribute((const void*)k_ntt_pass<3, true, 6>, hipFuncAttributeMaxDynamicSharedMemorySize, bytes);
+    (void)hipFuncSetAttribute((const void*)k_ntt_pass<3, false, 6>, hipFuncAttributeMaxDynamicSharedMemorySize, bytes);
     (void)hipFuncSetAttribute((const void*)k_ntt_pass<3, false>, hipFuncAttributeMaxDynamicSharedMemorySize, bytes);
     (void)hipFuncSetAttribute((const void*)k_ntt_pass<2, true>, hipFuncAttributeMaxDynamicSharedMemorySize, bytes);
     (void)hipFuncSetAttribute((const void*)k_ntt_pass<2, false>, hipFuncAttributeMaxDynamicSharedMemorySize, bytes);
@@ -760,7 +780,23 @@ static int ntt_exec(zk_context* ctx, const NttPlan* plan, const NttCall& c, hipS
     const uint32_t tiles = (uint32_t)(n / E);
     const size_t lds = (size_t)NL * 4 * (E + (1u << (g.logR - 1)));
     const dim3 grid(tiles, c.batch), block(threads);
-    if (kmax == 3 && g.logR >= 3) {
+    const bool fixed = kmax == 3 && E == (1u << NTT_TILE_FIXED_LOG) && threads == (E >> 3);
+    if (fixed && g.logR == 8) {
+      if (last)
+        ZK_LAUNCH(ctx, st, "ntt_pass", (k_ntt_pass<3, true, 8>), grid, block, lds, g, io);
+      else
+        ZK_LAUNCH(ctx, st, "ntt_pass", (k_ntt_pass<3, false, 8>), grid, block, lds, g, io);
+    } else if (fixed && g.logR == 7) {
+      if (last)
+        ZK_LAUNCH(ctx, st, "ntt_pass", (k_ntt_pass<3, true, 7>), grid, block, lds, g, io);
+      else
+        ZK_LAUNCH(ctx, st, "ntt_pass", (k_ntt_pass<3, false, 7>), grid, block, lds, g, io);
+    } else if (fixed && g.logR == 6) {
+      if (last)
+        ZK_LAUNCH(ctx, st, "ntt_pass", (k_ntt_pass<3, true, 6>), grid, block, lds, g, io);
+      else
+        ZK_LAUNCH(ctx, st, "ntt_pass", (k_ntt_pass<3, false, 6>), grid, block, lds, g, io);
+    } else if (kmax == 3 && g.logR >= 3) {
       if (last)
         ZK_LAUNCH(ctx, st, "ntt_pass", (k_ntt_pass<3, true>), grid, block, lds, g, io);
       else
