@@ -338,6 +338,102 @@ __device__ __forceinline__ void tile_copy_out(const TileCtx& tc, const PassGeo& 
   }
 }
 
+// ---- fixed-geometry tiles: the elements stay in registers between steps
+// and move through LDS in two halves (limbs 0-4, then 5-8) over five planes,
+// so a 2048-element tile takes 45 KB of LDS instead of 78 KB and three
+// blocks (three waves per SIMD) fit on a CU where two did.
+constexpr int NTT_XPLANES = 5;
+
+// LDS rows of a step of K stages starting at stage s: group gi of the
+// thread holds rows j0 + t 2^s (t < 2^K) of column c; element e = gi 2^K + t.
+template <int EPT, int K>
+__device__ __forceinline__ void step_rows(const TileCtx& tc, uint32_t s, uint32_t (&row)[EPT], uint32_t (&col)[EPT],
+                                          uint32_t (&jl)[EPT >> K]) {
+  const uint32_t h = 1u << s;
+  unroll<(EPT >> K)>([&](auto GI) {
+    const uint32_t grp = tc.tid + (uint32_t)GI * tc.nthr;
+    const uint32_t q = grp >> tc.logT, c = grp & tc.cmask;
+    const uint32_t l = q & (h - 1);
+    jl[GI] = l;
+    const uint32_t j0 = ((q >> s) << (s + K)) | l;
+    unroll<(1 << K)>([&](auto T) {
+      row[GI * (1 << K) + T] = j0 + ((uint32_t)T << s);
+      col[GI * (1 << K) + T] = c;
+    });
+  });
+}
+
+// Registers x (at LDS index ixo of each element) to the elements at ixi.
+template <int EPT>
+__device__ __forceinline__ void xchg_halves(const TileCtx& tc, fr (&x)[EPT], const uint32_t (&ixo)[EPT],
+                                            const uint32_t (&ixi)[EPT]) {
+  uint32_t* s = tc.s;
+  const uint32_t E = tc.E;
+  uint32_t lo[EPT][NTT_XPLANES];
+  __syncthreads();
+  unroll<EPT>([&](auto e) { unroll<NTT_XPLANES>([&](auto l) { s[l * E + ixo[e]] = x[e].l[l]; }); });
+  __syncthreads();
+  unroll<EPT>([&](auto e) { unroll<NTT_XPLANES>([&](auto l) { lo[e][l] = s[l * E + ixi[e]]; }); });
+  __syncthreads();
+  unroll<EPT>([&](auto e) { unroll<NL - NTT_XPLANES>([&](auto l) { s[l * E + ixo[e]] = x[e].l[NTT_XPLANES + l]; }); });
+  __syncthreads();
+  unroll<EPT>([&](auto e) {
+    unroll<NL - NTT_XPLANES>([&](auto l) { x[e].l[NTT_XPLANES + l] = s[l * E + ixi[e]]; });
+    unroll<NTT_XPLANES>([&](auto l) { x[e].l[l] = lo[e][l]; });
+  });
+}
+
+// A whole pass over one tile of R = 2^LR rows (LR > KMAX) with the tile's
+// elements in registers: first step from HBM, middle steps of KMAX stages,
+// the last step of the remaining stages straight to HBM.
+template <int KMAX, bool LAST, int LR>
+__device__ __forceinline__ void tile_fixed(const TileCtx& tc, const PassGeo& g, const PassIO& io, const uint4* src,
+                                           uint4* dst, const TileOrigin& o) {
+  constexpr int EPT = 1 << KMAX;
+  constexpr int NSTEPS = (LR + KMAX - 1) / KMAX;
+  constexpr int KLAST = LR - KMAX * (NSTEPS - 1);
+  static_assert(NSTEPS >= 2, "fixed tiles take at least two steps");
+  fr x[EPT];
+  uint32_t ixo[EPT], ixi[EPT];
+  {
+    const uint32_t q = tc.tid >> tc.logT, c = tc.tid & tc.cmask;
+    const uint32_t rq = bitrev(q, LR - KMAX);
+    auto rowp = [&](int t) { return in_pos<LAST>(g, o, rq + (bitrev(t, KMAX) << (LR - KMAX)), c); };
+    if (io.pre_mode == PRE_QUOTIENT) {
+      unroll<EPT>([&](auto T) { x[T] = quotient_in(g, io, src, rowp(T)); });
+    } else {
+      unroll<EPT>([&](auto T) { x[T] = load_elem(src, rowp(T)); });
+      if (io.pre_mode == PRE_TABLE) unroll<EPT>([&](auto T) { x[T] = fmul(x[T], load_packed(io.pre, rowp(T))); });
+    }
+    first_step<KMAX>(x, tc.tw, tc.half, LR);
+    unroll<EPT>([&](auto T) { ixo[T] = lds_ix((q << KMAX) + T, c, tc.logT, tc.smask); });
+  }
+  uint32_t stage = KMAX;
+  unroll<NSTEPS - 2>([&](auto) {
+    uint32_t row[EPT], col[EPT], jl[1];
+    step_rows<EPT, KMAX>(tc, stage, row, col, jl);
+    unroll<EPT>([&](auto e) { ixi[e] = lds_ix(row[e], col[e], tc.logT, tc.smask); });
+    xchg_halves<EPT>(tc, x, ixo, ixi);
+    mid_step<KMAX>(x, tc.tw, tc.half, LR, stage, jl[0]);
+    unroll<EPT>([&](auto e) { ixo[e] = ixi[e]; });
+    stage += KMAX;
+  });
+  uint32_t row[EPT], col[EPT], jl[EPT >> KLAST];
+  step_rows<EPT, KLAST>(tc, stage, row, col, jl);
+  unroll<EPT>([&](auto e) { ixi[e] = lds_ix(row[e], col[e], tc.logT, tc.smask); });
+  xchg_halves<EPT>(tc, x, ixo, ixi);
+  unroll<(EPT >> KLAST)>([&](auto GI) {
+    fr y[1 << KLAST];
+    unroll<(1 << KLAST)>([&](auto T) { y[T] = x[GI * (1 << KLAST) + T]; });
+    mid_step<KLAST>(y, tc.tw, tc.half, LR, stage, jl[GI]);
+    unroll<(1 << KLAST)>([&](auto T) {
+      size_t pos;
+      const fr r = finish<LAST>(g, io, o, row[GI * (1 << KLAST) + T], col[GI * (1 << KLAST) + T], y[T], pos);
+      store_elem_raw(dst, pos, r);
+    });
+  });
+}
+
 // One pass over tiles of R = 2^logR rows and T = 2^logT columns; block =
 // T*R / 2^min(KMAX, logR) threads; grid = (tiles, batch).  Dynamic LDS: nine
 // planes of T*R words plus nine planes of R/2 twiddles.  Inputs below 2m
@@ -352,7 +448,7 @@ __device__ __forceinline__ void tile_copy_out(const TileCtx& tc, const PassGeo& 
 // from g.
 constexpr uint32_t NTT_TILE_FIXED_LOG = 11;
 template <int KMAX, bool LAST, int LR = 0>
-__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(KMAX == 3 ? 2 : 3)))
+__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(LR > 0 || KMAX != 3 ? 3 : 2)))
 void k_ntt_pass(PassGeo g, PassIO io) {
   quotient_priority();
   extern __shared__ uint32_t smem[];
@@ -372,7 +468,7 @@ void k_ntt_pass(PassGeo g, PassIO io) {
   tc.smask = tc.logT >= 5 ? 0u : (tc.logT >= 3 ? (32u >> tc.logT) - 1u : 7u);
   tc.cmask = (1u << tc.logT) - 1;
   tc.s = smem;
-  tc.tw = smem + NL * tc.E;
+  tc.tw = smem + (LR > 0 ? NTT_XPLANES : NL) * tc.E;
   tc.tid = threadIdx.x;
 
   const size_t boff = (size_t)blockIdx.y * g.n;
@@ -392,12 +488,16 @@ void k_ntt_pass(PassGeo g, PassIO io) {
     o.base = (size_t)o.v << g.logS1;
   }
 
-  uint32_t* twl = smem + NL * tc.E;
+  uint32_t* twl = (uint32_t*)tc.tw;
   for (uint32_t e = tc.tid; e < tc.half; e += tc.nthr) {
 #pragma unroll
     for (int l = 0; l < NL; l++) twl[l * tc.half + e] = io.twr[l * tc.half + e];
   }
   __syncthreads();
+  if constexpr (LR > 0) {
+    tile_fixed<KMAX, LAST, LR>(tc, g, io, src, dst, o);
+    return;
+  }
 
   const uint32_t nsteps = (tc.logR + KMAX - 1) / KMAX;
   const uint32_t klast = tc.logR - KMAX * (nsteps - 1);
@@ -778,9 +878,10 @@ static int ntt_exec(zk_context* ctx, const NttPlan* plan, const NttCall& c, hipS
     const uint32_t kk = std::min<uint32_t>((uint32_t)kmax, g.logR);
     const uint32_t threads = std::max<uint32_t>(1, E >> kk);
     const uint32_t tiles = (uint32_t)(n / E);
-    const size_t lds = (size_t)NL * 4 * (E + (1u << (g.logR - 1)));
+    const bool fixed = kmax == 3 && E == (1u << NTT_TILE_FIXED_LOG) && threads == (E >> 3) && g.logR >= 6 &&
+                       g.logR <= 8;
+    const size_t lds = (size_t)4 * ((fixed ? NTT_XPLANES : NL) * E + NL * (1u << (g.logR - 1)));
     const dim3 grid(tiles, c.batch), block(threads);
-    const bool fixed = kmax == 3 && E == (1u << NTT_TILE_FIXED_LOG) && threads == (E >> 3);
     if (fixed && g.logR == 8) {
       if (last)
         ZK_LAUNCH(ctx, st, "ntt_pass", (k_ntt_pass<3, true, 8>), grid, block, lds, g, io);
