@@ -1,9 +1,36 @@
 // Context, device memory and kernel-timing entry points of the C ABI.
 #include <string.h>
 
+#include <atomic>
+
 #include "zk_internal.hpp"
 
 using namespace zk;
+
+namespace zk {
+// Allocations left until the injected failure (0: none armed).
+static std::atomic<int> g_fail_at{0};
+
+hipError_t dev_malloc(void** p, size_t bytes) {
+  int n = g_fail_at.load();
+  while (n > 0) {
+    if (g_fail_at.compare_exchange_weak(n, n - 1)) {
+      if (n == 1) {
+        *p = nullptr;
+        return hipErrorOutOfMemory;
+      }
+      break;
+    }
+  }
+  return hipMalloc(p, bytes);
+}
+}  // namespace zk
+
+int zk_debug_fail_device_alloc(int nth) {
+  if (nth < 0) return ZK_ERR_INVALID;
+  g_fail_at.store(nth);
+  return ZK_OK;
+}
 
 int zk_context::ensure(DevBuf& b, size_t bytes) {
   if (b.bytes >= bytes) return ZK_OK;
@@ -13,7 +40,7 @@ int zk_context::ensure(DevBuf& b, size_t bytes) {
     b.bytes = 0;
   }
   if (bytes == 0) return ZK_OK;
-  if (hipMalloc(&b.p, bytes) != hipSuccess) {
+  if (dev_malloc(&b.p, bytes) != hipSuccess) {
     b.p = nullptr;
     return fail(ZK_ERR_OOM, "device allocation failed");
   }

@@ -732,7 +732,7 @@ static int plan_get(zk_context* ctx, int log_n, NttPlan** out, hipStream_t st) {
   plan_init(p.get(), log_n);
   const size_t words = plan_table_words(pass_shape(log_n), log_n);
   void* mem = nullptr;
-  if (hipMalloc(&mem, words * 4) != hipSuccess) return ctx->fail(ZK_ERR_OOM, "NTT table allocation failed");
+  if (dev_malloc(&mem, words * 4) != hipSuccess) return ctx->fail(ZK_ERR_OOM, "NTT table allocation failed");
   plan_place(p.get(), (uint32_t*)mem);
   // Tables are filled on the caller's stream and waited for before the plan
   // is cached, so a later call on any stream finds them complete.
@@ -774,7 +774,7 @@ static int coset_get(zk_context* ctx, int log_n, uint64_t g, const NttPlan* plan
   const size_t n = (size_t)1 << log_n;
   std::unique_ptr<CosetTables> c(new CosetTables());
   void* mem = nullptr;
-  if (hipMalloc(&mem, 3 * n * PACKED_WORDS * 4) != hipSuccess)
+  if (dev_malloc(&mem, 3 * n * PACKED_WORDS * 4) != hipSuccess)
     return ctx->fail(ZK_ERR_OOM, "coset table allocation failed");
   uint32_t* w = (uint32_t*)mem;
   c->pre = FrTable{w, n};

@@ -36,6 +36,11 @@ struct DevBuf {
   size_t bytes = 0;
 };
 
+// hipMalloc for the library's own device memory (workspaces, NTT plan and
+// coset tables).  Fails without allocating while a test has armed
+// zk_debug_fail_device_alloc.
+hipError_t dev_malloc(void** p, size_t bytes);
+
 struct NttPlan;
 struct MsmWorkspace;
 

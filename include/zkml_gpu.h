@@ -72,6 +72,11 @@ int zk_dev_free(zk_context* ctx, void* d_ptr);
 int zk_memcpy_h2d(zk_context* ctx, void* d_dst, const void* h_src, size_t bytes);
 int zk_memcpy_d2h(zk_context* ctx, void* h_dst, const void* d_src, size_t bytes);
 int zk_memcpy_d2d(zk_context* ctx, void* d_dst, const void* d_src, size_t bytes);
+/* Test hook, no counterpart in the reference: the nth device allocation
+ * from now that the library makes for its own workspaces and NTT tables
+ * (1 = the next one) fails with ZK_ERR_OOM, once; 0 disarms.  For tests of
+ * the error paths only; affects every context of the process. */
+int zk_debug_fail_device_alloc(int nth);
 
 /* Per-kernel timing with HIP events recorded on the stream each kernel is
  * launched on (off by default).  Names: see zk_kernel_stats_names(). */
