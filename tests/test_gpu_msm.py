@@ -307,6 +307,20 @@ def test_msm_g2_vs_oracle(ctx, n):
     assert np.array_equal(got, oracle_msm(pts, sc, g2=True))
 
 
+def test_msm_g2_all_equal_scalars(ctx):
+    """G2, every scalar equal at 2^16: each window's one bucket spans more
+    than 1024 chunks, so a standalone G2 MSM takes the tree combine on lane
+    pairs (the proofs take it on split lanes).  Closed form (s sum k_i) G2."""
+    n = 1 << 16
+    rng = np.random.default_rng(17)
+    ks = from_std_arr(rand_std(n, rng))
+    s = 0xFEDCBA9876543210FEDCBA9876543210
+    dp = gpu_points(ctx, to_mont(std_words(ks)), g2=True)
+    ds = ctx.upload(to_mont(std_words([s] * n)))
+    got = ctx.msm_g2(dp, ds, n)
+    assert Z.g2_from_words(got) == Z.g2.pmul(Z.G2, sum(ks) * s % Z.R)
+
+
 @pytest.mark.parametrize("log_n,dist", [(14, "witness"), (16, "uniform"), (16, "witness"), (22, "uniform")])
 def test_msm_g2_closed_form(ctx, log_n, dist):
     """G2 MSM over Q_i = k_i G2 against (sum k_i s_i) G2: the proof sizes of
