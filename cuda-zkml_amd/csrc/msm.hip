@@ -70,6 +70,9 @@ constexpr uint32_t MSM_TREE_SPAN = ZK_MSM_TREE_SPAN;
 #ifndef ZK_MSM_G2_L0_SHIFT
 #define ZK_MSM_G2_L0_SHIFT 0
 #endif
+#ifndef ZK_MSM_G2_ONE_LANE
+#define ZK_MSM_G2_ONE_LANE 1
+#endif
 #ifndef ZK_MSM_G2_ACC_WAVES
 #define ZK_MSM_G2_ACC_WAVES 3
 #endif
@@ -808,6 +811,27 @@ __device__ __forceinline__ bool load_rec_lanes(const uint4* __restrict__ recs, u
   return any == 0;
 }
 
+__device__ __forceinline__ bool load_rec_lanes(const uint4* __restrict__ recs, uint32_t idx, fq2& x, fq2& y) {
+  return load_rec(recs, idx, x, y);
+}
+
+// One lane per G2 chunk (the whole Fq2 accumulator in one lane): ~14% fewer
+// instructions per addition than a lane pair (no lane swaps or selects), but
+// 2 waves per SIMD instead of 3.  Used for the largest G2 MSMs, where the
+// accumulation is throughput-bound.
+template <class F>
+struct OneLane {
+  typedef F R;
+  static constexpr int N = 1;
+  __device__ static xyzz<F> load(const xyzz<F>& p) { return p; }
+  __device__ static void store(xyzz<F>& p, const xyzz<F>& v) { p = v; }
+};
+
+template <class LN>
+constexpr int acc_waves() {
+  return sizeof(typename LN::R) == sizeof(fq) ? 4 : sizeof(typename LN::R) == sizeof(fq2) ? 2 : ZK_MSM_G2_ACC_WAVES;
+}
+
 // Chunk ch covers sorted positions [ch*L0, ch*L0 + L0) of window
 // ch / chunks_per_window; positions past the window's entry count are empty.
 // blockIdx.y selects the base set; its buckets start at set * nbuckets.  A
@@ -821,8 +845,8 @@ __device__ __forceinline__ bool load_rec_lanes(const uint4* __restrict__ recs, u
 // sit in a few windows (small witness values fill the low ones); in chunk
 // order those windows' waves would land on a fraction of the CUs, scattered
 // they spread over all of them.
-template <class F, bool TAB>
-__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(sizeof(F) == sizeof(fq) ? 4 : ZK_MSM_G2_ACC_WAVES))) void k_msm_accumulate(const uint2* __restrict__ sorted, BaseSets sets,
+template <class F, bool TAB, class LN = Lanes<F>>
+__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(acc_waves<LN>()))) void k_msm_accumulate(const uint2* __restrict__ sorted, BaseSets sets,
                                                         const uint32_t* __restrict__ start,
                                                         const uint32_t* __restrict__ end,
                                                         const uint32_t* __restrict__ wstat, uint32_t nchunks,
@@ -830,7 +854,6 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(sizeof(F) =
                                                         size_t nbuckets, xyzz<F>* __restrict__ buckets,
                                                         ChunkSlots<F> all_slots, uint32_t nwaves,
                                                         uint32_t wave_mul) {
-  typedef Lanes<F> LN;
   typedef typename LN::R R;
   constexpr uint32_t PER_WAVE = 64 / LN::N;  // chunks per wave
   msm_accumulate_priority<F>();
@@ -1548,16 +1571,30 @@ static int msm_accumulate(zk_context* ctx, MsmWorkspace& ws, const MsmShape& sh,
   ZK_TRY(ctx->ensure(ws.hpt, (size_t)nsets * nchunks * sizeof(xyzz<F>)));
   ZK_TRY(ctx->ensure(ws.tpt, (size_t)nsets * nchunks * sizeof(xyzz<F>)));
   ChunkSlots<F> slots{(uint32_t*)ws.hkey.p, (uint32_t*)ws.tkey.p, (xyzz<F>*)ws.hpt.p, (xyzz<F>*)ws.tpt.p};
-  const uint32_t gxl = cdiv((size_t)nchunks * Lanes<F>::N, 256);  // accumulation: Lanes<F>::N lanes per chunk
-  const uint32_t nwaves = cdiv((size_t)nchunks * Lanes<F>::N, 64);
-  if (sets.pstride)
+  // lanes per chunk: G1 one, G2 a lane pair, or one for the longest chunks
+  // (the largest G2 MSMs, throughput-bound)
+  const bool one_lane = G2 && ZK_MSM_G2_ONE_LANE && L0 >= (uint32_t)MSM_L0;
+  const uint32_t lanes = one_lane ? 1 : Lanes<F>::N;
+  const uint32_t gxl = cdiv((size_t)nchunks * lanes, 256);
+  const uint32_t nwaves = cdiv((size_t)nchunks * lanes, 64);
+  if (one_lane) {
+    if (sets.pstride)
+      ZK_LAUNCH(ctx, st, "msm_accumulate", (k_msm_accumulate<F, true, OneLane<F>>), dim3(gxl, nsets), dim3(256), 0,
+                sorted, sets, start, end, wstat, nchunks, ap.cpw, sh.n_pad, L0, nbuckets, buckets, slots, nwaves,
+                wave_scatter(nwaves));
+    else
+      ZK_LAUNCH(ctx, st, "msm_accumulate", (k_msm_accumulate<F, false, OneLane<F>>), dim3(gxl, nsets), dim3(256), 0,
+                sorted, sets, start, end, wstat, nchunks, ap.cpw, sh.n_pad, L0, nbuckets, buckets, slots, nwaves,
+                wave_scatter(nwaves));
+  } else if (sets.pstride) {
     ZK_LAUNCH(ctx, st, "msm_accumulate", (k_msm_accumulate<F, true>), dim3(gxl, nsets), dim3(256), 0, sorted, sets,
               start, end, wstat, nchunks, ap.cpw, sh.n_pad, L0, nbuckets, buckets, slots, nwaves,
               wave_scatter(nwaves));
-  else
+  } else {
     ZK_LAUNCH(ctx, st, "msm_accumulate", (k_msm_accumulate<F, false>), dim3(gxl, nsets), dim3(256), 0, sorted, sets,
               start, end, wstat, nchunks, ap.cpw, sh.n_pad, L0, nbuckets, buckets, slots, nwaves,
               wave_scatter(nwaves));
+  }
   // The chunk combine and the bucket reduction are chains of dependent
   // additions.  Few of their waves are busy at once (the combine's active
   // chunks are the spanning runs), so they deal each point operation to two
