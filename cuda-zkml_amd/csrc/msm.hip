@@ -1578,14 +1578,16 @@ static int msm_accumulate(zk_context* ctx, MsmWorkspace& ws, const MsmShape& sh,
   const uint32_t gxl = cdiv((size_t)nchunks * lanes, 256);
   const uint32_t nwaves = cdiv((size_t)nchunks * lanes, 64);
   if (one_lane) {
-    if (sets.pstride)
-      ZK_LAUNCH(ctx, st, "msm_accumulate", (k_msm_accumulate<F, true, OneLane<F>>), dim3(gxl, nsets), dim3(256), 0,
-                sorted, sets, start, end, wstat, nchunks, ap.cpw, sh.n_pad, L0, nbuckets, buckets, slots, nwaves,
-                wave_scatter(nwaves));
-    else
-      ZK_LAUNCH(ctx, st, "msm_accumulate", (k_msm_accumulate<F, false, OneLane<F>>), dim3(gxl, nsets), dim3(256), 0,
-                sorted, sets, start, end, wstat, nchunks, ap.cpw, sh.n_pad, L0, nbuckets, buckets, slots, nwaves,
-                wave_scatter(nwaves));
+    if constexpr (G2) {
+      if (sets.pstride)
+        ZK_LAUNCH(ctx, st, "msm_accumulate", (k_msm_accumulate<F, true, OneLane<F>>), dim3(gxl, nsets), dim3(256), 0,
+                  sorted, sets, start, end, wstat, nchunks, ap.cpw, sh.n_pad, L0, nbuckets, buckets, slots, nwaves,
+                  wave_scatter(nwaves));
+      else
+        ZK_LAUNCH(ctx, st, "msm_accumulate", (k_msm_accumulate<F, false, OneLane<F>>), dim3(gxl, nsets), dim3(256),
+                  0, sorted, sets, start, end, wstat, nchunks, ap.cpw, sh.n_pad, L0, nbuckets, buckets, slots, nwaves,
+                  wave_scatter(nwaves));
+    }
   } else if (sets.pstride) {
     ZK_LAUNCH(ctx, st, "msm_accumulate", (k_msm_accumulate<F, true>), dim3(gxl, nsets), dim3(256), 0, sorted, sets,
               start, end, wstat, nchunks, ap.cpw, sh.n_pad, L0, nbuckets, buckets, slots, nwaves,
