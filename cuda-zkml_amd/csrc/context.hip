@@ -118,6 +118,9 @@ void zk_destroy(zk_context* ctx) {
   for (DevBuf* b : {&ctx->scratch_a, &ctx->scratch_b, &ctx->scratch_c, &ctx->scratch_d})
     if (b->p) (void)hipFree(b->p);
   if (ctx->h_flag) (void)hipHostFree(ctx->h_flag);
+  if (ctx->h_stage) (void)hipHostFree(ctx->h_stage);
+  for (hipEvent_t e : ctx->stage_ev)
+    if (e) (void)hipEventDestroy(e);
   if (ctx->g1_table) (void)hipFree(ctx->g1_table);
   if (ctx->g2_table) (void)hipFree(ctx->g2_table);
   (void)hipStreamDestroy(ctx->stream);

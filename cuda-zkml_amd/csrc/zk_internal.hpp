@@ -82,6 +82,9 @@ struct zk_context {
   hipStream_t job_stream[zk::ZK_JOBS] = {};
   zk::MsmWorkspace* job_ws[zk::ZK_JOBS] = {};
   uint32_t* h_flag = nullptr;  // pinned word: the proof's witness-check count
+  // pinned staging slots of large host-to-device uploads (zk_prove's witness)
+  uint8_t* h_stage = nullptr;
+  hipEvent_t stage_ev[4] = {};
   // profiling
   bool profiling = false;
   std::string profile_only;  // when set, only kernels of this name are timed
