@@ -62,7 +62,7 @@ constexpr uint32_t MSM_SERIAL_SPAN = 8;  // longest serial chunk-partial chain o
 constexpr uint32_t MSM_COMBINE_S = 2;
 // Spans above which the tree combine replaces the level combine.
 #ifndef ZK_MSM_TREE_SPAN
-#define ZK_MSM_TREE_SPAN 1024
+#define ZK_MSM_TREE_SPAN 512
 #endif
 constexpr uint32_t MSM_TREE_SPAN = ZK_MSM_TREE_SPAN;
 // G2 accumulation tuning: chunk length divided by 2^ZK_MSM_G2_L0_SHIFT (down

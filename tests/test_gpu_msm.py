@@ -309,7 +309,7 @@ def test_msm_g2_vs_oracle(ctx, n):
 
 def test_msm_g2_all_equal_scalars(ctx):
     """G2, every scalar equal at 2^16: each window's one bucket spans more
-    than 1024 chunks, so a standalone G2 MSM takes the tree combine on lane
+    than 512 chunks, so a standalone G2 MSM takes the tree combine on lane
     pairs (the proofs take it on split lanes).  Closed form (s sum k_i) G2."""
     n = 1 << 16
     rng = np.random.default_rng(17)
