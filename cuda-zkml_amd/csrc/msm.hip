@@ -2053,6 +2053,25 @@ int msm_recs_ws(zk_context* ctx, MsmWorkspace* ws, bool g2, const void* d_recs, 
   return msm_run_recs<fq>(ctx, *ws, (const uint4*)d_recs, d_scalars, n, out, st, beside);
 }
 
+// Records of n points for MSMs over one base set, converted once (the
+// conversion k_msm_convert otherwise runs on every standalone MSM call).
+int msm_points_to_recs(zk_context* ctx, bool g2, const void* d_points, size_t n, void* d_recs, hipStream_t st) {
+  if (n == 0) return ZK_OK;
+  if (!d_points || !d_recs) return ctx->fail(ZK_ERR_INVALID, "msm: null buffer");
+  if (n > MSM_MAX_N) return ctx->fail(ZK_ERR_SIZE, "msm: n above 2^26");
+  const size_t bytes = n * (size_t)(g2 ? Rec<fq2>::WORDS : Rec<fq>::WORDS) * 4;
+  const uintptr_t p0 = (uintptr_t)d_points, r0 = (uintptr_t)d_recs;
+  if (p0 < r0 + bytes && r0 < p0 + bytes) return ctx->fail(ZK_ERR_INVALID, "msm: records overlap the points");
+  if (g2) {
+    ZK_LAUNCH(ctx, st, "msm_convert", k_msm_convert<fq2>, dim3(cdiv(n, 256)), dim3(256), 0, (uint4*)d_recs,
+              (const uint32_t*)d_points, n);
+  } else {
+    ZK_LAUNCH(ctx, st, "msm_convert", k_msm_convert<fq>, dim3(cdiv(n, 256)), dim3(256), 0, (uint4*)d_recs,
+              (const uint32_t*)d_points, n);
+  }
+  return ZK_OK;
+}
+
 int msm_g1_recs(zk_context* ctx, const void* d_recs, const void* d_scalars, size_t n, uint64_t out[8],
                 hipStream_t st) {
   if (!ctx->msm_ws) ctx->msm_ws = new MsmWorkspace();
@@ -2120,6 +2139,34 @@ static int zk_msm_g2_impl(zk_context* ctx, const void* d_points, const void* d_s
 
 int zk_msm_g2(zk_context* ctx, const void* d_points, const void* d_scalars, size_t n, void* h_result, void* stream) {
   return zk::guard(ctx, [&] { return zk_msm_g2_impl(ctx, d_points, d_scalars, n, h_result, stream); });
+}
+
+size_t zk_msm_record_bytes(int g2) { return (size_t)(g2 ? zk::Rec<zk::fq2>::WORDS : zk::Rec<zk::fq>::WORDS) * 4; }
+
+int zk_msm_prepare_points(zk_context* ctx, const void* d_points, size_t n, int g2, void* d_recs, void* stream) {
+  if (!ctx) return ZK_ERR_INVALID;
+  return zk::guard(ctx, [&] { return zk::msm_points_to_recs(ctx, g2 != 0, d_points, n, d_recs, ctx->s(stream)); });
+}
+
+static int zk_msm_prepared_impl(zk_context* ctx, bool g2, const void* d_recs, const void* d_scalars, size_t n,
+                                void* h_result, void* stream) {
+  if (!ctx || !h_result) return ZK_ERR_INVALID;
+  if (n > 0 && (!d_recs || !d_scalars)) {
+    memset(h_result, 0, g2 ? 128 : 64);
+    return ctx->fail(ZK_ERR_INVALID, "msm: null buffer");
+  }
+  if (g2) return zk::msm_g2_recs(ctx, d_recs, d_scalars, n, (uint64_t*)h_result, ctx->s(stream));
+  return zk::msm_g1_recs(ctx, d_recs, d_scalars, n, (uint64_t*)h_result, ctx->s(stream));
+}
+
+int zk_msm_g1_prepared(zk_context* ctx, const void* d_recs, const void* d_scalars, size_t n, void* h_result,
+                       void* stream) {
+  return zk::guard(ctx, [&] { return zk_msm_prepared_impl(ctx, false, d_recs, d_scalars, n, h_result, stream); });
+}
+
+int zk_msm_g2_prepared(zk_context* ctx, const void* d_recs, const void* d_scalars, size_t n, void* h_result,
+                       void* stream) {
+  return zk::guard(ctx, [&] { return zk_msm_prepared_impl(ctx, true, d_recs, d_scalars, n, h_result, stream); });
 }
 
 int zk_msm_config(size_t n, int g2, int* window_bits, int* windows) {

@@ -187,6 +187,7 @@ int msm_g1_run(zk_context* ctx, const void* d_points, const void* d_scalars, siz
 int msm_g2_run(zk_context* ctx, const void* d_points, const void* d_scalars, size_t n, uint64_t out_affine[16],
                hipStream_t st);
 // MSM over prepared point records (proving-key queries stay in this form)
+int msm_points_to_recs(zk_context* ctx, bool g2, const void* d_points, size_t n, void* d_recs, hipStream_t st);
 int msm_g1_recs(zk_context* ctx, const void* d_recs, const void* d_scalars, size_t n, uint64_t out_affine[8],
                 hipStream_t st);
 int msm_g2_recs(zk_context* ctx, const void* d_recs, const void* d_scalars, size_t n, uint64_t out_affine[16],

@@ -71,6 +71,11 @@ def lib():
         L.zk_coset_ntt.argtypes = [vp, vp, vp, ctypes.c_int, ctypes.c_uint64, ctypes.c_int, ctypes.c_int, vp]
         L.zk_msm_g1.argtypes = [vp, vp, vp, ctypes.c_size_t, vp, vp]
         L.zk_msm_g2.argtypes = [vp, vp, vp, ctypes.c_size_t, vp, vp]
+        L.zk_msm_record_bytes.argtypes = [ctypes.c_int]
+        L.zk_msm_record_bytes.restype = ctypes.c_size_t
+        L.zk_msm_prepare_points.argtypes = [vp, vp, ctypes.c_size_t, ctypes.c_int, vp, vp]
+        L.zk_msm_g1_prepared.argtypes = [vp, vp, vp, ctypes.c_size_t, vp, vp]
+        L.zk_msm_g2_prepared.argtypes = [vp, vp, vp, ctypes.c_size_t, vp, vp]
         L.zk_msm_config.argtypes = [ctypes.c_size_t, ctypes.c_int, ctypes.POINTER(ctypes.c_int),
                                     ctypes.POINTER(ctypes.c_int)]
         L.zk_msm_g1_host.argtypes = [vp, vp, vp, ctypes.c_int, vp]
@@ -275,6 +280,25 @@ class Context:
     def msm_g2(self, d_points, d_scalars, n):
         out = np.zeros(16, dtype=np.uint64)
         self._check(lib().zk_msm_g2(self.h, vp(d_points.ptr), vp(d_scalars.ptr), n, _np_ptr(out), None), "zk_msm_g2")
+        return out
+
+    def msm_prepare(self, d_points, n, g2=False):
+        """Point records of n points for repeated MSMs (zk_msm_prepare_points)."""
+        d_recs = self.alloc(max(1, n) * lib().zk_msm_record_bytes(int(g2)))
+        self._check(lib().zk_msm_prepare_points(self.h, vp(d_points.ptr), n, int(g2), vp(d_recs.ptr), None),
+                    "zk_msm_prepare_points")
+        return d_recs
+
+    def msm_g1_prepared(self, d_recs, d_scalars, n):
+        out = np.zeros(8, dtype=np.uint64)
+        self._check(lib().zk_msm_g1_prepared(self.h, vp(d_recs.ptr), vp(d_scalars.ptr), n, _np_ptr(out), None),
+                    "zk_msm_g1_prepared")
+        return out
+
+    def msm_g2_prepared(self, d_recs, d_scalars, n):
+        out = np.zeros(16, dtype=np.uint64)
+        self._check(lib().zk_msm_g2_prepared(self.h, vp(d_recs.ptr), vp(d_scalars.ptr), n, _np_ptr(out), None),
+                    "zk_msm_g2_prepared")
         return out
 
     def kzg_commit(self, d_srs, d_coeffs, degree):

@@ -129,6 +129,22 @@ int zk_msm_g1(zk_context* ctx, const void* d_points, const void* d_scalars, size
 int zk_msm_g2(zk_context* ctx, const void* d_points, const void* d_scalars, size_t n, void* h_result,
               void* stream);
 
+/* MSMs over one base set, its conversion done once.  No counterpart in the
+ * reference (bn254::msm_g1 / msm_g2 read affine points on every call); for
+ * callers that run many MSMs over the same points.  zk_msm_prepare_points
+ * writes the n points (zk_g1_affine, or zk_g2_affine when g2 != 0) as the
+ * MSM's point records into d_recs, zk_msm_record_bytes(g2) bytes per point;
+ * d_recs must not overlap d_points (ZK_ERR_INVALID).  zk_msm_g1_prepared /
+ * zk_msm_g2_prepared then give the same result as zk_msm_g1 / zk_msm_g2 over
+ * those points, without the per-call conversion; the records stay valid
+ * while d_recs is unchanged. */
+size_t zk_msm_record_bytes(int g2);
+int zk_msm_prepare_points(zk_context* ctx, const void* d_points, size_t n, int g2, void* d_recs, void* stream);
+int zk_msm_g1_prepared(zk_context* ctx, const void* d_recs, const void* d_scalars, size_t n, void* h_result,
+                       void* stream);
+int zk_msm_g2_prepared(zk_context* ctx, const void* d_recs, const void* d_scalars, size_t n, void* h_result,
+                       void* stream);
+
 /* Window configuration the MSM uses for n points (replaces
  * bn254::MSMConfig::for_size, src/msm/msm.cuh:40-64): window bits c (the
  * widest window) and the number of signed-digit windows.  CPU only. */

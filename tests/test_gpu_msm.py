@@ -336,6 +336,40 @@ def test_msm_g2_closed_form(ctx, log_n, dist):
     assert Z.g2_from_words(got) == Z.g2.pmul(Z.G2, closed_form_scalar(kstd, sstd))
 
 
+# ------------------------------------------------------------------ converted once
+@pytest.mark.parametrize("g2,log_n", [(False, 0), (False, 10), (False, 16), (False, 20), (True, 10), (True, 16)])
+def test_msm_prepared_records(ctx, g2, log_n):
+    """zk_msm_prepare_points + zk_msm_g*_prepared: over points P_i = k_i G
+    the result equals zk_msm_g* over the same points and the closed form
+    (sum k_i s_i) G, for two scalar vectors in a row over the same records,
+    the second over a shorter prefix."""
+    n = 1 << log_n
+    rng = np.random.default_rng(700 + log_n + 50 * g2)
+    kstd = rand_std(n, rng)
+    dp = gpu_points(ctx, to_mont(kstd), g2=g2)
+    drecs = ctx.msm_prepare(dp, n, g2=g2)
+    G, from_words = (Z.g2, Z.g2_from_words) if g2 else (Z.g1, Z.g1_from_words)
+    base = Z.G2 if g2 else Z.G1
+    run, run_prep = (ctx.msm_g2, ctx.msm_g2_prepared) if g2 else (ctx.msm_g1, ctx.msm_g1_prepared)
+    for m in (n, max(1, n // 3)):
+        sstd = rand_std(m, rng)
+        ds = ctx.upload(to_mont(sstd))
+        print(f"[msm prepared {'g2' if g2 else 'g1'} 2^{log_n} m={m}]", flush=True)
+        got = run_prep(drecs, ds, m)
+        assert np.array_equal(got, run(dp, ds, m))
+        assert from_words(got) == G.pmul(base, closed_form_scalar(kstd[:m], sstd))
+
+
+def test_msm_prepare_rejects_overlap(ctx):
+    """Records written over their own points are refused before any launch."""
+    import zkml_amd
+    n = 64
+    dp = gpu_points(ctx, to_mont(rand_std(n, np.random.default_rng(1))))
+    st = zkml_amd.lib().zk_msm_prepare_points(ctx.h, zkml_amd.vp(dp.ptr), n, 0, zkml_amd.vp(dp.ptr + 64), None)
+    with pytest.raises(zkml_amd.ZkError, match="overlap"):
+        ctx._check(st, "zk_msm_prepare_points")
+
+
 # ------------------------------------------------------------------ host-pointer drop-in
 def test_msm_g1_host_reference_layout(ctx):
     """zk_msm_g1_host takes the reference's 72-byte G1Affine structs and
