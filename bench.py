@@ -70,6 +70,15 @@ def host_cpu():
         info["model"] = next((l.split(":", 1)[1].strip() for l in txt.splitlines() if l.startswith("model name")), None)
     except OSError:
         pass
+    try:  # lscpu's identification lines, as printed
+        import subprocess
+        out = subprocess.run(["lscpu"], capture_output=True, text=True, timeout=20).stdout
+        keep = ("Model name", "Vendor ID", "CPU family", "Model", "Stepping", "Thread(s) per core",
+                "Core(s) per socket", "Socket(s)", "CPU max MHz", "L3 cache", "Hypervisor vendor")
+        info["lscpu"] = {k.strip(): v.strip() for k, v in (l.split(":", 1) for l in out.splitlines() if ":" in l)
+                         if k.strip() in keep}
+    except (OSError, ValueError, subprocess.SubprocessError):
+        pass
     return info
 
 
@@ -408,14 +417,22 @@ def main():
         if kept:
             nc, nv, npub, A, B, C, w = kept["stmt"]
             oc = OracleR1CS(nc, nv, npub, kept["npriv"], [(M["row"], M["col"], M["value"]) for M in (A, B, C)])
-            prove_cpu = {}
-            for threads in sorted({1, all_threads}):
-                t0 = time.perf_counter()
-                rc, proof_o, _ = oc.prove(kept["pk_path"], w, 0xCAFEBABE, threads=threads)
-                dt = time.perf_counter() - t0
-                prove_cpu[threads] = {"ms": round(dt * 1e3, 1), "equals_gpu": rc == 0 and proof_o == kept["proof"]}
-                log(f"[bench] CPU prove config 4, {threads} threads: {dt * 1e3:.0f} ms, equals GPU: "
-                    f"{prove_cpu[threads]['equals_gpu']}")
+            # G2 as the reference computes it (every G2 operation through affine
+            # coordinates, src/curve/g2.cuh:103-146) and as Jacobian formulas
+            # (~12x faster for B): same proof bytes either way
+            prove_cpu = {"reference_affine_g2": {}, "jacobian_g2": {}}
+            for g2_ref in (True, False):
+                key = "reference_affine_g2" if g2_ref else "jacobian_g2"
+                for threads in sorted({1, all_threads}):
+                    t0 = time.perf_counter()
+                    rc, proof_o, ms_o = oc.prove(kept["pk_path"], w, 0xCAFEBABE, threads=threads,
+                                                 g2_affine_ref=g2_ref)
+                    dt = time.perf_counter() - t0
+                    prove_cpu[key][str(threads)] = {
+                        "ms": round(dt * 1e3, 1), "equals_gpu": rc == 0 and proof_o == kept["proof"],
+                        "phases_ms": {k_: round(float(v), 1) for k_, v in zip(("h", "A", "B_g2", "C"), ms_o)}}
+                    log(f"[bench] CPU prove config 4 ({key}), {threads} threads: {dt * 1e3:.0f} ms, equals GPU: "
+                        f"{prove_cpu[key][str(threads)]['equals_gpu']}")
         top = msm_cpu[all_threads]
         cpu = {"value": top["Mpoints_per_s"], "unit": "Mpoints/s", "cores": all_threads, "kind": "port",
                "sample": f"G1 MSM over the same 2^{args.log_n} points/scalars, reference Pippenger (MSMConfig "
@@ -423,8 +440,7 @@ def main():
                          f"{top['s']} s on {all_threads} threads",
                "single_thread": msm_cpu[1], "all_threads": top,
                "ntt_2_22_ms": {"1": ntt_cpu[1], str(all_threads): ntt_cpu[all_threads]},
-               "prove_2_16_ms": None if prove_cpu is None else {"1": prove_cpu[1],
-                                                                str(all_threads): prove_cpu[all_threads]},
+               "prove_2_16_ms": prove_cpu,
                "host": host_cpu()}
     work.cleanup()
 

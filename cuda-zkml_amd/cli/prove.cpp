@@ -16,12 +16,16 @@
 // "Proving time: %.2f ms", checks the proof against the verification key and
 // exits 0 only if it verifies, as the reference does.  Output defaults are the
 // reference's: proof.bin, vk.bin, public_inputs.bin.
+// Seeds follow the reference's contract: the setup's toxic waste comes from a
+// fresh random 64-bit seed unless ZKML_DETERMINISTIC_SETUP=1 selects
+// 0xDEADBEEF42 (groth16.cu:455-462); --toxic-seed overrides both.
 // ZKML_DETERMINISTIC_PROVE=1 selects the blinding seed 0xCAFEBABE and
 // ZKML_SKIP_WITNESS_CHECK=1 skips the R1CS check (groth16.cu:687-718).
 #include <stdlib.h>
 #include <unistd.h>
 
 #include <algorithm>
+#include <chrono>
 #include <random>
 #include <string>
 #include <vector>
@@ -57,7 +61,8 @@ static void usage() {
   printf("Keys:\n");
   printf("  --pk-load FILE            ZKMLPK3 proving key; --vk names its verification key\n");
   printf("  --pk-save FILE            run the setup (GPU) and keep the proving key (default: temporary)\n");
-  printf("  --toxic-seed S            setup toxic-waste seed (default 0xDEADBEEF42)\n");
+  printf("  --toxic-seed S            setup toxic-waste seed (default: random; 0xDEADBEEF42 with\n");
+  printf("                            ZKML_DETERMINISTIC_SETUP=1)\n");
   printf("Outputs:\n");
   printf("  --output FILE             256-byte proof (default proof.bin)\n");
   printf("  --vk FILE                 verification key (default vk.bin)\n");
@@ -70,6 +75,20 @@ static void usage() {
   printf("  --repeat K                prove K times and report the median (default 1)\n");
   printf("  --device D                GPU ordinal (default 0)\n");
   printf("  --help\n");
+}
+
+static bool env_is_1(const char* name) {
+  const char* v = getenv(name);
+  return v && !strcmp(v, "1");
+}
+
+// A fresh 64-bit seed: the OS entropy source mixed with the clock, as the
+// reference's random_seed64 (groth16.cu:39-46) does for its setup.
+static uint64_t fresh_seed64() {
+  std::random_device rd;
+  const uint64_t hi = ((uint64_t)rd() << 32) ^ (uint64_t)rd();
+  const uint64_t t = (uint64_t)std::chrono::high_resolution_clock::now().time_since_epoch().count();
+  return hi ^ t ^ 0x9E3779B97F4A7C15ULL;
 }
 
 static bool parse_u64(const char* s, uint64_t& v) {
@@ -127,8 +146,8 @@ int main(int argc, char** argv) {
   const char *vk = "vk.bin", *out = "proof.bin", *pub_out = "public_inputs.bin";
   const char *exp_r1cs = nullptr, *exp_wtns = nullptr;
   long synthetic = -1, syn_pub = 4, syn_inputs = 16, repeat = 1, device = 0;
-  uint64_t syn_seed = 42, toxic = 0xDEADBEEF42ULL, seed = 0;
-  bool have_seed = false;
+  uint64_t syn_seed = 42, toxic = 0, seed = 0;
+  bool have_seed = false, have_toxic = false;
   // statement v2
   bool v2 = false, integer_model = false, integer_input = false, route = false;
   const char *model_path = nullptr, *arch_path = nullptr, *input_path = nullptr, *meta_path = nullptr;
@@ -216,7 +235,10 @@ int main(int argc, char** argv) {
       else if (a == "--repeat") repeat = std::max<long>(1, (long)u);
       else if (a == "--device") device = (long)u;
       else if (a == "--synthetic-seed") syn_seed = u;
-      else if (a == "--toxic-seed") toxic = u;
+      else if (a == "--toxic-seed") {
+        toxic = u;
+        have_toxic = true;
+      }
       else {
         seed = u;
         have_seed = true;
@@ -398,6 +420,15 @@ int main(int argc, char** argv) {
       key_path = buf.data();
       temp_key = true;
     }
+    // The seed is the whole toxic waste, so a random one is never printed.
+    const char* mode = "explicit";
+    if (!have_toxic) {
+      const bool det = env_is_1("ZKML_DETERMINISTIC_SETUP");
+      toxic = det ? 0xDEADBEEF42ULL : fresh_seed64();
+      mode = det ? "deterministic" : "randomized";
+    }
+    if (!strcmp(mode, "randomized")) printf("[Setup] RNG seed: (randomized, not shown)\n");
+    else printf("[Setup] RNG seed: 0x%016llx (%s)\n", (unsigned long long)toxic, mode);
     cli::Timer ts;
     const int st = zk_setup(ctx, rc, toxic, key_path.c_str(), vk);
     if (st != ZK_OK && temp_key) unlink(key_path.c_str());
@@ -413,8 +444,7 @@ int main(int argc, char** argv) {
   printf("Proving key loaded in %.2f ms\n", tk.ms());
   // ---- prove
   if (!have_seed) {
-    const char* det = getenv("ZKML_DETERMINISTIC_PROVE");
-    if (det && !strcmp(det, "1")) {
+    if (env_is_1("ZKML_DETERMINISTIC_PROVE")) {
       seed = 0xCAFEBABEULL;
     } else {
       std::random_device rd;

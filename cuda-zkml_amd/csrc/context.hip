@@ -26,6 +26,24 @@ hipError_t dev_malloc(void** p, size_t bytes) {
 }
 }  // namespace zk
 
+namespace zk {
+// Host-thread starts left to refuse (0: none armed).
+static std::atomic<int> g_fail_threads{0};
+
+bool debug_thread_start_refused() {
+  int n = g_fail_threads.load();
+  while (n > 0)
+    if (g_fail_threads.compare_exchange_weak(n, n - 1)) return true;
+  return false;
+}
+}  // namespace zk
+
+int zk_debug_fail_thread_start(int count) {
+  if (count < 0) return ZK_ERR_INVALID;
+  g_fail_threads.store(count);
+  return ZK_OK;
+}
+
 int zk_debug_fail_device_alloc(int nth) {
   if (nth < 0) return ZK_ERR_INVALID;
   g_fail_at.store(nth);

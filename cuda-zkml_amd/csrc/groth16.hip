@@ -13,6 +13,7 @@
 #include <functional>
 #include <mutex>
 #include <random>
+#include <system_error>
 #include <thread>
 #include <vector>
 
@@ -581,7 +582,7 @@ static MsmTab table_shape(size_t n, int wlarge, int sub = ZK_PK_TAB_SUB) {
 static int pk_table(zk_context* ctx, bool g2, const void* recs, size_t count, const MsmTab& t, void** out) {
   *out = nullptr;
   if (count == 0) return ZK_OK;
-  if (hipMalloc(out, msm_table_bytes(g2, count, t)) != hipSuccess) {
+  if (dev_malloc(out, msm_table_bytes(g2, count, t)) != hipSuccess) {
     *out = nullptr;
     return ctx->fail(ZK_ERR_OOM, "proving key: window table allocation failed");
   }
@@ -938,11 +939,16 @@ constexpr size_t GATE_G1_MIN_N = (size_t)1 << 21;
   ThreadJoiner joiner{workers};
   GateRelease gate_release{quotient_done};
   const std::function<void()> jobs[3] = {job(f_b2, rc_b2), job(f_g1, rc_g1), job(f_pre, rc_pre)};
+  // A job whose thread cannot be started runs on this thread once the
+  // quotient is enqueued and its gate is set: the gated G1 job waits for
+  // that gate, so running it here first would wait forever.
+  std::vector<const std::function<void()>*> inline_jobs;
   for (const std::function<void()>& fn : jobs) {
     try {
+      if (debug_thread_start_refused()) throw std::system_error(std::make_error_code(std::errc::resource_unavailable_try_again));
       workers.emplace_back(fn);
     } catch (...) {
-      fn();  // no thread available: run it here
+      inline_jobs.push_back(&fn);
     }
   }
   int qrc = quotient_run(ctx, c, d_w, d_h, ctx->scratch_b.p, st, check_witness != 0, d_bad);
@@ -956,6 +962,7 @@ constexpr size_t GATE_G1_MIN_N = (size_t)1 << 21;
   }
   if (qrc == ZK_OK && hipEventRecord(ev[2], st) != hipSuccess) qrc = ctx->fail(ZK_ERR_HIP, "prove: event record");
   quotient_done.state.store(qrc == ZK_OK ? 1 : 2);
+  for (const std::function<void()>* fn : inline_jobs) (*fn)();
   if (qrc == ZK_OK) {  // H after the quotient, same stream
     record(4 + 2 * JOB_H, st, rc_h);
     if (rc_h == ZK_OK && nh && pk->tH)

@@ -1036,15 +1036,21 @@ int quotient_ntts(zk_context* ctx, void* d_h, void* d_abc, void* d_work, int log
 // zk_ntt_noalloc runs the same kernels with its twiddle tables and its
 // pass-to-pass buffer in `scratch`, a fixed device array of this library:
 // every GPU holds one copy from module load to process end, and every call
-// on that GPU shares it (the tables of the last log_n stay there, so a call
-// of the same size only launches the passes; calls that overlap on one GPU
-// race).  Limits: 2^NTT_NA_MAX_LOG points per transform and
-// 2^NTT_NA_MAX_ELEMS_LOG elements per call.
+// on that GPU shares it (calls that overlap on one GPU race on the buffer).
+// Each log_n has its own table slot, filled by the first call of that size
+// and never written with other values, so a call never depends on which
+// sizes ran before it; a call on a stream under graph capture always puts
+// the (idempotent) fill into the graph, so a replay finds its tables whatever
+// ran between capture and replay.  Limits: 2^NTT_NA_MAX_LOG points per
+// transform and 2^NTT_NA_MAX_ELEMS_LOG elements per call.
 constexpr int NTT_NA_MAX_LOG = 16;
 constexpr int NTT_NA_MAX_ELEMS_LOG = 18;
-// tables of the largest plan (log_n = 16: two passes of 2^8, a 2^16-entry
-// inter-pass table per direction) and the pass-to-pass buffer, in words
-constexpr size_t NTT_NA_TABLE_WORDS = 2 * 2 * 128 * NL + 2 * ((size_t)1 << 16) * PACKED_WORDS;
+// the table slots of log_n = 1..16: each plan has at most 3 passes of at most
+// 2^8 rows (2 * 128 DFT twiddles of NL words per direction and pass) and
+// inter-pass tables of at most 2^log_n packed entries per direction; the exact
+// layout is checked against this bound at set-up (ntt_scratch_init)
+constexpr size_t NTT_NA_TABLE_WORDS =
+    NTT_NA_MAX_LOG * 3 * 2 * 128 * NL + 2 * (((size_t)2 << NTT_NA_MAX_LOG) - 2) * PACKED_WORDS;
 constexpr size_t NTT_NA_MID_WORDS = ((size_t)1 << NTT_NA_MAX_ELEMS_LOG) * 8;
 constexpr size_t NTT_NA_WORDS = NTT_NA_TABLE_WORDS + NTT_NA_MID_WORDS;
 
@@ -1054,7 +1060,20 @@ constexpr int NTT_NA_DEVICES = 64;
 static std::mutex g_na_mu;
 static uint32_t* g_na_ptr[NTT_NA_DEVICES];   // device address of `scratch` per GPU
 static int g_na_status[NTT_NA_DEVICES];      // 0 not looked up, 1 ok, -1 lookup failed
-static int g_na_log_n[NTT_NA_DEVICES];       // log_n whose tables `scratch` holds (0: none)
+static uint32_t g_na_filled[NTT_NA_DEVICES]; // bit log_n: that slot's tables are complete
+static size_t g_na_slot[NTT_NA_MAX_LOG + 2]; // word offset of the slot of log_n (slot 17: end)
+
+// Word offsets of the per-log_n table slots; false if they overrun the bound.
+static bool na_slots_layout() {
+  size_t off = 0;
+  for (int k = 1; k <= NTT_NA_MAX_LOG; k++) {
+    g_na_slot[k] = off;
+    off += plan_table_words(pass_shape(k), k);
+    off = (off + 63) & ~(size_t)63;  // 256-byte aligned slots
+  }
+  g_na_slot[NTT_NA_MAX_LOG + 1] = off;
+  return off <= NTT_NA_TABLE_WORDS;
+}
 
 // Once per device, with that device current (zk_create): the device address
 // of `scratch`.  The host-side name `scratch` is no device address; kernels
@@ -1065,12 +1084,10 @@ int ntt_scratch_init(int device) {
   if (g_na_status[device] != 0) return g_na_status[device] > 0 ? ZK_OK : ZK_ERR_HIP;
   void* p = nullptr;
   const hipError_t e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
-  g_na_status[device] = (e == hipSuccess && p) ? 1 : -1;
+  g_na_status[device] = (e == hipSuccess && p && na_slots_layout()) ? 1 : -1;
   g_na_ptr[device] = g_na_status[device] > 0 ? (uint32_t*)p : nullptr;
   return g_na_status[device] > 0 ? ZK_OK : ZK_ERR_HIP;
 }
-
-static_assert(NTT_NA_TABLE_WORDS >= 2 * 2 * 128 * NL, "scratch holds every plan up to 2^16");
 
 int ntt_run_noalloc(zk_context* ctx, void* d_out, const void* d_in, int log_n, int inverse, int batch,
                     hipStream_t st) {
@@ -1079,26 +1096,29 @@ int ntt_run_noalloc(zk_context* ctx, void* d_out, const void* d_in, int log_n, i
     return ctx->fail(ZK_ERR_SIZE, "ntt_noalloc: log_n outside [1, 16] (the fixed scratch holds 2^16-point plans)");
   if (((size_t)batch << log_n) > ((size_t)1 << NTT_NA_MAX_ELEMS_LOG))
     return ctx->fail(ZK_ERR_SIZE, "ntt_noalloc: batch * 2^log_n above 2^18 elements (the fixed scratch's buffer)");
+  hipStreamCaptureStatus cap = hipStreamCaptureStatusNone;
+  if (hipStreamIsCapturing(st, &cap) != hipSuccess) return ctx->fail(ZK_ERR_HIP, "ntt_noalloc: capture status");
+  const bool capturing = cap != hipStreamCaptureStatusNone;
   const int dev = ctx->device;
   uint32_t* base;
-  bool fill;
+  bool filled;
   {
     std::lock_guard<std::mutex> lk(g_na_mu);
     if (dev < 0 || dev >= NTT_NA_DEVICES || g_na_status[dev] <= 0)
       return ctx->fail(ZK_ERR_HIP, "ntt_noalloc: scratch address of this device unknown");
     base = g_na_ptr[dev];
-    fill = g_na_log_n[dev] != log_n;
-    g_na_log_n[dev] = log_n;
+    filled = (g_na_filled[dev] >> log_n) & 1u;
   }
   NttPlan plan;
   plan_init(&plan, log_n);
-  plan_place(&plan, base);
-  if (fill) {
-    const int rc = plan_fill(ctx, &plan, st);
-    if (rc != ZK_OK) {
+  plan_place(&plan, base + g_na_slot[log_n]);
+  if (!filled || capturing) {
+    ZK_TRY(plan_fill(ctx, &plan, st));
+    // a fill recorded into a graph has not run yet: the slot stays unfilled
+    // for eager calls until one of them fills it
+    if (!capturing) {
       std::lock_guard<std::mutex> lk(g_na_mu);
-      g_na_log_n[dev] = 0;
-      return rc;
+      g_na_filled[dev] |= 1u << log_n;
     }
   }
   NttCall c{};

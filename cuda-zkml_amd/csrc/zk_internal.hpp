@@ -40,6 +40,9 @@ struct DevBuf {
 // coset tables).  Fails without allocating while a test has armed
 // zk_debug_fail_device_alloc.
 hipError_t dev_malloc(void** p, size_t bytes);
+// True when a test armed zk_debug_fail_thread_start and a refusal is left
+// (consumes it): the caller then behaves as if std::thread had thrown.
+bool debug_thread_start_refused();
 
 struct NttPlan;
 struct MsmWorkspace;

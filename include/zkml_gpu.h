@@ -77,6 +77,11 @@ int zk_memcpy_d2d(zk_context* ctx, void* d_dst, const void* d_src, size_t bytes)
  * (1 = the next one) fails with ZK_ERR_OOM, once; 0 disarms.  For tests of
  * the error paths only; affects every context of the process. */
 int zk_debug_fail_device_alloc(int nth);
+/* Test hook, no counterpart in the reference: the next `count` host threads
+ * that zk_prove would start for its MSM jobs are refused as if the system had
+ * none left, so the jobs run on the calling thread instead; 0 disarms.  For
+ * tests of that fallback only; affects every context of the process. */
+int zk_debug_fail_thread_start(int count);
 
 /* Per-kernel timing with HIP events recorded on the stream each kernel is
  * launched on (off by default).  Names: see zk_kernel_stats_names(). */
@@ -104,11 +109,13 @@ int zk_ntt(zk_context* ctx, void* d_out, const void* d_in, int log_n, int invers
  * that forbid hipMalloc).  Same transform, layouts and stream argument as
  * zk_ntt, with 1 <= log_n <= 16 and batch * 2^log_n <= 2^18 elements; larger
  * sizes return ZK_ERR_SIZE.  Allocates nothing: its twiddle tables and
- * pass-to-pass buffer live in a fixed device array of the library (13 MB per
+ * pass-to-pass buffer live in a fixed device array of the library (17 MB per
  * GPU, held from library load to process end) that every call on a GPU
- * shares and that keeps the last call's contents (the tables of the last
- * log_n are reused).  Calls that overlap on one GPU race: order them on one
- * stream or synchronize between them. */
+ * shares.  Each log_n has its own table slot, filled by the first call of
+ * that size; a call on a stream under graph capture records that fill into
+ * the graph, so replays do not depend on the calls made between capture and
+ * replay.  Calls that overlap on one GPU race on the pass-to-pass buffer:
+ * order them on one stream or synchronize between them. */
 int zk_ntt_noalloc(zk_context* ctx, void* d_out, const void* d_in, int log_n, int inverse, int batch, void* stream);
 
 /* Coset NTT as used by Groth16Prover::compute_h (src/prover/groth16.cu:350-383):

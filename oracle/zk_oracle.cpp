@@ -182,9 +182,8 @@ static inline uint64_t window_bits(const uint64_t* s, int w, int c) {
   return (s[limb] >> sh) & mask;
 }
 
-template <class E>
-static Jac<E> msm_pippenger(const Aff<E>* pts, const Fr* sc, int n, bool g2, int threads) {
-  typedef Jac<E> J;
+template <class E, class J = Jac<E>>
+static J msm_pippenger(const Aff<E>* pts, const Fr* sc, int n, bool g2, int threads) {
   if (n == 0) return J::identity();
   // CPU fallback for small n (msm.cu:330-339, 537-544)
   if (n <= (g2 ? 128 : 256)) {
@@ -225,6 +224,9 @@ static Jac<E> msm_pippenger(const Aff<E>* pts, const Fr* sc, int n, bool g2, int
 
 G1J msm_g1(const G1A* pts, const Fr* sc, int n, int threads) { return msm_pippenger<Fq>(pts, sc, n, false, threads); }
 G2J msm_g2(const G2A* pts, const Fr* sc, int n, int threads) { return msm_pippenger<Fq2>(pts, sc, n, true, threads); }
+G2Ref msm_g2_affine_ref(const G2A* pts, const Fr* sc, int n, int threads) {
+  return msm_pippenger<Fq2, G2Ref>(pts, sc, n, true, threads);
+}
 
 G1J msm_g1_naive(const G1A* pts, const Fr* sc, int n) {
   G1J r = G1J::identity();
@@ -472,7 +474,7 @@ void setup(const R1CS& c, uint64_t seed, ProvingKey& pk, VerifyingKey& vk, int t
 
 // groth16.cu:655-920 (group-element path, deterministic seed)
 Proof prove(const ProvingKey& pk, const R1CS& c, const std::vector<Fr>& w, uint64_t seed, int threads,
-            double* ms) {
+            double* ms, bool g2_affine_ref) {
   Proof pf;
   const int m = (int)w.size();
   if (m == 0 || m != c.num_variables) return pf;
@@ -491,10 +493,17 @@ Proof prove(const ProvingKey& pk, const R1CS& c, const std::vector<Fr>& w, uint6
   pf.A = A.to_affine();
   double t2 = now_ms();
   int nb = std::min(m, (int)pk.B_g2_query.size());
-  G2J B = G2J::from_affine(pk.beta_g2).add(nb > 0 ? msm_g2(pk.B_g2_query.data(), w.data(), nb, threads)
-                                                  : G2J::identity());
-  B = B.add(G2J::from_affine(pk.delta_g2).mul(s));
-  pf.B = B.to_affine();
+  if (g2_affine_ref) {  // groth16.cu:790-798 on the reference's G2 arithmetic
+    G2Ref B = G2Ref::from_affine(pk.beta_g2)
+                  .add(nb > 0 ? msm_g2_affine_ref(pk.B_g2_query.data(), w.data(), nb, threads) : G2Ref::identity());
+    B = B.add(G2Ref::from_affine(pk.delta_g2).mul(s));
+    pf.B = B.to_affine();
+  } else {
+    G2J B = G2J::from_affine(pk.beta_g2).add(nb > 0 ? msm_g2(pk.B_g2_query.data(), w.data(), nb, threads)
+                                                    : G2J::identity());
+    B = B.add(G2J::from_affine(pk.delta_g2).mul(s));
+    pf.B = B.to_affine();
+  }
   double t3 = now_ms();
   G1J C = G1J::identity();
   int npriv = std::min((int)pk.L_query.size(), m - 1 - pk.num_public);
@@ -888,7 +897,8 @@ void orc_g2_gen_batch(const uint64_t* k_mont, size_t n, uint64_t* o, int threads
   for (size_t i = 0; i < n; i++) put_g2(out[i], o + 16 * i);
 }
 
-// mode 0: reference Pippenger (with its n<=256 / n<=128 CPU fallback); 1: naive
+// mode 0: reference Pippenger (with its n<=256 / n<=128 CPU fallback); 1: naive;
+// 2 (G2 only): reference Pippenger on the reference's affine-inversion G2Ref
 void orc_msm_g1(const uint64_t* pts, const uint64_t* sc, size_t n, int mode, int threads, uint64_t* o) {
   std::vector<G1A> p(n);
   for (size_t i = 0; i < n; i++) p[i] = get_g1(pts + 8 * i);
@@ -898,6 +908,10 @@ void orc_msm_g1(const uint64_t* pts, const uint64_t* sc, size_t n, int mode, int
 void orc_msm_g2(const uint64_t* pts, const uint64_t* sc, size_t n, int mode, int threads, uint64_t* o) {
   std::vector<G2A> p(n);
   for (size_t i = 0; i < n; i++) p[i] = get_g2(pts + 16 * i);
+  if (mode == 2) {
+    put_g2(msm_g2_affine_ref(p.data(), (const Fr*)sc, (int)n, threads).to_affine(), o);
+    return;
+  }
   G2J r = mode == 1 ? msm_g2_naive(p.data(), (const Fr*)sc, (int)n) : msm_g2(p.data(), (const Fr*)sc, (int)n, threads);
   put_g2(r.to_affine(), o);
 }
@@ -976,6 +990,18 @@ int orc_setup(void* h, uint64_t seed, const char* pk_path, const char* vk_path, 
   return 0;
 }
 // Returns 0 and fills 256 bytes on success; ms[0..3] = h, A, B, C phases.
+// g2_affine_ref: the B term on the reference's affine-inversion G2 (same bytes).
+int orc_prove_g2mode(const char* pk_path, void* h, const uint64_t* w, size_t m, uint64_t seed, int threads,
+                     uint8_t* out, double* ms, int g2_affine_ref) {
+  ProvingKey pk;
+  if (!pk.load(pk_path)) return -1;
+  std::vector<Fr> wv(m);
+  memcpy(wv.data(), w, m * 32);
+  Proof pf = prove(pk, *(R1CS*)h, wv, seed, threads, ms, g2_affine_ref != 0);
+  if (!pf.valid) return -2;
+  pf.serialize(out);
+  return 0;
+}
 int orc_prove(const char* pk_path, void* h, const uint64_t* w, size_t m, uint64_t seed, int threads, uint8_t* out,
               double* ms) {
   ProvingKey pk;

@@ -319,6 +319,86 @@ typedef Jac<Fq> G1J;
 typedef Aff<Fq2> G2A;
 typedef Jac<Fq2> G2J;
 
+// The reference's own G2 arithmetic (src/curve/g2.cuh:88-146): Jacobian
+// storage, but every group operation converts its operands to affine (one
+// Fq2 inversion per operand, z = 1 included, as G2Jacobian::to_affine does)
+// and applies the affine chord/tangent formulas, whose slope is one more
+// inversion.  Same canonical affine results as Jac<Fq2>, at the reference's
+// cost; used for the timed CPU baseline of the reference's host algorithm.
+struct G2Ref {
+  Fq2 x, y, z;
+  static G2Ref identity() { return G2Ref{Fq2::zero(), Fq2::one(), Fq2::zero()}; }
+  static G2Ref from_affine(const G2A& p) {  // g2.cuh:90-93
+    if (p.inf) return identity();
+    return G2Ref{p.x, p.y, Fq2::one()};
+  }
+  bool is_inf() const { return z.is_zero(); }
+  G2A to_affine() const {  // g2.cuh:95-101
+    G2A a;
+    if (is_inf()) {
+      a.x = Fq2::zero();
+      a.y = Fq2::zero();
+      a.inf = true;
+      return a;
+    }
+    Fq2 zi = z.inv(), zi2 = zi.sqr(), zi3 = zi2 * zi;
+    a.x = x * zi2;
+    a.y = y * zi3;
+    a.inf = false;
+    return a;
+  }
+  static G2A inf_point() {
+    G2A a;
+    a.x = Fq2::zero();
+    a.y = Fq2::zero();
+    a.inf = true;
+    return a;
+  }
+  static G2A dbl_aff(const G2A& p) {  // g2.cuh:103-115: lambda = 3x^2 / 2y
+    if (p.inf || p.y.is_zero()) return inf_point();
+    Fq2 lambda = (p.x.sqr() + p.x.sqr() + p.x.sqr()) * (p.y + p.y).inv();
+    G2A r;
+    r.x = lambda.sqr() - p.x - p.x;
+    r.y = lambda * (p.x - r.x) - p.y;
+    r.inf = false;
+    return r;
+  }
+  static G2A add_aff(const G2A& p, const G2A& q) {  // g2.cuh:117-132
+    if (p.inf) return q;
+    if (q.inf) return p;
+    if (p.x == q.x) {
+      if (!(p.y == q.y)) return inf_point();
+      return dbl_aff(p);
+    }
+    Fq2 lambda = (q.y - p.y) * (q.x - p.x).inv();
+    G2A r;
+    r.x = lambda.sqr() - p.x - q.x;
+    r.y = lambda * (p.x - r.x) - p.y;
+    r.inf = false;
+    return r;
+  }
+  G2Ref dbl() const { return from_affine(dbl_aff(to_affine())); }                       // g2.cuh:134-136
+  G2Ref add(const G2Ref& o) const { return from_affine(add_aff(to_affine(), o.to_affine())); }  // :139-141
+  G2Ref add_affine(const G2A& o) const { return from_affine(add_aff(to_affine(), o)); }  // :144-146
+  // MSB-first double-and-add over the standard-form scalar (g2.cuh:153-190)
+  G2Ref mul(const Fr& k) const {
+    uint64_t s[4];
+    k.to_std(s);
+    G2Ref r = identity();
+    int top = -1;
+    for (int i = 255; i >= 0; i--)
+      if ((s[i >> 6] >> (i & 63)) & 1) {
+        top = i;
+        break;
+      }
+    for (int i = top; i >= 0; i--) {
+      r = r.dbl();
+      if ((s[i >> 6] >> (i & 63)) & 1) r = r.add(*this);
+    }
+    return r;
+  }
+};
+
 G1A g1_generator();  // (1, 2)            g1.cuh:40
 G2A g2_generator();  // EIP-197           g2.cuh:47-65
 
@@ -341,6 +421,8 @@ G1J msm_g1(const G1A* pts, const Fr* sc, int n, int threads);  // msm.cu:320-442
 G2J msm_g2(const G2A* pts, const Fr* sc, int n, int threads);  // msm.cu:526-598
 G1J msm_g1_naive(const G1A* pts, const Fr* sc, int n);        // tests/test_msm.cu:20-28
 G2J msm_g2_naive(const G2A* pts, const Fr* sc, int n);
+// msm_g2 on the reference's affine-inversion arithmetic (G2Ref)
+G2Ref msm_g2_affine_ref(const G2A* pts, const Fr* sc, int n, int threads);
 
 // ---------------------------------------------------------------- R1CS / Groth16
 struct Entry {  // src/prover/circuit.cuh:32-36
@@ -383,7 +465,9 @@ struct Proof {
 int qap_log_n(int num_constraints);  // groth16.cu:225-242
 std::vector<Fr> compute_h(const R1CS& c, const std::vector<Fr>& w, int threads);  // groth16.cu:263-390
 void setup(const R1CS& c, uint64_t seed, ProvingKey& pk, VerifyingKey& vk, int threads);  // groth16.cu:446-642
+// g2_affine_ref: B's MSM and s*delta2 on G2Ref (the reference's G2 cost)
+// instead of Jac<Fq2>; the proof is the same either way
 Proof prove(const ProvingKey& pk, const R1CS& c, const std::vector<Fr>& w, uint64_t seed, int threads,
-            double* ms_breakdown);  // groth16.cu:655-920
+            double* ms_breakdown, bool g2_affine_ref = false);  // groth16.cu:655-920
 
 }  // namespace orc

@@ -45,6 +45,8 @@ def oracle():
         lib.orc_compute_h.argtypes = [vp, vp, ctypes.c_size_t, vp, ctypes.c_int]
         lib.orc_setup.argtypes = [vp, ctypes.c_uint64, ctypes.c_char_p, ctypes.c_char_p, ctypes.c_int]
         lib.orc_prove.argtypes = [ctypes.c_char_p, vp, vp, ctypes.c_size_t, ctypes.c_uint64, ctypes.c_int, vp, vp]
+        lib.orc_prove_g2mode.argtypes = [ctypes.c_char_p, vp, vp, ctypes.c_size_t, ctypes.c_uint64, ctypes.c_int,
+                                         vp, vp, ctypes.c_int]
         lib.orc_msm_g1.argtypes = [vp, vp, ctypes.c_size_t, ctypes.c_int, ctypes.c_int, vp]
         lib.orc_msm_g2.argtypes = [vp, vp, ctypes.c_size_t, ctypes.c_int, ctypes.c_int, vp]
         lib.orc_g1_gen_batch.argtypes = [vp, ctypes.c_size_t, vp, ctypes.c_int]
@@ -132,11 +134,14 @@ class OracleR1CS:
         rc = self.lib.orc_setup(self.h, seed, pk_path.encode(), vk_path.encode(), threads)
         assert rc == 0, rc
 
-    def prove(self, pk_path, w, seed, threads=4):
+    def prove(self, pk_path, w, seed, threads=4, g2_affine_ref=False):
+        """g2_affine_ref: the B term on the reference's affine-inversion G2
+        arithmetic (src/curve/g2.cuh:103-146) instead of Jacobian G2."""
         w = np.ascontiguousarray(w, dtype=np.uint64)
         out = np.zeros(256, dtype=np.uint8)
         ms = np.zeros(4, dtype=np.float64)
-        rc = self.lib.orc_prove(pk_path.encode(), self.h, ptr(w), w.shape[0], seed, threads, ptr(out), ptr(ms))
+        rc = self.lib.orc_prove_g2mode(pk_path.encode(), self.h, ptr(w), w.shape[0], seed, threads, ptr(out),
+                                       ptr(ms), int(g2_affine_ref))
         return rc, out.tobytes(), ms
 
     def __del__(self):

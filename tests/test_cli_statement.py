@@ -8,6 +8,11 @@ inputs, builds the statement, checks the witness and writes --export-r1cs /
 exported files carry the quantized-model tag as a public input, so equal
 bytes pin the architecture parser, the int32 loader, the .npy / .bin input
 loaders, the hex parser and the tag together with the statement builder.
+The oracle/_ref comparisons run the reference's host code compiled in place
+with the reference's own CUDA-runtime test shim (tests/host/shim).  They are
+cross-checks and pin nothing by themselves: these tests skip without it, and the
+statement builder behind the front end is pinned without it in
+tests/test_statement_pins.py.
 """
 import os
 import re

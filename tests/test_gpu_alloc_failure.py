@@ -49,3 +49,58 @@ def test_table_allocation_failure_then_recovery(log_n):
     finally:
         _fail_at(0)
         ctx.close()
+
+
+def _free_bytes():
+    import ctypes
+    hip = ctypes.CDLL("libamdhip64.so")
+    free, total = ctypes.c_size_t(), ctypes.c_size_t()
+    assert hip.hipMemGetInfo(ctypes.byref(free), ctypes.byref(total)) == 0
+    return free.value
+
+
+def test_pk_window_table_allocation_failure_falls_back(tmp_path):
+    """zk_pk_load of a key with 2^15 variables builds window tables for its
+    queries (each table, then its temporary, in the order A, B1, L, B2, H).
+    A failed allocation of a table or of its temporary drops every table: the
+    load still succeeds, leaves no error behind and holds a fraction of the
+    tables' memory, and the next proof is byte-identical to a table-backed
+    proof and to the oracle's prove on the same key and seed."""
+    import zkml_amd
+    from test_gpu_groth16 import PROVE_SEED, SETUP_SEED, _oracle_of
+    ctx = zkml_amd.Context(0)
+    try:
+        nc, npub = (1 << 15) - 64, 4
+        A, B, C, w = zkml_amd.synthetic_r1cs(nc, npub, 16, 15)
+        r = ctx.r1cs(nc, w.shape[0], npub, A, B, C)
+        pk_path, vk_path = str(tmp_path / "pk.bin"), str(tmp_path / "vk.bin")
+        ctx.setup(r, SETUP_SEED, pk_path, vk_path)
+        ctx.sync()
+        before = _free_bytes()
+        pk = ctx.load_pk(pk_path)
+        with_tables = before - _free_bytes()
+        proof, _ = ctx.prove(pk, r, w, npub, PROVE_SEED)
+        pk.close()
+        # 1: A's table, 2: A's temporary, 7: B2's table, 10: H's temporary
+        for nth in (1, 2, 7, 10):
+            print(f"[pk tables] allocation {nth} fails", flush=True)
+            ctx.sync()
+            before = _free_bytes()
+            _fail_at(nth)
+            try:
+                pk = ctx.load_pk(pk_path)
+            finally:
+                _fail_at(0)
+            used = before - _free_bytes()
+            assert used < with_tables // 2, (nth, used, with_tables)
+            assert zkml_amd.lib().zk_last_error(ctx.h) in (None, b"")
+            again, _ = ctx.prove(pk, r, w, npub, PROVE_SEED)
+            assert again == proof, nth
+            pk.close()
+        oc = _oracle_of(A, B, C, nc, w.shape[0], npub)
+        rc, proof_o, _ = oc.prove(pk_path, w, PROVE_SEED, threads=16)
+        assert rc == 0 and proof_o == proof
+        r.close()
+    finally:
+        _fail_at(0)
+        ctx.close()

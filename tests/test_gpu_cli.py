@@ -8,7 +8,15 @@ Pins:
     again from those iden3 files with --pk-load gives the same 256 bytes;
   * the oracle's restatement of the reference prover gives the same 256 bytes
     for the same R1CS, witness, key and seed;
-  * exit code 1 and no proof acceptance for a tampered witness.
+  * exit code 1 and no proof acceptance for a tampered witness;
+  * the setup seed contract of the reference (groth16.cu:455-462): without
+    ZKML_DETERMINISTIC_SETUP two setups of one statement give different keys,
+    with ZKML_DETERMINISTIC_SETUP=1 the keys are byte-identical to the
+    oracle's setup at 0xDEADBEEF42, and --toxic-seed S to the oracle's at S.
+The oracle/_ref comparisons run the reference's host code compiled in place
+with the reference's own CUDA-runtime test shim (tests/host/shim).  They are
+cross-checks and pin nothing by themselves: the proofs are pinned by the oracle
+(same bytes) and verify under the product verifier.
 """
 import os
 import subprocess
@@ -24,11 +32,12 @@ ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
 PROVE = os.path.join(ROOT, "cuda-zkml_amd", "zkml-prove")
 VERIFY = os.path.join(ROOT, "cuda-zkml_amd", "zkml-verify")
 ENV = dict(os.environ, ZKML_DETERMINISTIC_PROVE="1")
+ENV.pop("ZKML_DETERMINISTIC_SETUP", None)
 
 
-def run(args, **kw):
+def run(args, env=None, **kw):
     print("[cli]", " ".join(os.path.basename(a) if a.startswith("/") else a for a in args), flush=True)
-    return subprocess.run(args, capture_output=True, text=True, env=ENV, timeout=240, **kw)
+    return subprocess.run(args, capture_output=True, text=True, env=env or ENV, timeout=240, **kw)
 
 
 def test_cli_synthetic_then_files(tmp_path):
@@ -104,3 +113,35 @@ def test_cli_statement_v2_end_to_end(tmp_path):
     json.dump(bad, open(t("bad.json"), "w"))
     v2 = run([VERIFY, "--vk", t("vk.bin"), "--proof", t("proof.bin"), "--public-inputs", t("bad.json")])
     assert v2.returncode == 1
+
+
+def test_cli_setup_seed_contract(tmp_path):
+    t = lambda name: str(tmp_path / name)
+    stmt = ["--synthetic", "400", "--synthetic-seed", "5"]
+
+    def setup(tag, env=None, extra=()):
+        r = run([PROVE, *stmt, "--pk-save", t(tag + ".pk"), "--vk", t(tag + ".vk"), "--output", t(tag + ".proof"),
+                 "--public-inputs", t(tag + ".pub"), "--export-r1cs", t("s.r1cs"), *extra], env=env)
+        assert r.returncode == 0, r.stdout + r.stderr
+        return r.stdout, open(t(tag + ".pk"), "rb").read(), open(t(tag + ".vk"), "rb").read()
+
+    out1, pk1, vk1 = setup("rand1")
+    out2, pk2, vk2 = setup("rand2")
+    assert "randomized" in out1 and "randomized" in out2
+    assert "DEADBEEF42" not in out1.upper()
+    assert vk1 != vk2 and pk1 != pk2, "two setups without ZKML_DETERMINISTIC_SETUP gave the same key"
+    outd, pkd, vkd = setup("det", env=dict(ENV, ZKML_DETERMINISTIC_SETUP="1"))
+    assert "0x000000deadbeef42 (deterministic)" in outd
+    oute, pke, vke = setup("explicit", extra=("--toxic-seed", "77"))
+    assert "(explicit)" in oute
+    # the oracle's setup of the same statement at the same seeds
+    nc, nv, npub, npriv, A, B, C = zkml_amd.iden3_r1cs_read(t("s.r1cs"))
+    oc = OracleR1CS(nc, nv, npub, npriv, [(M["row"], M["col"], M["value"].reshape(-1, 4)) for M in (A, B, C)])
+    for seed, pk, vk in ((0xDEADBEEF42, pkd, vkd), (77, pke, vke)):
+        oc.setup(seed, t("o.pk"), t("o.vk"))
+        assert open(t("o.vk"), "rb").read() == vk and open(t("o.pk"), "rb").read() == pk, hex(seed)
+    assert vk1 not in (vkd, vke) and vk2 not in (vkd, vke)
+    # every key gives a proof that verifies
+    for tag in ("rand1", "rand2", "det", "explicit"):
+        v = run([VERIFY, "--vk", t(tag + ".vk"), "--proof", t(tag + ".proof"), "--public-inputs", t(tag + ".pub")])
+        assert v.returncode == 0, tag + v.stdout + v.stderr

@@ -16,6 +16,10 @@ Pins:
     reference's own verifier code; a wrong public input rejected, an
     unsatisfying witness refused;
   * the reference's own T4 proving keys load with the reference checks.
+The oracle/_ref comparisons run the reference's host code compiled in place
+with the reference's own CUDA-runtime test shim (tests/host/shim).  They are
+cross-checks and pin nothing by themselves: the proofs are pinned by the oracle (itself
+pinned by closed forms) and the scalar-domain closed forms above.
 """
 import os
 import struct
@@ -240,7 +244,8 @@ def test_prove_2_22_config5_verifies(ctx, tmp_path):
     oracle's prove with the same key, witness and seed; it is accepted by the
     product's verifier (and by the reference's own code in oracle/_ref where
     built), a changed public input is rejected, and a second prove with the
-    same seed gives the same bytes."""
+    same seed, its MSM jobs run on the calling thread (thread starts refused
+    by the test hook), gives the same bytes."""
     import zkml_amd
     nc, npub = 1 << 22, 4
     A, B, C, w = zkml_amd.synthetic_r1cs(nc, npub, 16, 22)
@@ -252,7 +257,15 @@ def test_prove_2_22_config5_verifies(ctx, tmp_path):
     pk = ctx.load_pk(pk_path)
     print("[prove 2^22] prove", flush=True)
     proof, _ = ctx.prove(pk, r, w, npub, PROVE_SEED)
-    again, _ = ctx.prove(pk, r, w, npub, PROVE_SEED)
+    # again with every job thread refused: the jobs run on the calling thread
+    # after the quotient (the gated G1 job of this size would otherwise wait
+    # for a gate that only that thread opens)
+    print("[prove 2^22] prove with the job threads refused", flush=True)
+    assert zkml_amd.lib().zk_debug_fail_thread_start(3) == 0
+    try:
+        again, _ = ctx.prove(pk, r, w, npub, PROVE_SEED)
+    finally:
+        zkml_amd.lib().zk_debug_fail_thread_start(0)
     assert proof == again
     print("[prove 2^22] oracle prove", flush=True)
     oc = _oracle_of(A, B, C, nc, w.shape[0], npub)

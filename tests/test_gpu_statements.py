@@ -6,6 +6,10 @@ product's builder):
     the reference prover for the same key, witness and seed;
   * the proof verifies under the product's verifier and the reference's;
   * a wrong public input is rejected.
+The oracle/_ref comparisons run the reference's host code compiled in place
+with the reference's own CUDA-runtime test shim (tests/host/shim).  They are
+cross-checks and pin nothing by themselves: the proofs are pinned by the oracle
+and the statements by tests/test_statement_pins.py.
 """
 import os
 import time

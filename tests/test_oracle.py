@@ -16,6 +16,10 @@ Pins per oracle function (the function it checks in brackets):
                              wrong public input rejected
   ZKMLPK3 / VK / proof I/O   T4 golden files: reference verifier accepts the
                              T4 proofs; PK parse equals an independent parser
+The oracle/_ref comparisons run the reference's host code compiled in place
+with the reference's own CUDA-runtime test shim (tests/host/shim).  They are
+cross-checks and pin nothing by themselves: every oracle function also has a
+pin that needs no reference code (closed forms, KATs, T4 golden files).
 """
 import os
 import random
@@ -281,9 +285,39 @@ def test_msm_g2_closed_form(n):
     ks, ss, pts = msm_inputs(n, 100 + n, g2=True)
     sc = fr_array(ss)
     expect = Z.g2.pmul(Z.G2, sum(k * s for k, s in zip(ks, ss)) % Z.R)
-    o = np.zeros(16, dtype=np.uint64)
-    lib.orc_msm_g2(ptr(pts), ptr(sc), n, 0, 4, ptr(o))
-    assert Z.g2_from_words(o) == expect
+    for mode in (0, 2):  # Jacobian G2; the reference's affine-inversion G2
+        o = np.zeros(16, dtype=np.uint64)
+        lib.orc_msm_g2(ptr(pts), ptr(sc), n, mode, 4, ptr(o))
+        assert Z.g2_from_words(o) == expect, mode
+
+
+def test_msm_g2_affine_ref_special_cases():
+    """The reference's affine-inversion G2 (g2.cuh:103-146) through the
+    Pippenger path (n > 128) with a repeated point (bucket sums P + P take the
+    tangent), a negated point (P + -P gives infinity), an infinity point and
+    zero, one and r - 1 scalars: equal to the closed form and to Jacobian G2."""
+    lib = oracle()
+    n = 300
+    ks, ss, pts = msm_inputs(n, 9, g2=True)
+    ks[5], ks[6] = ks[4], Z.R - ks[4]
+    ss[5] = ss[4]
+    ss[6] = ss[4]
+    ks[10] = 0
+    ss[3], ss[7], ss[8] = 0, 1, Z.R - 1
+    ss[20] = ss[21] = ss[22] = 12345  # one bucket, three different points
+    fresh = np.zeros((3, 16), dtype=np.uint64)
+    lib.orc_g2_gen_batch(ptr(fr_array([ks[4], Z.R - ks[4], 1])), 3, ptr(fresh), 1)
+    pts[5], pts[6] = fresh[0], fresh[1]
+    pts[10] = 0
+    sc = fr_array(ss)
+    expect = Z.g2.pmul(Z.G2, sum(k * s for k, s in zip(ks, ss)) % Z.R)
+    got = {}
+    for mode in (0, 2):
+        o = np.zeros(16, dtype=np.uint64)
+        lib.orc_msm_g2(ptr(pts), ptr(sc), n, mode, 4, ptr(o))
+        got[mode] = o
+        assert Z.g2_from_words(o) == expect, mode
+    assert np.array_equal(got[0], got[2])
 
 
 @needs_ref
@@ -405,6 +439,19 @@ def test_oracle_groth16_verifies_with_reference(kind, tmp_path):
     assert proof2 == proof
     rc3, proof3, _ = oc.prove(pk, circ.witness_words(), 0xCAFEBABF)
     assert proof3 != proof
+
+
+def test_oracle_prove_affine_g2_same_bytes(tmp_path):
+    """The oracle's prove with B on the reference's affine-inversion G2 (the
+    timed CPU baseline's arithmetic) gives the same 256 bytes as with
+    Jacobian G2 (whose proofs the seed pins check against closed forms)."""
+    circ = random_r1cs(300, npub=3, seed=8)
+    oc = OracleR1CS(circ.nc, circ.nv, circ.npub, circ.npriv, circ.mats())
+    pk, vk = str(tmp_path / "pk.bin"), str(tmp_path / "vk.bin")
+    oc.setup(0xDEADBEEF42, pk, vk)
+    rc, proof, _ = oc.prove(pk, circ.witness_words(), 0xCAFEBABE)
+    rc2, proof2, _ = oc.prove(pk, circ.witness_words(), 0xCAFEBABE, g2_affine_ref=True)
+    assert rc == 0 and rc2 == 0 and proof == proof2
 
 
 # ------------------------------------------------------------------ T4 golden artefacts

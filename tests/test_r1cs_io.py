@@ -14,6 +14,10 @@ Pins:
   synthetic    the generated witness satisfies the R1CS under the oracle's
                checker and the reference's R1CS::verify_witness; determinism
                by seed; sizes as documented.
+The oracle/_ref comparisons run the reference's host code compiled in place
+with the reference's own CUDA-runtime test shim (tests/host/shim).  They are
+cross-checks and pin nothing by themselves: the codecs are pinned by the
+independent reader and the round trips.
 """
 import os
 import struct

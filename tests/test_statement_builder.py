@@ -16,6 +16,10 @@ Pins:
                a randomized sweep over layer mixes and statement options is
                byte-identical to the reference builder (oracle/_ref), metadata
                JSON and rejection messages included.
+The oracle/_ref comparisons run the reference's host code compiled in place
+with the reference's own CUDA-runtime test shim (tests/host/shim).  They are
+cross-checks and pin nothing by themselves: the builder is pinned without
+them by the committed fixtures here and by tests/test_statement_pins.py.
 """
 import hashlib
 import json

@@ -12,6 +12,10 @@ Pins:
                (all valid), a tampered proof, a wrong public input and a
                wrong public-input count; .json public inputs; a proof made by
                the oracle's restatement of the reference prover.
+The oracle/_ref comparisons run the reference's host code compiled in place
+with the reference's own CUDA-runtime test shim (tests/host/shim).  They are
+cross-checks and pin nothing by themselves: the pairing is pinned by bilinearity,
+non-degeneracy and e(O, Q) = 1, the verifier by the T4 golden proofs.
 """
 import json
 import os

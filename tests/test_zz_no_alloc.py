@@ -74,3 +74,73 @@ def test_noalloc_rejects_sizes_beyond_the_scratch(ctx):
     ctx.ntt(ref, d, 16, batch=2)
     ctx.sync()
     assert np.array_equal(ctx.d2h(o, a.shape), ctx.d2h(ref, a.shape))
+
+
+def test_noalloc_graph_replays_after_other_sizes(ctx):
+    """zk_ntt_noalloc captured into HIP graphs (one size whose tables were
+    already filled by an eager call, one whose first call is the captured
+    one), replayed three times each with eager calls of other sizes in
+    between: every replay equals zk_ntt, and so does an eager call of the
+    size first seen under capture."""
+    hip = ctypes.CDLL("libamdhip64.so")
+    vp = ctypes.c_void_p
+    rng = np.random.default_rng(29)
+    st = vp()
+    assert hip.hipStreamCreate(ctypes.byref(st)) == 0
+
+    def sync():
+        assert hip.hipStreamSynchronize(st) == 0
+
+    def call(d_out, d_in, log_n, inverse=0):
+        rc = zkml_amd.lib().zk_ntt_noalloc(ctx.h, vp(d_out.ptr), vp(d_in.ptr), log_n, inverse, 1, st)
+        assert rc == 0, zkml_amd.lib().zk_last_error(ctx.h)
+
+    def reference(d_in, log_n, inverse=0):
+        d = ctx.alloc(32 << log_n)
+        ctx.ntt(d, d_in, log_n, inverse=bool(inverse))
+        ctx.sync()
+        return ctx.d2h(d, (1 << log_n, 4))
+
+    def capture(d_out, d_in, log_n, inverse):
+        graph, exe = vp(), vp()
+        assert hip.hipStreamBeginCapture(st, 0) == 0  # global capture mode
+        call(d_out, d_in, log_n, inverse)
+        assert hip.hipStreamEndCapture(st, ctypes.byref(graph)) == 0
+        assert hip.hipGraphInstantiate(ctypes.byref(exe), graph, None, None, ctypes.c_size_t(0)) == 0
+        return graph, exe
+
+    cases = []
+    for log_n, inverse, eager_first in ((12, 0, True), (10, 1, False)):
+        a = zkml_amd.random_fr(1 << log_n, rng)
+        d_in, d_out = ctx.upload(a), ctx.alloc(a.nbytes)
+        if eager_first:
+            call(d_out, d_in, log_n, inverse)
+            sync()
+        print(f"[noalloc graph] capture log_n={log_n} inverse={inverse} eager_first={eager_first}", flush=True)
+        graph, exe = capture(d_out, d_in, log_n, inverse)
+        cases.append((log_n, inverse, d_in, d_out, graph, exe, reference(d_in, log_n, inverse)))
+    others = [13, 9, 16, 3]
+    try:
+        for rep in range(3):
+            for (log_n, inverse, d_in, d_out, graph, exe, want) in cases:
+                # an eager call of another size between the replays
+                o = others[(rep + log_n) % len(others)]
+                b = zkml_amd.random_fr(1 << o, rng)
+                db, ob = ctx.upload(b), ctx.alloc(b.nbytes)
+                call(ob, db, o)
+                sync()
+                assert np.array_equal(ctx.d2h(ob, b.shape), reference(db, o))
+                assert hip.hipMemsetAsync(vp(d_out.ptr), 0, ctypes.c_size_t(32 << log_n), st) == 0
+                assert hip.hipGraphLaunch(exe, st) == 0
+                sync()
+                assert np.array_equal(ctx.d2h(d_out, want.shape), want), (rep, log_n, inverse)
+        # the size first seen under capture, eagerly
+        log_n, inverse, d_in, d_out, _, _, want = cases[1]
+        call(d_out, d_in, log_n, inverse)
+        sync()
+        assert np.array_equal(ctx.d2h(d_out, want.shape), want)
+    finally:
+        for c in cases:
+            hip.hipGraphExecDestroy(c[5])
+            hip.hipGraphDestroy(c[4])
+        hip.hipStreamDestroy(st)
