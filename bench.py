@@ -42,7 +42,7 @@ sys.path.insert(0, os.path.join(ROOT, "tests"))
 PEAK_MAD_TOPS = 256 * 64 * 2.4e9 / 1e12
 PEAK_HBM_GBS = 8000.0
 R_ORDER = 0x30644E72E131A029B85045B68181585D2833E84879B9709143E1F593F0000001
-MADS_PER_FIELD_MUL = 136  # 8x32-bit CIOS: 2*8^2 + 8
+MADS_PER_FIELD_MUL = 136  # 8x32-bit CIOS Montgomery product: 2*8^2 + 8 word multiply-adds
 
 
 def log(msg):
@@ -50,7 +50,10 @@ def log(msg):
 
 
 def msm_algorithmic_mults(n, c):
-    """BASELINE.md F(N) with W = ceil(255/c) signed windows."""
+    """Algorithmic field multiplications of a G1 MSM of n points with c-bit
+    signed windows (W = ceil(255/c)): 10 per mixed addition of every point in
+    every window, 14 per bucket-reduction addition (2 per bucket), and 6c + 14
+    per window for the window combination."""
     w = -(-255 // c)
     return n * w * 10 + w * (1 << (c - 1)) * 2 * 14 + w * (6 * c + 14)
 
@@ -245,7 +248,7 @@ def main():
         pmc = {k_: prof.get(k_) for k_ in ("sq_insts_valu_per_launch", "sq_active_inst_valu_per_launch", "valu_busy",
                                             "clock_ghz", "lane_instructions_per_mixed_add")}
         pmc["source"] = "profiles/msm_2e20_pmc_traffic.md"
-    # whole-MSM VALU fraction with BASELINE.md's algorithmic count
+    # whole-MSM VALU fraction from the algorithmic multiplication count above
     f_mults = msm_algorithmic_mults(n, best_c(n))
     msm_frac = f_mults * MADS_PER_FIELD_MUL / (ms_step * 1e-3) / 1e12 / PEAK_MAD_TOPS
 
