@@ -434,6 +434,67 @@ __global__ __launch_bounds__(SORT_T) void k_msm_scatter(const uint32_t* __restri
   }
 }
 
+// The lanes of a wave that share `key` take their positions with one atomic
+// when all active lanes hold the same key (a hot bucket or bin), else one
+// atomic each; returns this lane's position.  KEY_INVALID lanes take none.
+__device__ __forceinline__ uint32_t wave_claim(uint32_t* ctr, uint32_t key, uint32_t idx) {
+  const uint32_t lead = __builtin_amdgcn_readfirstlane(key);
+  const uint64_t same = __ballot(key == lead);
+  uint32_t pos = 0;
+  if (same == __ballot(1) && lead != KEY_INVALID) {
+    const uint32_t rank = __builtin_amdgcn_mbcnt_hi((uint32_t)(same >> 32), __builtin_amdgcn_mbcnt_lo((uint32_t)same, 0u));
+    if (rank == 0) pos = atomicAdd(&ctr[idx], (uint32_t)__popcll(same));
+    pos = __builtin_amdgcn_readfirstlane(pos) + rank;
+  } else if (key != KEY_INVALID) {
+    pos = atomicAdd(&ctr[idx], 1u);
+  }
+  return pos;
+}
+
+// Tile-sorted writes of the placement.  A block takes its bin's entries in
+// tiles of TILE_E; each entry's bucket gives it a rank from LDS counters
+// (wave_claim), one wave turns the tile's counts into offsets, the entries are
+// staged in LDS in bucket order and written out by consecutive threads, so
+// every bucket's share of the tile leaves as one contiguous run (~32 entries
+// at 2^15 buckets) where entry-by-entry stores would each touch their own
+// cache line.
+constexpr int TILE_U = 4;
+constexpr int TILE_E = PLACE_T * TILE_U;  // entries per tile
+
+// Wave 0 only (threadIdx.x < 64): toff = exclusive scan of cnt[0, ns) (ns <=
+// 256), gbase = the buckets' global write positions for this tile (cur
+// advances by the counts), cnt cleared for the next tile, *tot = the tile's
+// entry count.
+__device__ __forceinline__ void tile_offsets(uint32_t* cnt, uint32_t* toff, uint32_t* gbase, uint32_t* cur,
+                                             uint32_t ns, uint32_t* tot) {
+  const uint32_t lane = threadIdx.x;
+  uint32_t c[4], sum = 0;
+#pragma unroll
+  for (int i = 0; i < 4; i++) {
+    const uint32_t j = lane * 4 + i;
+    c[i] = j < ns ? cnt[j] : 0u;
+    sum += c[i];
+  }
+  uint32_t inc = sum;
+  for (int off = 1; off < 64; off <<= 1) {
+    const uint32_t o = (uint32_t)__shfl_up((int)inc, off, 64);
+    if (lane >= (uint32_t)off) inc += o;
+  }
+  uint32_t ex = inc - sum;
+#pragma unroll
+  for (int i = 0; i < 4; i++) {
+    const uint32_t j = lane * 4 + i;
+    if (j < ns) {
+      toff[j] = ex;
+      gbase[j] = cur[j];
+      cur[j] += c[i];
+      cnt[j] = 0u;
+      ex += c[i];
+    }
+  }
+  if (lane == 63) *tot = inc;
+}
+
 // Two-pass placement for wide windows (B >= 2^13 buckets): one-pass random
 // 8-byte writes across the whole window region leave every cache line
 // partially written by many blocks.
@@ -492,50 +553,92 @@ __global__ __launch_bounds__(SORT_T) void k_msm_scatter_coarse(const uint32_t* _
 }
 
 // Pass 2 (block per window x coarse bin): LDS cursors for the bin's BPC
-// buckets; every write stays inside the bin's region.
+// buckets; every write stays inside the bin's region.  A bin whose largest
+// bucket holds at least half of its entries (the hot bucket of skewed
+// scalars) writes entry by entry: a wave's lanes then mostly share that
+// bucket and take consecutive positions with one atomic (wave_claim), so its
+// stores are contiguous already and the tile staging would only add barriers
+// on the one block that decides the launch's length.  Other bins go through
+// the tile-sorted writes above.
 __global__ __launch_bounds__(PLACE_T) void k_msm_place(const uint2* __restrict__ tmp, uint32_t B, uint32_t BPC,
                                                        const uint32_t* __restrict__ start,
-                                                       const uint32_t* __restrict__ end, uint2* __restrict__ out) {
+                                                       const uint32_t* __restrict__ end,
+                                                       const uint32_t* __restrict__ bmax, uint2* __restrict__ out) {
+  static_assert(MSM_BPC_MAX <= 256 && MSM_BPC_MAX <= SCAN_T, "one wave scans the bin's counters");
   msm_short_priority();
-  __shared__ uint32_t cur[MSM_BPC_MAX];
+  __shared__ uint32_t cur[MSM_BPC_MAX], cnt[MSM_BPC_MAX], toff[MSM_BPC_MAX], gbase[MSM_BPC_MAX], ttot;
+  __shared__ uint2 stg[TILE_E];
   const uint32_t cb = blockIdx.x, w = blockIdx.y, t = threadIdx.x;
   const uint32_t k0 = w * B + cb * BPC;
-  for (uint32_t j = t; j < BPC; j += PLACE_T) cur[j] = start[k0 + j];
   const uint32_t lo = start[k0], hi = end[k0 + BPC - 1];
+  for (uint32_t j = t; j < BPC; j += PLACE_T) {
+    cur[j] = start[k0 + j];
+    cnt[j] = 0u;
+  }
+  // the largest bucket of the column-scan block holding this bin (BPC <=
+  // SCAN_T: that block's buckets include the bin's), an upper bound of the
+  // bin's own largest bucket
+  const bool hot = 2u * bmax[k0 / SCAN_T] >= hi - lo;
   __syncthreads();
-  for (uint32_t p0 = lo + t; p0 < hi; p0 += PLACE_T * SORT_U) {
-    uint2 e[SORT_U];
+  if (hot) {
+    for (uint32_t p0 = lo + t; p0 < hi; p0 += PLACE_T * SORT_U) {
+      uint2 e[SORT_U];
 #pragma unroll
-    for (int u = 0; u < SORT_U; u++) {
-      const uint32_t p = p0 + u * PLACE_T;
-      e[u] = p < hi ? tmp[p] : make_uint2(KEY_INVALID, 0u);
-    }
-    // When every active lane of a wave holds the same bucket, the wave takes
-    // its positions with one atomic (order inside a bucket is free: its
-    // points are summed).  A hot bucket (the carry digit of small witness
-    // values can hold ~40% of all points) would otherwise serialize the CU's
-    // LDS on one counter.  All eight atomics are issued before any result is
-    // read, so their round trips overlap.
-    uint32_t pos[SORT_U], rank[SORT_U];
-    bool agg[SORT_U];
+      for (int u = 0; u < SORT_U; u++) {
+        const uint32_t p = p0 + u * PLACE_T;
+        e[u] = p < hi ? tmp[p] : make_uint2(KEY_INVALID, 0u);
+      }
+      // When every active lane of a wave holds the same bucket, the wave
+      // takes its positions with one atomic (order inside a bucket is free:
+      // its points are summed); a hot bucket would otherwise serialize the
+      // CU's LDS on one counter.  All eight atomics are issued before any
+      // result is read, so their round trips overlap.
+      uint32_t pos[SORT_U], rank[SORT_U];
+      bool agg[SORT_U];
 #pragma unroll
-    for (int u = 0; u < SORT_U; u++) {
-      const uint32_t key = e[u].x;
-      const uint32_t lead = __builtin_amdgcn_readfirstlane(key);
-      const uint64_t same = __ballot(key == lead);
-      agg[u] = same == __ballot(1) && lead != KEY_INVALID;
-      rank[u] = __builtin_amdgcn_mbcnt_hi((uint32_t)(same >> 32), __builtin_amdgcn_mbcnt_lo((uint32_t)same, 0u));
-      pos[u] = 0;
-      if (agg[u]) {
-        if (rank[u] == 0) pos[u] = atomicAdd(&cur[lead - k0], (uint32_t)__popcll(same));
-      } else if (key != KEY_INVALID) {
-        pos[u] = atomicAdd(&cur[key - k0], 1u);
+      for (int u = 0; u < SORT_U; u++) {
+        const uint32_t key = e[u].x;
+        const uint32_t lead = __builtin_amdgcn_readfirstlane(key);
+        const uint64_t same = __ballot(key == lead);
+        agg[u] = same == __ballot(1) && lead != KEY_INVALID;
+        rank[u] = __builtin_amdgcn_mbcnt_hi((uint32_t)(same >> 32), __builtin_amdgcn_mbcnt_lo((uint32_t)same, 0u));
+        pos[u] = 0;
+        if (agg[u]) {
+          if (rank[u] == 0) pos[u] = atomicAdd(&cur[lead - k0], (uint32_t)__popcll(same));
+        } else if (key != KEY_INVALID) {
+          pos[u] = atomicAdd(&cur[key - k0], 1u);
+        }
+      }
+#pragma unroll
+      for (int u = 0; u < SORT_U; u++) {
+        if (agg[u]) pos[u] = __builtin_amdgcn_readfirstlane(pos[u]) + rank[u];
+        if (e[u].x != KEY_INVALID) out[pos[u]] = e[u];
       }
     }
+    return;
+  }
+  for (uint32_t p0 = lo; p0 < hi; p0 += TILE_E) {
+    uint2 e[TILE_U];
+    uint32_t rank[TILE_U];
 #pragma unroll
-    for (int u = 0; u < SORT_U; u++) {
-      if (agg[u]) pos[u] = __builtin_amdgcn_readfirstlane(pos[u]) + rank[u];
-      if (e[u].x != KEY_INVALID) out[pos[u]] = e[u];
+    for (int u = 0; u < TILE_U; u++) {
+      const uint32_t p = p0 + t + u * PLACE_T;
+      e[u] = p < hi ? tmp[p] : make_uint2(KEY_INVALID, 0u);
+    }
+#pragma unroll
+    for (int u = 0; u < TILE_U; u++) rank[u] = wave_claim(cnt, e[u].x, e[u].x == KEY_INVALID ? 0 : e[u].x - k0);
+    __syncthreads();
+    if (t < 64) tile_offsets(cnt, toff, gbase, cur, BPC, &ttot);
+    __syncthreads();
+#pragma unroll
+    for (int u = 0; u < TILE_U; u++)
+      if (e[u].x != KEY_INVALID) stg[toff[e[u].x - k0] + rank[u]] = e[u];
+    __syncthreads();
+    const uint32_t nt = ttot;
+    for (uint32_t lp = t; lp < nt; lp += PLACE_T) {
+      const uint2 x = stg[lp];
+      const uint32_t j = x.x - k0;
+      out[gbase[j] + (lp - toff[j])] = x;
     }
   }
 }
@@ -549,23 +652,6 @@ __global__ __launch_bounds__(PLACE_T) void k_msm_place(const uint2* __restrict__
 // 2^22 proof: 256 bins of 2048 buckets placed 1.7 ms per MSM).
 constexpr int WIDE_NB = 1024;
 constexpr int WIDE_LOG_NB = 10;
-
-// The lanes of a wave that share `key` take their positions with one atomic
-// when all active lanes hold the same key (a hot bucket or bin), else one
-// atomic each; returns this lane's position.  KEY_INVALID lanes take none.
-__device__ __forceinline__ uint32_t wave_claim(uint32_t* ctr, uint32_t key, uint32_t idx) {
-  const uint32_t lead = __builtin_amdgcn_readfirstlane(key);
-  const uint64_t same = __ballot(key == lead);
-  uint32_t pos = 0;
-  if (same == __ballot(1) && lead != KEY_INVALID) {
-    const uint32_t rank = __builtin_amdgcn_mbcnt_hi((uint32_t)(same >> 32), __builtin_amdgcn_mbcnt_lo((uint32_t)same, 0u));
-    if (rank == 0) pos = atomicAdd(&ctr[idx], (uint32_t)__popcll(same));
-    pos = __builtin_amdgcn_readfirstlane(pos) + rank;
-  } else if (key != KEY_INVALID) {
-    pos = atomicAdd(&ctr[idx], 1u);
-  }
-  return pos;
-}
 
 // Pass 1a: coarse-bin counts of slice s -> cnt[bin * S + s].
 __global__ __launch_bounds__(SORT_T) void k_wide_count(const uint32_t* __restrict__ dig, size_t np, uint32_t slice,
@@ -1469,7 +1555,7 @@ static int msm_sort(zk_context* ctx, MsmWorkspace& ws, const MsmShape& sh, hipSt
     uint2* tmp = (uint2*)ws.tmp.p;
     ZK_LAUNCH(ctx, st, "msm_scatter", k_msm_scatter_coarse, dim3(S, W), dim3(SORT_T), 0, dig, n, slice, S, B, BPC,
               n_pad, hist, boff, lex, tot, start, end, tmp);
-    ZK_LAUNCH(ctx, st, "msm_place", k_msm_place, dim3(MSM_NCB, W), dim3(PLACE_T), 0, tmp, B, BPC, start, end,
+    ZK_LAUNCH(ctx, st, "msm_place", k_msm_place, dim3(MSM_NCB, W), dim3(PLACE_T), 0, tmp, B, BPC, start, end, bmax,
               sorted);
   }
   return ZK_OK;
