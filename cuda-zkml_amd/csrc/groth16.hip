@@ -167,21 +167,38 @@ G2 g2_from_words(const uint64_t* w) {
   if (inf) return G2::inf();
   return G2::affine(Fq2{Fq::raw(w), Fq::raw(w + 4)}, Fq2{Fq::raw(w + 8), Fq::raw(w + 12)});
 }
-void g1_to_words(const G1& p, uint64_t* w) {
-  Fq x, y;
-  memset(w, 0, 64);
-  if (!p.to_affine(x, y)) return;
-  memcpy(w, x.v, 32);
-  memcpy(w + 4, y.v, 32);
-}
-void g2_to_words(const G2& p, uint64_t* w) {
-  Fq2 x, y;
-  memset(w, 0, 128);
-  if (!p.to_affine(x, y)) return;
-  memcpy(w, x.c0.v, 32);
-  memcpy(w + 4, x.c1.v, 32);
-  memcpy(w + 8, y.c0.v, 32);
-  memcpy(w + 12, y.c1.v, 32);
+
+// Affine words of the three proof points with one field inversion: the
+// Jacobian z of A and C and the norm z0^2 + z1^2 of B's z (1 / z = conj(z) /
+// norm in Fq2) are inverted together (Montgomery's trick); a point at
+// infinity enters as 1 and is written as zeros.
+void proof_to_words(const G1& A, const G2& B, const G1& C, uint64_t* aw, uint64_t* bw, uint64_t* cw) {
+  const Fq one = Fq::one();
+  const Fq za = A.is_inf() ? one : A.z, zc = C.is_inf() ? one : C.z;
+  const Fq nb = B.is_inf() ? one : B.z.c0.sqr() + B.z.c1.sqr();
+  const Fq ac = za * zc;
+  const Fq inv = (ac * nb).inv();
+  const Fq ia = inv * zc * nb, ic = inv * za * nb, inb = inv * ac;
+  auto g1w = [](const G1& p, const Fq& zi, uint64_t* w) {
+    memset(w, 0, 64);
+    if (p.is_inf()) return;
+    const Fq zi2 = zi.sqr();
+    const Fq x = p.x * zi2, y = p.y * (zi2 * zi);
+    memcpy(w, x.v, 32);
+    memcpy(w + 4, y.v, 32);
+  };
+  g1w(A, ia, aw);
+  g1w(C, ic, cw);
+  memset(bw, 0, 128);
+  if (!B.is_inf()) {
+    const Fq2 zi{B.z.c0 * inb, -(B.z.c1 * inb)};
+    const Fq2 zi2 = zi.sqr();
+    const Fq2 x = B.x * zi2, y = B.y * (zi2 * zi);
+    memcpy(bw, x.c0.v, 32);
+    memcpy(bw + 4, x.c1.v, 32);
+    memcpy(bw + 8, y.c0.v, 32);
+    memcpy(bw + 12, y.c1.v, 32);
+  }
 }
 
 // Fr::from_uint(rng()) until nonzero (groth16.cu:48-58)
@@ -917,8 +934,9 @@ constexpr size_t GATE_G1_MIN_N = (size_t)1 << 21;
                              tab ? &pk->tab_w : nullptr, tab ? rows : nullptr);
     record(5 + 2 * JOB_G1, js, rc_g1);
     if (rc_g1 == ZK_OK) {
-      g1_tail = g1_from_words(a_msm).mul(s).add(g1_from_words(l_msm));
-      if (nb1 > 0) g1_tail = g1_tail.add(g1_from_words(b1_msm).mul(r));
+      const G1 sa_rb = nb1 > 0 ? G1::mul2(g1_from_words(a_msm), s, g1_from_words(b1_msm), r)
+                               : g1_from_words(a_msm).mul(s);
+      g1_tail = sa_rb.add(g1_from_words(l_msm));
     }
   };
   for (int j = 0; j < JOB_STREAMS; j++) ZK_HIP(ctx, hipStreamWaitEvent(ctx->job_stream[j], ev[1], 0));
@@ -989,9 +1007,7 @@ constexpr size_t GATE_G1_MIN_N = (size_t)1 << 21;
   const G2 B = pre_b.add(nb2 > 0 ? g2_from_words(b2_msm) : G2::inf());
   const G1 Cj = g1_tail.add(g1_from_words(h_msm)).add(pre_c);
   uint64_t Aw[8], Bw[16], Cw[8];
-  g1_to_words(A, Aw);
-  g2_to_words(B, Bw);
-  g1_to_words(Cj, Cw);
+  proof_to_words(A, B, Cj, Aw, Bw, Cw);
   // 256-byte serialization in standard form (groth16.cu:1058-1074)
   uint8_t* o = proof_out;
   auto put = [&](const uint64_t* mont) {

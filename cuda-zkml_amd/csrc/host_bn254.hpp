@@ -203,9 +203,26 @@ struct Jac {
     r.z = (y * z).dbl();
     return r;
   }
+  // Sum with a point whose z is one (an affine point): z2 = 1 drops three
+  // multiplications and a squaring from the general formula below.
+  Jac add_mixed(const Jac& o) const {
+    if (is_inf()) return o;
+    const E z1z1 = z.sqr();
+    const E u2 = o.x * z1z1, s2 = o.y * (z * z1z1);
+    const E h = u2 - x, rr = s2 - y;
+    if (h.is_zero()) return rr.is_zero() ? dbl() : inf();
+    const E hh = h.sqr(), hhh = hh * h, v = x * hh;
+    Jac r;
+    r.x = rr.sqr() - hhh - v.dbl();
+    r.y = rr * (v - r.x) - y * hhh;
+    r.z = z * h;
+    return r;
+  }
   Jac add(const Jac& o) const {
     if (is_inf()) return o;
     if (o.is_inf()) return *this;
+    if (o.z == E::one()) return add_mixed(o);
+    if (z == E::one()) return o.add_mixed(*this);
     E z1z1 = z.sqr(), z2z2 = o.z.sqr();
     E u1 = x * z2z2, u2 = o.x * z1z1;
     E s1 = y * o.z * z2z2, s2 = o.y * z * z1z1;
@@ -238,6 +255,26 @@ struct Jac {
     uint64_t s[4];
     k.to_std(s);
     return mul_std(s);
+  }
+  // a P + b Q with one chain of doublings (Shamir's trick): each bit
+  // position adds P, Q or the precomputed P + Q.
+  static Jac mul2(const Jac& P, const Fr& a, const Jac& Q, const Fr& b) {
+    uint64_t ka[4], kb[4];
+    a.to_std(ka);
+    b.to_std(kb);
+    const Jac PQ = P.add(Q);
+    Jac r = inf();
+    int top = -1;
+    for (int i = 255; i >= 0 && top < 0; i--)
+      if (((ka[i >> 6] | kb[i >> 6]) >> (i & 63)) & 1) top = i;
+    for (int i = top; i >= 0; i--) {
+      r = r.dbl();
+      const int ba = (int)((ka[i >> 6] >> (i & 63)) & 1), bb = (int)((kb[i >> 6] >> (i & 63)) & 1);
+      if (ba && bb) r = r.add(PQ);
+      else if (ba) r = r.add(P);
+      else if (bb) r = r.add(Q);
+    }
+    return r;
   }
   // canonical affine; returns false for infinity (x = y = 0 then)
   bool to_affine(E& ax, E& ay) const {
