@@ -13,7 +13,6 @@
 #include <functional>
 #include <mutex>
 #include <random>
-#include <system_error>
 #include <thread>
 #include <vector>
 
@@ -851,6 +850,9 @@ constexpr size_t GATE_G1_MIN_N = (size_t)1 << 21;
       g.state.compare_exchange_strong(pending, 2);
     }
   };
+  // idle workers spin while the proof runs (its jobs and per-set
+  // combinations then start within a microsecond)
+  WorkerPool::Hot hot_workers(ctx->pool);
   uint8_t* base = (uint8_t*)ctx->scratch_c.p;
   void* d_h = base;
   void* d_w = base + n * 32;
@@ -953,21 +955,31 @@ constexpr size_t GATE_G1_MIN_N = (size_t)1 << 21;
   };
   const std::function<void()> f_b2(run_b2), f_g1(run_g1), f_pre(precompute);
   if (n >= GATE_G1_MIN_N) msm_workspace_gate(ctx->job_ws[JOB_G1], &quotient_done);
-  std::vector<std::thread> workers;
-  ThreadJoiner joiner{workers};
+  // The jobs run on the context's worker threads.  TaskJoiner finishes them
+  // on every way out of this function (after GateRelease has opened the
+  // gate: destructors run in reverse order).
+  struct TaskJoiner {
+    std::vector<WorkerPool::TaskRef> v;
+    void join() {
+      for (const WorkerPool::TaskRef& t : v) WorkerPool::finish(t);
+    }
+    ~TaskJoiner() { join(); }
+  } joiner;
   GateRelease gate_release{quotient_done};
   const std::function<void()> jobs[3] = {job(f_b2, rc_b2), job(f_g1, rc_g1), job(f_pre, rc_pre)};
-  // A job whose thread cannot be started runs on this thread once the
-  // quotient is enqueued and its gate is set: the gated G1 job waits for
-  // that gate, so running it here first would wait forever.
+  // A job that no worker can take runs on this thread once the quotient is
+  // enqueued and its gate is set: the gated G1 job waits for that gate, so
+  // running it here first would wait forever.
   std::vector<const std::function<void()>*> inline_jobs;
   for (const std::function<void()>& fn : jobs) {
+    WorkerPool::TaskRef t;
     try {
-      if (debug_thread_start_refused()) throw std::system_error(std::make_error_code(std::errc::resource_unavailable_try_again));
-      workers.emplace_back(fn);
+      t = ctx->pool.submit(fn, debug_thread_start_refused());
     } catch (...) {
-      inline_jobs.push_back(&fn);
+      t = nullptr;
     }
+    if (t) joiner.v.push_back(t);
+    else inline_jobs.push_back(&fn);
   }
   int qrc = quotient_run(ctx, c, d_w, d_h, ctx->scratch_b.p, st, check_witness != 0, d_bad);
   // the check's count goes to pinned memory: the copy does not block this

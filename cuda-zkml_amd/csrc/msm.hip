@@ -1962,17 +1962,27 @@ static int msm_run_sets(zk_context* ctx, MsmWorkspace& ws, const BaseSets& sets_
       rc_fin[k] = ZK_ERR_OOM;
     }
   };
-  std::vector<std::thread> helpers;
-  ThreadJoiner joiner{helpers};
-  for (int k = 1; k < nsets; k++) {
-    try {
-      helpers.emplace_back(finish, k);
-    } catch (...) {
-      finish(k);  // no thread available
+  // the other sets on the context's worker threads (run here when none can
+  // take them)
+  std::vector<WorkerPool::TaskRef> helpers;
+  struct Joiner {
+    std::vector<WorkerPool::TaskRef>& v;
+    ~Joiner() {
+      for (const WorkerPool::TaskRef& t : v) WorkerPool::finish(t);
     }
+  } joiner{helpers};
+  for (int k = 1; k < nsets; k++) {
+    WorkerPool::TaskRef t;
+    try {
+      t = ctx->pool.submit([&finish, k] { finish(k); });
+    } catch (...) {
+      t = nullptr;
+    }
+    if (t) helpers.push_back(t);
+    else finish(k);
   }
   finish(0);
-  joiner.join();
+  for (const WorkerPool::TaskRef& t : helpers) WorkerPool::finish(t);
   for (int k = 0; k < nsets; k++)
     if (rc_fin[k] != ZK_OK) return ctx->fail(rc_fin[k], "msm: host allocation failed");
   return ZK_OK;

@@ -14,6 +14,7 @@
 
 #include "../../include/zkml_gpu.h"
 #include "field.hpp"
+#include "worker_pool.hpp"
 
 namespace zk {
 
@@ -96,6 +97,9 @@ struct zk_context {
   std::string stat_names;
   // guards last_error and pending: zk_prove runs MSMs from several threads
   std::mutex mu;
+  // host workers of zk_prove's MSM jobs and the three-set MSM's per-set
+  // window combination (started on first use, joined by zk_destroy)
+  zk::WorkerPool pool{5};
 
   int fail(int code, const char* what, const char* detail = "") {
     std::lock_guard<std::mutex> lk(mu);

@@ -77,10 +77,11 @@ int zk_memcpy_d2d(zk_context* ctx, void* d_dst, const void* d_src, size_t bytes)
  * (1 = the next one) fails with ZK_ERR_OOM, once; 0 disarms.  For tests of
  * the error paths only; affects every context of the process. */
 int zk_debug_fail_device_alloc(int nth);
-/* Test hook, no counterpart in the reference: the next `count` host threads
- * that zk_prove would start for its MSM jobs are refused as if the system had
- * none left, so the jobs run on the calling thread instead; 0 disarms.  For
- * tests of that fallback only; affects every context of the process. */
+/* Test hook, no counterpart in the reference: the next `count` MSM jobs that
+ * zk_prove would hand to the context's host worker threads are refused as if
+ * no worker could be started, so the jobs run on the calling thread instead;
+ * 0 disarms.  For tests of that fallback only; affects every context of the
+ * process. */
 int zk_debug_fail_thread_start(int count);
 
 /* Per-kernel timing with HIP events recorded on the stream each kernel is
