@@ -899,8 +899,15 @@ constexpr size_t GATE_G1_MIN_N = (size_t)1 << 21;
   auto record = [&](int slot, hipStream_t s, int& rc) {
     if (hipEventRecord(ev[slot], s) != hipSuccess && rc == ZK_OK) rc = ctx->fail(ZK_ERR_HIP, "prove: event record");
   };
+  // Each job makes its own stream wait for the resident witness, on its own
+  // thread: the call took ~17 us on the GPU hosts, and two of them on this
+  // thread delayed the quotient by that much.
+  auto wait_witness = [&](hipStream_t js, int& rc) {
+    if (hipStreamWaitEvent(js, ev[1], 0) != hipSuccess && rc == ZK_OK) rc = ctx->fail(ZK_ERR_HIP, "prove: stream wait");
+  };
   auto run_b2 = [&] {
     hipStream_t js = ctx->job_stream[S_G2];
+    wait_witness(js, rc_b2);
     record(4 + 2 * JOB_B2, js, rc_b2);
     if (rc_b2 == ZK_OK && nb2 && pk->tB2)
       rc_b2 = msm_recs_tab(ctx, ctx->job_ws[JOB_B2], true, pk->tB2, pk->nB2, pk->tab_b2, d_w, nb2, b2_msm, js,
@@ -911,6 +918,7 @@ constexpr size_t GATE_G1_MIN_N = (size_t)1 << 21;
   };
   auto run_g1 = [&] {
     hipStream_t js = ctx->job_stream[S_G1];
+    wait_witness(js, rc_g1);
     record(4 + 2 * JOB_G1, js, rc_g1);
     const void* recs[3];
     size_t lo[3], cnt[3], rows[3];
@@ -941,7 +949,6 @@ constexpr size_t GATE_G1_MIN_N = (size_t)1 << 21;
       g1_tail = sa_rb.add(g1_from_words(l_msm));
     }
   };
-  for (int j = 0; j < JOB_STREAMS; j++) ZK_HIP(ctx, hipStreamWaitEvent(ctx->job_stream[j], ev[1], 0));
   // Each job reports a C++ exception (a failed host allocation) as a status;
   // the joiner waits for the threads on every way out of this function.
   auto job = [&](const std::function<void()>& fn, int& rc) {
