@@ -134,6 +134,36 @@ struct F {
     mont(r.v, s, M::R2);
     return r;
   }
+  // The integer of nine 29-bit limbs (the device kernels' form of an element,
+  // x 2^261 mod m, below 2^261) reduced mod m, taken as this type's
+  // Montgomery word: it stands for x 2^5.  A ratio of two such values
+  // (X / ZZ, Y / ZZZ of an XYZZ point) is then exact with no radix
+  // conversion, the 2^5 cancelling.
+  static F from_limbs29_scaled(const uint32_t* l) {
+    uint64_t w[5] = {0, 0, 0, 0, 0};
+    for (int i = 0; i < 9; i++) {
+      const int bit = 29 * i, wd = bit >> 6, sh = bit & 63;
+      w[wd] |= (uint64_t)l[i] << sh;
+      if (sh > 64 - 29) w[wd + 1] |= (uint64_t)l[i] >> (64 - sh);
+    }
+    // below 2^261 < 256 m: subtract m 2^k where it fits, k = 7 .. 0
+    for (int k = 7; k >= 0; k--) {
+      uint64_t mk[5], d[5];
+      mk[4] = k ? M::M[3] >> (64 - k) : 0;
+      for (int j = 3; j >= 1; j--) mk[j] = k ? (M::M[j] << k) | (M::M[j - 1] >> (64 - k)) : M::M[j];
+      mk[0] = M::M[0] << k;
+      unsigned char b = 0;
+      for (int j = 0; j < 5; j++) {
+        unsigned long long t;
+        b = _subborrow_u64(b, w[j], mk[j], &t);
+        d[j] = t;
+      }
+      if (!b) memcpy(w, d, sizeof(d));
+    }
+    F r;
+    memcpy(r.v, w, 32);
+    return r;
+  }
   static F from_u64(uint64_t x) {
     uint64_t s[4] = {x, 0, 0, 0};
     return from_std(s);

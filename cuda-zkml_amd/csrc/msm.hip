@@ -1435,14 +1435,13 @@ static int choose_c(size_t n, bool g2) {
 // ------------------------------------------------------------------ host tail
 template <class F>
 struct HostSide;
+// conv takes the device's limbs as they are (zkh::F::from_limbs29_scaled):
+// every host use is a ratio X / ZZ or Y / ZZZ, in which the radix factor
+// 2^5 cancels, so no conversion multiply is needed.
 template <>
 struct HostSide<fq> {
   typedef zkh::Fq E;
-  static E conv(const fq& a) {
-    uint32_t w[8];
-    to_mont256(a, w);
-    return E::raw(w);
-  }
+  static E conv(const fq& a) { return E::from_limbs29_scaled(a.l); }
   static void out(const E& x, const E& y, uint64_t* o) {
     memcpy(o, x.v, 32);
     memcpy(o + 4, y.v, 32);
@@ -1452,10 +1451,7 @@ template <>
 struct HostSide<fq2> {
   typedef zkh::Fq2 E;
   static E conv(const fq2& a) {
-    uint32_t w0[8], w1[8];
-    to_mont256(a.c0, w0);
-    to_mont256(a.c1, w1);
-    return E{zkh::Fq::raw(w0), zkh::Fq::raw(w1)};
+    return E{zkh::Fq::from_limbs29_scaled(a.c0.l), zkh::Fq::from_limbs29_scaled(a.c1.l)};
   }
   static void out(const E& x, const E& y, uint64_t* o) {
     memcpy(o, x.c0.v, 32);

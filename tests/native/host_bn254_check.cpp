@@ -87,3 +87,9 @@ int hb_g2_mul(const uint64_t* p, const uint64_t* k, uint64_t* out) {
 }
 
 }  // extern "C"
+
+extern "C" int hb_fq_from_limbs29_scaled(const uint32_t* limbs, uint64_t* out) {
+  const Fq r = Fq::from_limbs29_scaled(limbs);
+  memcpy(out, r.v, 32);
+  return 0;
+}

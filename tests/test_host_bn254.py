@@ -9,6 +9,9 @@ branch of an addition fails here before any proof is compared:
   add (G1, G2)   affine + affine and Jacobian + affine (the z = 1 path),
                  affine + Jacobian, Jacobian + Jacobian (the general path);
                  P + P (doubling inside both paths), P + (-P) and infinity
+  limbs29_scaled the device's nine 29-bit limbs as an integer below 2^261,
+                 reduced mod q (the host's MSM window combination takes the
+                 ratios X / ZZ, Y / ZZZ of such values, the radix cancelling)
   mul2 (G1)      a P + b Q with one doubling chain (Shamir's trick) for
                  64-bit blinding-size and full-size scalars, 0, 1, r - 1,
                  P = Q and Q = -P; against mul and the Python reference
@@ -115,3 +118,36 @@ def test_g2_mul(hb):
         out = W16()
         assert hb.hb_g2_mul(W16(*g2_to_words(p)), fr_w(a), out) == 0
         assert g2_from_words(out) == g2.pmul(p, a)
+
+
+def test_fq_from_limbs29_scaled(hb):
+    rng = random.Random(15)
+    U9 = ctypes.c_uint32 * 9
+    vals = [0, 1, Q - 1, Q, Q + 1, 2 * Q - 1, 2 * Q, (1 << 256) - 1, 1 << 256, (1 << 261) - 1, 127 * Q, 128 * Q - 1]
+    vals += [rng.randrange(2 * Q) for _ in range(200)] + [rng.randrange(1 << 261) for _ in range(200)]
+    for v in vals:
+        out = W4()
+        assert hb.hb_fq_from_limbs29_scaled(U9(*[(v >> (29 * i)) & ((1 << 29) - 1) for i in range(9)]), out) == 0
+        assert sum(int(w) << (64 * i) for i, w in enumerate(out)) == v % Q, hex(v)
+
+
+def test_ratio_of_scaled_values_is_exact(hb):
+    """x = X / ZZ from device-form limbs equals the affine x (the 2^5 of the
+    radix cancels): checked through the G1 adder, whose affine output divides
+    by z^2 = ZZ."""
+    rng = random.Random(16)
+    RP = 1 << 261
+    U9 = ctypes.c_uint32 * 9
+    for _ in range(20):
+        p = g1.pmul(G1, rng.randrange(1, R))
+        z = rng.randrange(1, Q)
+        X, Y, ZZ = p[0] * z * z % Q, p[1] * z * z * z % Q, z * z % Q
+        dev = [v * RP % Q for v in (X, Y, ZZ)]  # the device's internal form
+        words = []
+        for v in dev:
+            out = W4()
+            hb.hb_fq_from_limbs29_scaled(U9(*[(v >> (29 * i)) & ((1 << 29) - 1) for i in range(9)]), out)
+            words.append(sum(int(w) << (64 * i) for i, w in enumerate(out)))
+        inv_mont = pow(1 << 256, -1, Q)
+        xs, ys, zzs = (w * inv_mont % Q for w in words)  # the values the host arithmetic sees
+        assert xs * pow(zzs, -1, Q) % Q == p[0]
