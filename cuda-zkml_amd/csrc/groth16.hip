@@ -580,6 +580,12 @@ int zk_quotient_h(zk_context* ctx, const zk_r1cs* c, const void* d_witness, size
 #ifndef ZK_PK_TAB_SUB_H
 #define ZK_PK_TAB_SUB_H 8
 #endif
+// B2's sub-windows: 2^9 buckets (the G2 job ends the 2^16 proof; its
+// reduction chains are Fq2 additions, one level shallower this way: config 4
+// 1.32-1.36 -> 1.30 ms; 2^8 and 2^7 1.30-1.31 ms)
+#ifndef ZK_PK_TAB_SUB_B2
+#define ZK_PK_TAB_SUB_B2 9
+#endif
 // Table shape for MSMs of n scalars (W = 0: no table); wlarge: windows from
 // 2^15 scalars on; sub: log2 of the sub-window size up to 2^18 scalars.
 static MsmTab table_shape(size_t n, int wlarge, int sub = ZK_PK_TAB_SUB) {
@@ -615,7 +621,7 @@ static void pk_drop_tables(zk_pk* pk) {
 
 static int pk_tables_build(zk_context* ctx, zk_pk* pk) {
   pk->tab_w = table_shape((size_t)pk->m, ZK_PK_TAB_W_LARGE);
-  pk->tab_b2 = table_shape((size_t)pk->m, ZK_PK_TAB_W_LARGE_B2);
+  pk->tab_b2 = table_shape((size_t)pk->m, ZK_PK_TAB_W_LARGE_B2, ZK_PK_TAB_SUB_B2);
   pk->tab_h = table_shape((size_t)pk->n, ZK_PK_TAB_W_LARGE_H, ZK_PK_TAB_SUB_H);
   if (pk->tab_w.W) {
     ZK_TRY(pk_table(ctx, false, pk->A, pk->nA, pk->tab_w, &pk->tA));
