@@ -1604,12 +1604,12 @@ struct AccPlan {
 // for less than W*n): short chunks give small MSMs enough threads (a thread's
 // chunk is a serial chain of additions), long chunks keep the chunk-combine
 // tree of large ones shallow.  Measured on MI355X over 2^10 .. 2^20 points,
-// G1 and G2, uniform and witness-like scalars.  Beside other kernels (see
-// msm_recs_ws) a G1 chunk below the longest is one step shorter (measured in
-// the 2^16 proof: 1.97 -> 1.87 ms; the 2^22 proof's MSMs keep the longest
-// chunks, shorter ones cost it 2 ms).
+// G1 and G2, uniform and witness-like scalars.  Inside a proof the same
+// lengths serve: halving the G1 chunks beside the other jobs once paid (2^16
+// proof 1.97 -> 1.87 ms), but with the proof's later host and placement
+// work it cost config 4's 2^16 proof 1.26 -> 1.29 ms.
 template <class F>
-static AccPlan plan_accumulation(const MsmWorkspace& ws, const MsmShape& sh, bool beside) {
+static AccPlan plan_accumulation(const MsmWorkspace& ws, const MsmShape& sh) {
   constexpr bool G2 = sizeof(F) != sizeof(fq);
   size_t entries = 0;
   uint32_t maxrun = 1;
@@ -1627,9 +1627,7 @@ static AccPlan plan_accumulation(const MsmWorkspace& ws, const MsmShape& sh, boo
                             : entries >= ((size_t)1 << 18) ? MSM_L0 / 4
                                                            : MSM_L0 / 8;
   AccPlan ap;
-  ap.L0 = G2 ? std::max<uint32_t>(L0_alone >> ZK_MSM_G2_L0_SHIFT, MSM_L0 / 8)
-             : beside && L0_alone < (uint32_t)MSM_L0 ? std::max<uint32_t>(L0_alone / 2, MSM_L0 / 8)
-                                                      : L0_alone;
+  ap.L0 = G2 ? std::max<uint32_t>(L0_alone >> ZK_MSM_G2_L0_SHIFT, MSM_L0 / 8) : L0_alone;
   ap.cpw = sh.n_pad / ap.L0;
   ap.nchunks = ap.cpw * (uint32_t)sh.W;
   ap.max_span = (maxrun + ap.L0 - 2) / ap.L0 + 1;
@@ -1933,7 +1931,7 @@ static int msm_run_sets(zk_context* ctx, MsmWorkspace& ws, const BaseSets& sets_
   // the windows' entry counts and largest buckets come back while the
   // scatter runs
   ZK_HIP(ctx, hipEventSynchronize(ws.stat_ready));
-  const AccPlan ap = plan_accumulation<F>(ws, sh, beside);
+  const AccPlan ap = plan_accumulation<F>(ws, sh);
   if (ws.gate) {
     int gs;
     while ((gs = ws.gate->state.load()) == 0) std::this_thread::yield();

@@ -216,10 +216,9 @@ struct MsmGate {
 // Gate of a workspace's next MSMs (null: none).
 void msm_workspace_gate(MsmWorkspace* ws, MsmGate* wait_before_accumulate);
 // MSM over records with an explicit workspace (one per concurrent caller).
-// beside: the MSM shares the GPU with other kernels (a proof); a G1 MSM then
-// gives each accumulation thread half as many entries, so its waves free CU
-// slots for the other streams' kernels sooner, and the latency-bound combine
-// and reduction choose their lane layouts for a shared GPU.
+// beside: the MSM shares the GPU with other kernels (a proof); the
+// latency-bound combine and reduction then choose their lane layouts for a
+// shared GPU.
 int msm_recs_ws(zk_context* ctx, MsmWorkspace* ws, bool g2, const void* d_recs, const void* d_scalars, size_t n,
                 uint64_t* out_affine, hipStream_t st, bool beside = false);
 // Window tables of fixed bases (proving-key queries): for W digit windows
