@@ -54,7 +54,7 @@ static void usage() {
   printf("  --statement-meta FILE     statement metadata JSON\n");
   printf("Other statements:\n");
   printf("  --r1cs FILE --wtns FILE   iden3 R1CS (v1) and witness (v2)\n");
-  printf("  --synthetic N             random R1CS with N constraints (BASELINE config 5 shape)\n");
+  printf("  --synthetic N             random R1CS with N constraints (1-3 term rows, C a fresh variable)\n");
   printf("  --synthetic-public P      public inputs of the synthetic R1CS (default 4)\n");
   printf("  --synthetic-inputs K      free private inputs of the synthetic R1CS (default 16)\n");
   printf("  --synthetic-seed S        generator seed (default 42)\n");

@@ -121,7 +121,7 @@ int zk_ntt_noalloc(zk_context* ctx, void* d_out, const void* d_in, int log_n, in
 
 /* Coset NTT as used by Groth16Prover::compute_h (src/prover/groth16.cu:350-383):
  * forward: out = NTT(in[i] * g^i); inverse: out[i] = iNTT(in)[i] * g^-i.
- * g is a small plain integer (the prover uses 5; BASELINE config 2 uses 7). */
+ * g is a small plain integer (the prover uses 5; the coset tests also use 7). */
 int zk_coset_ntt(zk_context* ctx, void* d_out, const void* d_in, int log_n, uint64_t g, int inverse, int batch,
                  void* stream);
 
@@ -235,8 +235,8 @@ int zk_prove(zk_context* ctx, const zk_pk* pk, const zk_r1cs* r1cs, const void* 
  * hold standard form.  Reading: zk_iden3_r1cs_info gives the sizes (public =
  * nPubOut + nPubIn), then zk_iden3_r1cs_read fills caller arrays of those
  * sizes; zk_wtns_info / zk_wtns_read likewise.
- * zk_synthetic_r1cs builds the large random R1CS of BASELINE config 5 from a
- * seed: w[0] = 1, num_public + num_inputs uniform variables, then per row A and
+ * zk_synthetic_r1cs builds a large random R1CS (the shape of the 2^22-row
+ * benchmark statement) from a seed: w[0] = 1, num_public + num_inputs uniform variables, then per row A and
  * B with 1-3 terms over earlier variables (uniform coefficients) and C = one
  * fresh variable set to (A.w)(B.w), so the witness satisfies every row.
  * Capacities: A, B 3 * num_constraints entries, C num_constraints, w_mont
