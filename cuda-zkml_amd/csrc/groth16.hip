@@ -811,8 +811,10 @@ static int zk_prove_impl(zk_context* ctx, const zk_pk* pk, const zk_r1cs* c, con
 // the quotient is done: the quotient's transforms then get the CU slots
 // they wait for beside the accumulations (2^22 proof 45.9 -> 45.0 ms).  At
 // 2^16 every such gate lost (1.42 ms -> 1.53 ms gating the G1 job, 1.70 ms
-// gating B2, 1.69 ms both), and so did holding the G1 accumulation until the
-// G2 accumulation kernel had finished (1.33 -> 1.52 ms; 2^20 9.09 -> 9.17 ms).
+// gating B2, 1.69 ms both; measured again with the current kernels: 1.27 ->
+// 1.33 ms gating G1, 1.37 ms gating B2, 1.44 ms both), and so did holding the
+// G1 accumulation until the G2 accumulation kernel had finished (1.33 -> 1.52
+// ms; 2^20 9.09 -> 9.17 ms).
 constexpr size_t GATE_G1_MIN_N = (size_t)1 << 21;
   hipEvent_t ev[NEV];
   for (auto& e : ev) ZK_HIP(ctx, hipEventCreate(&e));
