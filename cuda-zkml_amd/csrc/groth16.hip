@@ -9,6 +9,7 @@
 
 #include <algorithm>
 #include <atomic>
+#include <chrono>
 #include <condition_variable>
 #include <functional>
 #include <mutex>
@@ -165,6 +166,16 @@ G2 g2_from_words(const uint64_t* w) {
   for (int i = 0; i < 16; i++) inf = inf && w[i] == 0;
   if (inf) return G2::inf();
   return G2::affine(Fq2{Fq::raw(w), Fq::raw(w + 4)}, Fq2{Fq::raw(w + 8), Fq::raw(w + 12)});
+}
+// Jacobian words x, y, z (an MSM's jac_out result; z = 0 at infinity)
+G1 g1_from_jac_words(const uint64_t* w) {
+  const G1 p{Fq::raw(w), Fq::raw(w + 4), Fq::raw(w + 8)};
+  return p.is_inf() ? G1::inf() : p;
+}
+G2 g2_from_jac_words(const uint64_t* w) {
+  const G2 p{Fq2{Fq::raw(w), Fq::raw(w + 4)}, Fq2{Fq::raw(w + 8), Fq::raw(w + 12)},
+             Fq2{Fq::raw(w + 16), Fq::raw(w + 20)}};
+  return p.is_inf() ? G2::inf() : p;
 }
 
 // Affine words of the three proof points with one field inversion: the
@@ -804,9 +815,9 @@ static int zk_prove_impl(zk_context* ctx, const zk_pk* pk, const zk_r1cs* c, con
                          int num_public, uint64_t blind_seed, int check_witness, uint8_t proof_out[256],
                          double* timings) {
   if (!ctx || !pk || !c || !proof_out || (m && !h_witness)) return ZK_ERR_INVALID;
-  // events: 0 start, 1 witness resident, 2 quotient done, 3 end,
-  // 4 + 2j / 5 + 2j start / end of MSM job j
-  constexpr int NEV = 4 + 2 * ZK_JOBS;
+  // events: 0 start, 1 witness resident, 2 quotient done, 3 + 2j / 4 + 2j
+  // start / end of MSM job j
+  constexpr int NEV = 3 + 2 * ZK_JOBS;
 // From a 2^21 domain on, the three-set G1 job holds its accumulation until
 // the quotient is done: the quotient's transforms then get the CU slots
 // they wait for beside the accumulations (2^22 proof 45.9 -> 45.0 ms).  At
@@ -866,6 +877,7 @@ constexpr size_t GATE_G1_MIN_N = (size_t)1 << 21;
   void* d_h = base;
   void* d_w = base + n * 32;
   uint32_t* d_bad = (uint32_t*)(base + n * 32 + m * 32);
+  const auto t_start = std::chrono::steady_clock::now();
   ZK_HIP(ctx, hipEventRecord(ev[0], st));
   ZK_TRY(upload_staged(ctx, d_w, h_witness, m * 32, st));
   ZK_HIP(ctx, hipEventRecord(ev[1], st));
@@ -873,7 +885,9 @@ constexpr size_t GATE_G1_MIN_N = (size_t)1 << 21;
   std::mt19937_64 rng(blind_seed);
   Fr r = random_nonzero(rng);
   Fr s = random_nonzero(rng);
-  uint64_t a_msm[8], b2_msm[16], l_msm[8], h_msm[8], b1_msm[8];
+  // B2 and H come back as Jacobian words: they are only added to other
+  // points before proof_to_words' one inversion
+  uint64_t a_msm[8], b2_msm[24], l_msm[8], h_msm[12], b1_msm[8];
   memset(l_msm, 0, sizeof(l_msm));
   const size_t na = std::min(m, pk->nA);
   const size_t nb2 = std::min(m, pk->nB2);
@@ -917,18 +931,19 @@ constexpr size_t GATE_G1_MIN_N = (size_t)1 << 21;
   auto run_b2 = [&] {
     hipStream_t js = ctx->job_stream[S_G2];
     wait_witness(js, rc_b2);
-    record(4 + 2 * JOB_B2, js, rc_b2);
+    record(3 + 2 * JOB_B2, js, rc_b2);
     if (rc_b2 == ZK_OK && nb2 && pk->tB2)
       rc_b2 = msm_recs_tab(ctx, ctx->job_ws[JOB_B2], true, pk->tB2, pk->nB2, pk->tab_b2, d_w, nb2, b2_msm, js,
-                           /*beside=*/true);
+                           /*beside=*/true, /*jac_out=*/true);
     else if (rc_b2 == ZK_OK && nb2)
-      rc_b2 = msm_recs_ws(ctx, ctx->job_ws[JOB_B2], true, pk->B2, d_w, nb2, b2_msm, js, /*beside=*/true);
-    record(5 + 2 * JOB_B2, js, rc_b2);
+      rc_b2 = msm_recs_ws(ctx, ctx->job_ws[JOB_B2], true, pk->B2, d_w, nb2, b2_msm, js, /*beside=*/true,
+                          /*jac_out=*/true);
+    record(4 + 2 * JOB_B2, js, rc_b2);
   };
   auto run_g1 = [&] {
     hipStream_t js = ctx->job_stream[S_G1];
     wait_witness(js, rc_g1);
-    record(4 + 2 * JOB_G1, js, rc_g1);
+    record(3 + 2 * JOB_G1, js, rc_g1);
     const void* recs[3];
     size_t lo[3], cnt[3], rows[3];
     uint64_t* outs[3];
@@ -951,7 +966,7 @@ constexpr size_t GATE_G1_MIN_N = (size_t)1 << 21;
     if (rc_g1 == ZK_OK && ns)
       rc_g1 = msm_g1_sets_ws(ctx, ctx->job_ws[JOB_G1], ns, recs, lo, cnt, d_w, m, outs, js, /*beside=*/true,
                              tab ? &pk->tab_w : nullptr, tab ? rows : nullptr);
-    record(5 + 2 * JOB_G1, js, rc_g1);
+    record(4 + 2 * JOB_G1, js, rc_g1);
     if (rc_g1 == ZK_OK) {
       const G1 sa_rb = nb1 > 0 ? G1::mul2(g1_from_words(a_msm), s, g1_from_words(b1_msm), r)
                                : g1_from_words(a_msm).mul(s);
@@ -1010,14 +1025,15 @@ constexpr size_t GATE_G1_MIN_N = (size_t)1 << 21;
   quotient_done.state.store(qrc == ZK_OK ? 1 : 2);
   for (const std::function<void()>* fn : inline_jobs) (*fn)();
   if (qrc == ZK_OK) {  // H after the quotient, same stream
-    record(4 + 2 * JOB_H, st, rc_h);
+    record(3 + 2 * JOB_H, st, rc_h);
     if (rc_h == ZK_OK && nh && pk->tH)
       rc_h = msm_recs_tab(ctx, ctx->job_ws[JOB_H], false, pk->tH, pk->nH, pk->tab_h, d_h, nh, h_msm, st,
-                          /*beside=*/true);
+                          /*beside=*/true, /*jac_out=*/true);
     else if (rc_h == ZK_OK && nh)
-      rc_h = msm_recs_ws(ctx, ctx->job_ws[JOB_H], false, pk->H, d_h, nh, h_msm, st, /*beside=*/true);
+      rc_h = msm_recs_ws(ctx, ctx->job_ws[JOB_H], false, pk->H, d_h, nh, h_msm, st, /*beside=*/true,
+                         /*jac_out=*/true);
     else if (!nh) memset(h_msm, 0, sizeof(h_msm));
-    record(5 + 2 * JOB_H, st, rc_h);
+    record(4 + 2 * JOB_H, st, rc_h);
   }
   joiner.join();
   ZK_TRY(qrc);
@@ -1032,8 +1048,8 @@ constexpr size_t GATE_G1_MIN_N = (size_t)1 << 21;
   // the rest of the assembly; an empty A, L, H or B1 set left its result at
   // the identity (all-zero words)
   const G1 A = pre_a.add(g1_from_words(a_msm));
-  const G2 B = pre_b.add(nb2 > 0 ? g2_from_words(b2_msm) : G2::inf());
-  const G1 Cj = g1_tail.add(g1_from_words(h_msm)).add(pre_c);
+  const G2 B = pre_b.add(nb2 > 0 ? g2_from_jac_words(b2_msm) : G2::inf());
+  const G1 Cj = g1_tail.add(g1_from_jac_words(h_msm)).add(pre_c);
   uint64_t Aw[8], Bw[16], Cw[8];
   proof_to_words(A, B, Cj, Aw, Bw, Cw);
   // 256-byte serialization in standard form (groth16.cu:1058-1074)
@@ -1052,27 +1068,32 @@ constexpr size_t GATE_G1_MIN_N = (size_t)1 << 21;
   put(Bw + 12);
   put(Cw);
   put(Cw + 4);
-  ZK_HIP(ctx, hipEventRecord(ev[3], st));
-  ZK_HIP(ctx, hipEventSynchronize(ev[3]));
+  // Every MSM job synchronized its stream before its host step; the context
+  // stream still runs the quotient when H had nothing to do.
+  if (hipStreamQuery(st) != hipSuccess) ZK_HIP(ctx, hipStreamSynchronize(st));
   if (timings) {
-    float t = 0;
-    (void)hipEventElapsedTime(&t, ev[0], ev[3]);
-    timings[0] = t;  // total
-    (void)hipEventElapsedTime(&t, ev[0], ev[2]);
-    timings[1] = t;  // witness upload + quotient (+ check)
+    // total by the host clock (no event round trip after the assembly); the
+    // GPU phases from the events, all complete by now
+    timings[0] = std::chrono::duration<double, std::milli>(std::chrono::steady_clock::now() - t_start).count();
+    auto elapsed = [](hipEvent_t a, hipEvent_t b) {
+      float t = 0;
+      if (hipEventElapsedTime(&t, a, b) != hipSuccess) {
+        (void)hipEventSynchronize(b);
+        if (hipEventElapsedTime(&t, a, b) != hipSuccess) t = 0;
+      }
+      return (double)t;
+    };
+    timings[1] = elapsed(ev[0], ev[2]);  // witness upload + quotient (+ check)
     // each MSM from its start to its result on the host (they overlap); A,
     // L and B1 are one run and report its time
     const int slot_of[ZK_JOBS] = {0, 1, 0, 3, 0};  // A, B (G2), L, H, B1
-    float last = 0;
+    double last = 0;
     for (int j = 0; j < ZK_JOBS; j++) {
       const int e = slot_of[j];
-      (void)hipEventElapsedTime(&t, ev[4 + 2 * e], ev[5 + 2 * e]);
-      timings[2 + j] = t;
-      (void)hipEventElapsedTime(&t, ev[0], ev[5 + 2 * e]);
-      last = std::max(last, t);
+      timings[2 + j] = elapsed(ev[3 + 2 * e], ev[4 + 2 * e]);
+      last = std::max(last, elapsed(ev[0], ev[4 + 2 * e]));
     }
-    (void)hipEventElapsedTime(&t, ev[0], ev[3]);
-    timings[7] = t - last;  // host assembly after the last MSM
+    timings[7] = std::max(0.0, timings[0] - last);  // host assembly after the last MSM
   }
   return ZK_OK;
 }

@@ -1446,6 +1446,11 @@ struct HostSide<fq> {
     memcpy(o, x.v, 32);
     memcpy(o + 4, y.v, 32);
   }
+  static void out_jac(const zkh::Jac<E>& r, uint64_t* o) {
+    memcpy(o, r.x.v, 32);
+    memcpy(o + 4, r.y.v, 32);
+    memcpy(o + 8, r.z.v, 32);
+  }
 };
 template <>
 struct HostSide<fq2> {
@@ -1459,12 +1464,35 @@ struct HostSide<fq2> {
     memcpy(o + 8, y.c0.v, 32);
     memcpy(o + 12, y.c1.v, 32);
   }
+  static void out_jac(const zkh::Jac<E>& r, uint64_t* o) {
+    const E* c[3] = {&r.x, &r.y, &r.z};
+    for (int i = 0; i < 3; i++) {
+      memcpy(o + 8 * i, c[i]->c0.v, 32);
+      memcpy(o + 8 * i + 4, c[i]->c1.v, 32);
+    }
+  }
 };
+
+// An MSM's result: affine words (x, y), or with jac_out Jacobian words (x, y,
+// z) for a caller that adds it to other points before its own affine
+// conversion (one inversion fewer).  Infinity is all zeros either way.
+template <class F>
+static void host_result(const zkh::Jac<typename HostSide<F>::E>& r, bool jac_out, uint64_t* out) {
+  typedef typename HostSide<F>::E E;
+  if (jac_out) {
+    if (r.is_inf()) memset(out, 0, sizeof(E) * 3);
+    else HostSide<F>::out_jac(r, out);
+    return;
+  }
+  E ax, ay;
+  r.to_affine(ax, ay);
+  HostSide<F>::out(ax, ay, out);
+}
 
 // XYZZ partials (device layout, copied to the host) -> affine via one batch
 // inversion -> per-window sums -> Horner over windows.
 template <class F>
-static void host_finish(const std::vector<xyzz<F>>& parts, int W, int per_w, uint64_t* out) {
+static void host_finish(const std::vector<xyzz<F>>& parts, int W, int per_w, uint64_t* out, bool jac_out) {
   typedef typename HostSide<F>::E E;
   typedef zkh::Jac<E> J;
   const size_t m = parts.size();
@@ -1497,9 +1525,7 @@ static void host_finish(const std::vector<xyzz<F>>& parts, int W, int per_w, uin
     for (int k = 0; k < window_width(w, W); k++) r = r.dbl();
     r = r.add(win[w]);
   }
-  E ax, ay;
-  r.to_affine(ax, ay);
-  HostSide<F>::out(ax, ay, out);
+  host_result<F>(r, jac_out, out);
 }
 
 // Sizes of one MSM: n points, W windows of about c bits, B buckets per window.
@@ -1818,7 +1844,7 @@ static int msm_reduce(zk_context* ctx, MsmWorkspace& ws, int Wr, uint32_t Br, in
 //   sum_h P[h] + 2^log_sub sum_h h R[h],
 // the second sum as running sums from the top sub-window down.
 template <class F>
-static void host_finish_sub(const xyzz<F>* P, const xyzz<F>* R, int H, int log_sub, uint64_t* out) {
+static void host_finish_sub(const xyzz<F>* P, const xyzz<F>* R, int H, int log_sub, uint64_t* out, bool jac_out) {
   typedef typename HostSide<F>::E E;
   typedef zkh::Jac<E> J;
   const size_t m = 2 * (size_t)H;
@@ -1851,10 +1877,7 @@ static void host_finish_sub(const xyzz<F>* P, const xyzz<F>* R, int H, int log_s
   }
   for (int k = 0; k < log_sub; k++) weighted = weighted.dbl();
   for (int h = 0; h < H; h++) sum = sum.add(pt[h]);
-  J r = sum.add(weighted);
-  E ax, ay;
-  r.to_affine(ax, ay);
-  HostSide<F>::out(ax, ay, out);
+  host_result<F>(sum.add(weighted), jac_out, out);
 }
 
 // MSMs of `nsets` point sets over one scalar vector of n entries (see
@@ -1866,8 +1889,8 @@ static void host_finish_sub(const xyzz<F>* P, const xyzz<F>* R, int H, int log_s
 template <class F>
 static int msm_run_sets(zk_context* ctx, MsmWorkspace& ws, const BaseSets& sets_in, int nsets, const void* d_scalars,
                         size_t n, uint64_t* const* outs, hipStream_t st, bool beside = false,
-                        const MsmTab* tab = nullptr) {
-  constexpr int OUTW = sizeof(F) == sizeof(fq) ? 8 : 16;
+                        const MsmTab* tab = nullptr, bool jac_out = false) {
+  const int OUTW = (sizeof(F) == sizeof(fq) ? 4 : 8) * (jac_out ? 3 : 2);
   if (nsets < 1 || nsets > MSM_SETS) return ctx->fail(ZK_ERR_INVALID, "msm: 1 to 3 point sets");
   for (int k = 0; k < nsets; k++) memset(outs[k], 0, OUTW * 8);
   if (n == 0) return ZK_OK;
@@ -1949,9 +1972,11 @@ static int msm_run_sets(zk_context* ctx, MsmWorkspace& ws, const BaseSets& sets_
   auto finish = [&](int k) {
     try {
       if (tab)
-        host_finish_sub<F>(parts + (size_t)k * Wr, parts + (size_t)(nsets + k) * Wr, Wr, tab->log_sub, outs[k]);
+        host_finish_sub<F>(parts + (size_t)k * Wr, parts + (size_t)(nsets + k) * Wr, Wr, tab->log_sub, outs[k],
+                           jac_out);
       else
-        host_finish<F>(std::vector<xyzz<F>>(parts + (size_t)k * W, parts + (size_t)(k + 1) * W), W, 1, outs[k]);
+        host_finish<F>(std::vector<xyzz<F>>(parts + (size_t)k * W, parts + (size_t)(k + 1) * W), W, 1, outs[k],
+                       jac_out);
     } catch (...) {
       rc_fin[k] = ZK_ERR_OOM;
     }
@@ -1985,13 +2010,13 @@ static int msm_run_sets(zk_context* ctx, MsmWorkspace& ws, const BaseSets& sets_
 // One point set over all n scalars.
 template <class F>
 static int msm_run_recs(zk_context* ctx, MsmWorkspace& ws, const uint4* recs, const void* d_scalars, size_t n,
-                        uint64_t* out, hipStream_t st, bool beside = false) {
+                        uint64_t* out, hipStream_t st, bool beside = false, bool jac_out = false) {
   BaseSets sets{};
   sets.recs[0] = recs;
   sets.lo[0] = 0;
   sets.hi[0] = (uint32_t)std::min<size_t>(n, 0xffffffffu);
   uint64_t* outs[1] = {out};
-  return msm_run_sets<F>(ctx, ws, sets, 1, d_scalars, n, outs, st, beside);
+  return msm_run_sets<F>(ctx, ws, sets, 1, d_scalars, n, outs, st, beside, nullptr, jac_out);
 }
 
 template <class F>
@@ -2040,7 +2065,7 @@ int msm_g1_sets_ws(zk_context* ctx, MsmWorkspace* ws, int nsets, const void* con
 }
 
 int msm_recs_tab(zk_context* ctx, MsmWorkspace* ws, bool g2, const void* d_table, size_t rows, const MsmTab& tab,
-                 const void* d_scalars, size_t n, uint64_t* out, hipStream_t st, bool beside) {
+                 const void* d_scalars, size_t n, uint64_t* out, hipStream_t st, bool beside, bool jac_out) {
   if (!ws) return ctx->fail(ZK_ERR_INVALID, "msm: no workspace");
   if (n > rows) return ctx->fail(ZK_ERR_INVALID, "msm: more scalars than window table rows");
   BaseSets sets{};
@@ -2049,8 +2074,8 @@ int msm_recs_tab(zk_context* ctx, MsmWorkspace* ws, bool g2, const void* d_table
   sets.hi[0] = (uint32_t)n;
   sets.tstride[0] = (uint32_t)rows;
   uint64_t* outs[1] = {out};
-  if (g2) return msm_run_sets<fq2>(ctx, *ws, sets, 1, d_scalars, n, outs, st, beside, &tab);
-  return msm_run_sets<fq>(ctx, *ws, sets, 1, d_scalars, n, outs, st, beside, &tab);
+  if (g2) return msm_run_sets<fq2>(ctx, *ws, sets, 1, d_scalars, n, outs, st, beside, &tab, jac_out);
+  return msm_run_sets<fq>(ctx, *ws, sets, 1, d_scalars, n, outs, st, beside, &tab, jac_out);
 }
 
 // ------------------------------------------------------------------ window tables
@@ -2137,10 +2162,10 @@ int msm_table_build(zk_context* ctx, bool g2, const void* d_recs, size_t count, 
 }
 
 int msm_recs_ws(zk_context* ctx, MsmWorkspace* ws, bool g2, const void* d_recs, const void* d_scalars, size_t n,
-                uint64_t* out, hipStream_t st, bool beside) {
+                uint64_t* out, hipStream_t st, bool beside, bool jac_out) {
   if (!ws) return ctx->fail(ZK_ERR_INVALID, "msm: no workspace");
-  if (g2) return msm_run_recs<fq2>(ctx, *ws, (const uint4*)d_recs, d_scalars, n, out, st, beside);
-  return msm_run_recs<fq>(ctx, *ws, (const uint4*)d_recs, d_scalars, n, out, st, beside);
+  if (g2) return msm_run_recs<fq2>(ctx, *ws, (const uint4*)d_recs, d_scalars, n, out, st, beside, jac_out);
+  return msm_run_recs<fq>(ctx, *ws, (const uint4*)d_recs, d_scalars, n, out, st, beside, jac_out);
 }
 
 // Records of n points for MSMs over one base set, converted once (the

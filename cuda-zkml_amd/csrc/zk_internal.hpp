@@ -218,9 +218,10 @@ void msm_workspace_gate(MsmWorkspace* ws, MsmGate* wait_before_accumulate);
 // MSM over records with an explicit workspace (one per concurrent caller).
 // beside: the MSM shares the GPU with other kernels (a proof); the
 // latency-bound combine and reduction then choose their lane layouts for a
-// shared GPU.
+// shared GPU.  out gets affine words x, y (8 words G1, 16 G2), or with
+// jac_out Jacobian words x, y, z (12 / 24 words); all zeros at infinity.
 int msm_recs_ws(zk_context* ctx, MsmWorkspace* ws, bool g2, const void* d_recs, const void* d_scalars, size_t n,
-                uint64_t* out_affine, hipStream_t st, bool beside = false);
+                uint64_t* out, hipStream_t st, bool beside = false, bool jac_out = false);
 // Window tables of fixed bases (proving-key queries): for W digit windows
 // (the widths of the MSM's window split of 254 bits) row w holds 2^(bits of
 // the windows below w) P_j for every point; an MSM over a table has one
@@ -243,7 +244,8 @@ int msm_g1_sets_ws(zk_context* ctx, MsmWorkspace* ws, int nsets, const void* con
                    bool beside = false, const MsmTab* tab = nullptr, const size_t* rows = nullptr);
 // msm_recs_ws over a window table of `rows` points per window (n <= rows).
 int msm_recs_tab(zk_context* ctx, MsmWorkspace* ws, bool g2, const void* d_table, size_t rows, const MsmTab& tab,
-                 const void* d_scalars, size_t n, uint64_t* out_affine, hipStream_t st, bool beside = false);
+                 const void* d_scalars, size_t n, uint64_t* out, hipStream_t st, bool beside = false,
+                 bool jac_out = false);
 
 // ---- fixed base (pointgen.hip)
 int g1_generator_mul(zk_context* ctx, const void* d_scalars, size_t n, void* d_out, hipStream_t st);
