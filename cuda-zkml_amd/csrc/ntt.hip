@@ -447,9 +447,17 @@ __device__ __forceinline__ void tile_fixed(const TileCtx& tc, const PassGeo& g, 
 // strides cost an address computation per limb.  LR = 0 reads the geometry
 // from g.
 constexpr uint32_t NTT_TILE_FIXED_LOG = 11;
+
+// Occupancy: the fixed-geometry passes target 3 waves per SIMD, the runtime-
+// geometry radix-8 passes 2.  The small transforms' radix-4 passes (KMAX 2)
+// target 4: they then fit in 96 VGPRs without spills, so in a proof the
+// quotient's passes find room on a SIMD beside three MSM accumulation waves
+// (128 VGPRs each) instead of waiting for one to end (at 3 waves they took
+// 132 VGPRs; config 1 proof 0.543-0.548 -> 0.528-0.536 ms, standalone
+// transforms of 2^12-2^18 points unchanged).
 template <int KMAX, bool LAST, int LR = 0>
-__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(LR > 0 || KMAX != 3 ? 3 : 2)))
-void k_ntt_pass(PassGeo g, PassIO io) {
+__global__ __launch_bounds__(256)
+__attribute__((amdgpu_waves_per_eu(LR > 0 ? 3 : KMAX != 3 ? 4 : 2))) void k_ntt_pass(PassGeo g, PassIO io) {
   quotient_priority();
   extern __shared__ uint32_t smem[];
   constexpr int EPT = 1 << KMAX;
