@@ -36,6 +36,7 @@
 #include <algorithm>
 #include <numeric>
 #include <thread>
+#include <type_traits>
 #include <vector>
 
 #include "curve.hpp"
@@ -915,7 +916,9 @@ struct OneLane {
 
 template <class LN>
 constexpr int acc_waves() {
-  return sizeof(typename LN::R) == sizeof(fq) ? 4 : sizeof(typename LN::R) == sizeof(fq2) ? 2 : ZK_MSM_G2_ACC_WAVES;
+  if constexpr (std::is_same_v<typename LN::R, fq>) return 4;  // G1
+  else if constexpr (std::is_same_v<typename LN::R, fq2>) return 2;  // G2 on one lane
+  else return ZK_MSM_G2_ACC_WAVES;  // G2 on lane pairs
 }
 
 // Chunk ch covers sorted positions [ch*L0, ch*L0 + L0) of window
