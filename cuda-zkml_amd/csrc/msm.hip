@@ -920,6 +920,10 @@ constexpr int acc_waves() {
   else if constexpr (std::is_same_v<typename LN::R, fq2>) return 2;  // G2 on one lane
   else return ZK_MSM_G2_ACC_WAVES;  // G2 on lane pairs
 }
+// a pair's coordinate type has G1's size: the target must follow the layout
+static_assert(acc_waves<Lanes<fq>>() == 4 && acc_waves<Lanes<fq2>>() == ZK_MSM_G2_ACC_WAVES &&
+                  acc_waves<OneLane<fq2>>() == 2,
+              "accumulation wave targets by lane layout");
 
 // Chunk ch covers sorted positions [ch*L0, ch*L0 + L0) of window
 // ch / chunks_per_window; positions past the window's entry count are empty.

@@ -91,7 +91,10 @@ def test_setup_and_prove_match_oracle_and_verify(ctx, tmp_path, kind):
     rc, proof_o, _ = oc.prove(pk_o, circ.witness_words(), PROVE_SEED, threads=8)
     assert rc == 0
     assert proof == proof_o
-    assert t["total"] > 0
+    # phase timings: the total by the host clock, the GPU phases by events
+    # inside it (a small allowance for the two clocks)
+    assert t["total"] > 0 and all(v >= 0 for v in t.values())
+    assert max(t[k] for k in ("quotient", "A", "B_g2", "L", "H", "B_g1")) <= t["total"] + 0.05
     pf = tmp_path / "proof.bin"
     pf.write_bytes(proof)
     pub = tmp_path / "pub.bin"
