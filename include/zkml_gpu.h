@@ -216,9 +216,10 @@ int zk_quotient_h(zk_context* ctx, const zk_r1cs* r1cs, const void* d_witness, s
  * (Groth16Proof::serialize, groth16.cu:1058-1074).  check_witness mirrors the
  * ZKML_SKIP_WITNESS_CHECK switch (groth16.cu:687-695).  The five MSMs run
  * concurrently on streams of the context (one host thread each).
- * timings_ms (optional, 8 doubles): total, witness upload + quotient, then
- * each MSM's own duration (they overlap): A, B(G2), L, H, B1, and the host
- * assembly after the last MSM. */
+ * timings_ms (optional, 8 doubles): total (host clock, from the witness
+ * upload to the serialized proof), witness upload + quotient, then each
+ * MSM's own duration (GPU events; they overlap): A, B(G2), L, H, B1, and the
+ * host assembly after the last MSM. */
 int zk_pk_load(zk_context* ctx, const char* path, zk_pk** out);
 void zk_pk_destroy(zk_pk* pk);
 int zk_pk_info(const zk_pk* pk, int* num_constraints, int* num_variables, int* num_public);
