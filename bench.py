@@ -148,6 +148,9 @@ def main():
                     help="only the 2^20 G1 MSM steps (the run the rocprofv3 counter summaries profile)")
     ap.add_argument("--ntt-only", action="store_true",
                     help="only the forward NTT of 2^22 elements (config 2; the run the NTT counter summaries profile)")
+    ap.add_argument("--prove-only", action="store_true",
+                    help="only the config 4 (2^16) proves, --steps of them after 3 warm-up proves (the run the "
+                         "proof timeline summary traces)")
     ap.add_argument("--copy-calibration", type=int, default=0, metavar="MIB",
                     help="only run a plain device copy of MIB MiB (torch's copy kernel), the reference for "
                          "scaling rocprofv3 FETCH_SIZE / WRITE_SIZE readings to bytes")
@@ -187,6 +190,25 @@ def main():
     if args.ntt_only:
         ntt, _, _ = ntt_case(ctx, 22, rng)
         print(json.dumps({"ntt_2_22": ntt}), flush=True)
+        return
+    if args.prove_only:
+        from statements import load as load_statement
+        nc, nv, npub, _, A, B, C, w = load_statement("config4")
+        r = ctx.r1cs(nc, nv, npub, A, B, C)
+        with tempfile.TemporaryDirectory() as td:
+            ctx.setup(r, 0xDEADBEEF42, os.path.join(td, "pk.bin"), os.path.join(td, "vk.bin"))
+            pk = ctx.load_pk(os.path.join(td, "pk.bin"))
+            for _ in range(3):
+                ctx.prove(pk, r, w, npub, 0xCAFEBABE)
+            times = []
+            for _ in range(args.steps):
+                t0 = time.perf_counter()
+                ctx.prove(pk, r, w, npub, 0xCAFEBABE)
+                times.append((time.perf_counter() - t0) * 1e3)
+            pk.close()
+        r.close()
+        print(json.dumps({"prove_2_16_config4": {"ms": round(float(np.median(times)), 3),
+                                                 "min_ms": round(min(times), 3), "proves": args.steps}}), flush=True)
         return
     n = 1 << args.log_n
 

@@ -277,21 +277,21 @@ __global__ void k_msm_digits(uint32_t* __restrict__ dig, const uint4* __restrict
 // `slice` points; block (s, w) owns one.
 
 // Per-(window, slice) histogram -> H[(w*S + s)*B + b].
-template <int BMAX>
-__global__ __launch_bounds__(SORT_T) void k_msm_hist(const uint32_t* __restrict__ dig, size_t n, uint32_t slice,
+template <int BMAX, int TB = SORT_T>
+__global__ __launch_bounds__(TB) void k_msm_hist(const uint32_t* __restrict__ dig, size_t n, uint32_t slice,
                                                      uint32_t S, uint32_t B, uint32_t* __restrict__ H) {
   msm_short_priority();
   __shared__ uint32_t h[BMAX];
   const uint32_t s = blockIdx.x, w = blockIdx.y, t = threadIdx.x;
-  for (uint32_t i = t; i < B; i += SORT_T) h[i] = 0;
+  for (uint32_t i = t; i < B; i += TB) h[i] = 0;
   __syncthreads();
   const size_t lo = (size_t)s * slice, hi = min(n, lo + slice);
   const uint32_t* d = dig + (size_t)w * n;
-  for (size_t p0 = lo + t; p0 < hi; p0 += (size_t)SORT_T * SORT_U) {
+  for (size_t p0 = lo + t; p0 < hi; p0 += (size_t)TB * SORT_U) {
     uint32_t v[SORT_U];
 #pragma unroll
     for (int u = 0; u < SORT_U; u++) {
-      const size_t p = p0 + (size_t)u * SORT_T;
+      const size_t p = p0 + (size_t)u * TB;
       v[u] = p < hi ? d[p] : 0u;
     }
 #pragma unroll
@@ -302,7 +302,7 @@ __global__ __launch_bounds__(SORT_T) void k_msm_hist(const uint32_t* __restrict_
   }
   __syncthreads();
   uint32_t* out = H + ((size_t)w * S + s) * B;
-  for (uint32_t i = t; i < B; i += SORT_T) out[i] = h[i];
+  for (uint32_t i = t; i < B; i += TB) out[i] = h[i];
 }
 
 // Column scan over slices, one thread per bucket k = w*B + b, blocks of
@@ -391,8 +391,8 @@ __global__ __launch_bounds__(256) void k_msm_bscan(const uint32_t* __restrict__ 
 // Scatter: LDS cursors = bucket start + slice prefix, one LDS atomic per
 // entry; out[pos] = (key, point | sign<<31).  Bucket start = w*n_pad +
 // boff[k / SCAN_T] + lex[k]; the blocks of slice 0 also store start/end.
-template <int BMAX>
-__global__ __launch_bounds__(SORT_T) void k_msm_scatter(const uint32_t* __restrict__ dig, size_t n, uint32_t slice,
+template <int BMAX, int TB = SORT_T>
+__global__ __launch_bounds__(TB) void k_msm_scatter(const uint32_t* __restrict__ dig, size_t n, uint32_t slice,
                                                         uint32_t S, uint32_t B, uint32_t n_pad,
                                                         const uint32_t* __restrict__ H,
                                                         const uint32_t* __restrict__ boff,
@@ -404,7 +404,7 @@ __global__ __launch_bounds__(SORT_T) void k_msm_scatter(const uint32_t* __restri
   __shared__ uint32_t cur[BMAX];
   const uint32_t s = blockIdx.x, w = blockIdx.y, t = threadIdx.x;
   const uint32_t* hp = H + ((size_t)w * S + s) * B;
-  for (uint32_t i = t; i < B; i += SORT_T) {
+  for (uint32_t i = t; i < B; i += TB) {
     const uint32_t k = w * B + i;
     const uint32_t st = w * n_pad + boff[k / SCAN_T] + lex[k];
     cur[i] = st + hp[i];
@@ -417,11 +417,11 @@ __global__ __launch_bounds__(SORT_T) void k_msm_scatter(const uint32_t* __restri
   const size_t lo = (size_t)s * slice, hi = min(n, lo + slice);
   const uint32_t* d = dig + (size_t)w * n;
   const uint32_t kb = w * B - 1;
-  for (size_t p0 = lo + t; p0 < hi; p0 += (size_t)SORT_T * SORT_U) {
+  for (size_t p0 = lo + t; p0 < hi; p0 += (size_t)TB * SORT_U) {
     uint32_t v[SORT_U];
 #pragma unroll
     for (int u = 0; u < SORT_U; u++) {
-      const size_t p = p0 + (size_t)u * SORT_T;
+      const size_t p = p0 + (size_t)u * TB;
       v[u] = p < hi ? d[p] : 0u;
     }
 #pragma unroll
@@ -429,7 +429,7 @@ __global__ __launch_bounds__(SORT_T) void k_msm_scatter(const uint32_t* __restri
       const uint32_t m = v[u] & 0x7fffffffu;
       if (m) {
         const uint32_t pos = atomicAdd(&cur[m - 1], 1u);
-        out[pos] = make_uint2(kb + m, (uint32_t)(p0 + (size_t)u * SORT_T) | (v[u] & 0x80000000u));
+        out[pos] = make_uint2(kb + m, (uint32_t)(p0 + (size_t)u * TB) | (v[u] & 0x80000000u));
       }
     }
   }
@@ -1549,7 +1549,7 @@ struct MsmShape {
 // copy (the scatter is still running then).
 static int msm_sort_wide(zk_context* ctx, MsmWorkspace& ws, const MsmShape& sh, hipStream_t st);
 
-static int msm_sort(zk_context* ctx, MsmWorkspace& ws, const MsmShape& sh, hipStream_t st) {
+static int msm_sort(zk_context* ctx, MsmWorkspace& ws, const MsmShape& sh, bool small_blocks, hipStream_t st) {
   if (sh.B > MSM_LDS_B) return msm_sort_wide(ctx, ws, sh, st);
   const size_t n = sh.n;
   const int W = sh.W;
@@ -1566,7 +1566,18 @@ static int msm_sort(zk_context* ctx, MsmWorkspace& ws, const MsmShape& sh, hipSt
   uint32_t* end = (uint32_t*)ws.end.p;
   uint32_t* wstat = (uint32_t*)ws.wstat.p;
   uint2* sorted = (uint2*)ws.sorted.p;
-  if (B <= 4096) {
+  // small_blocks: the sort runs while other jobs' accumulations hold the CUs
+  // (a proof's H); its small-bucket kernels then take blocks of 256 threads,
+  // since a CU holding accumulation waves rarely has room for a 1024-thread
+  // block, which waits for one to end (a 2^16 proof's H histogram took 210
+  // us instead of 7 in a trace).  Config 4's proof 1.217-1.250 -> 1.213-1.236
+  // ms over six runs on one box; for the B2 job, which sorts before the
+  // accumulations, small blocks lost (1.23 -> 1.25 ms).
+  constexpr int SMALL_T = 256;
+  if (B <= 4096 && small_blocks) {
+    ZK_LAUNCH(ctx, st, "msm_hist", (k_msm_hist<4096, SMALL_T>), dim3(S, W), dim3(SMALL_T), 0, dig, n, slice, S, B,
+              hist);
+  } else if (B <= 4096) {
     ZK_LAUNCH(ctx, st, "msm_hist", k_msm_hist<4096>, dim3(S, W), dim3(SORT_T), 0, dig, n, slice, S, B, hist);
   } else {
     ZK_LAUNCH(ctx, st, "msm_hist", k_msm_hist<32768>, dim3(S, W), dim3(SORT_T), 0, dig, n, slice, S, B, hist);
@@ -1576,7 +1587,10 @@ static int msm_sort(zk_context* ctx, MsmWorkspace& ws, const MsmShape& sh, hipSt
   ZK_LAUNCH(ctx, st, "msm_scan", k_msm_bscan, dim3(W), dim3(256), 0, bsum, bmax, nb, boff, wstat);
   ZK_HIP(ctx, hipMemcpyAsync(ws.h_stat, wstat, (size_t)W * 8, hipMemcpyDeviceToHost, st));
   ZK_HIP(ctx, hipEventRecord(ws.stat_ready, st));
-  if (B <= 4096) {
+  if (B <= 4096 && small_blocks) {
+    ZK_LAUNCH(ctx, st, "msm_scatter", (k_msm_scatter<4096, SMALL_T>), dim3(S, W), dim3(SMALL_T), 0, dig, n, slice, S,
+              B, n_pad, hist, boff, lex, tot, start, end, sorted);
+  } else if (B <= 4096) {
     ZK_LAUNCH(ctx, st, "msm_scatter", k_msm_scatter<4096>, dim3(S, W), dim3(SORT_T), 0, dig, n, slice, S, B, n_pad,
               hist, boff, lex, tot, start, end, sorted);
   } else {
@@ -1957,7 +1971,9 @@ static int msm_run_sets(zk_context* ctx, MsmWorkspace& ws, const BaseSets& sets_
 
   ZK_LAUNCH(ctx, st, "msm_digits", k_msm_digits, dim3(cdiv(n, 256)), dim3(256), 0, (uint32_t*)ws.dig.p,
             (const uint4*)d_scalars, n, Wd);
-  ZK_TRY(msm_sort(ctx, ws, sh, st));
+  // a single-set G1 table MSM beside other jobs is a proof's H, sorted after
+  // the quotient while the other jobs accumulate
+  ZK_TRY(msm_sort(ctx, ws, sh, beside && nsets == 1 && tab != nullptr && sizeof(F) == sizeof(fq), st));
   // the windows' entry counts and largest buckets come back while the
   // scatter runs
   ZK_HIP(ctx, hipEventSynchronize(ws.stat_ready));
